@@ -1,0 +1,164 @@
+/*
+ * t2i_hip.h -- C ABI of the MI355X (gfx950) W4A16 hot path.
+ *
+ * Every pointer is a device pointer unless stated otherwise; `stream` is a
+ * hipStream_t (NULL = the legacy default stream).  All calls are
+ * stream-ordered and asynchronous; nothing here allocates device memory.
+ *
+ * Return codes: 0 ok; > 0 a hipError_t from the launch; < 0 an argument
+ * error (see T2I_ERR_*), detected on the host before anything is launched.
+ * t2i_last_error() gives a thread-local message for the last failure.
+ *
+ * Weight format: AutoGPTQ group-wise int4, unchanged from the checkpoint:
+ *   qweight int32 [K/8, N]   nibble j of word (r, n) = q[8r + j][n]
+ *   qzeros  int32 [K/g, N/8] nibble j of word (t, c) = stored zero of column 8c + j;
+ *                            effective zero = stored + 1
+ *   scales  fp16  [K/g, N]
+ * W[n][k] = (q[k][n] - z[k/g][n]) * s[k/g][n].  Group size g = 128.
+ * Activations are bf16 (uint16_t bit patterns), row-major, 16-byte aligned.
+ *
+ * Workspace: entry points that reduce across workgroups take a caller-owned
+ * workspace sized by the matching *_workspace_bytes() query.  It must be
+ * zero-filled once before its first use; the kernels leave their counters at
+ * zero again when they finish.  Calls that overlap in time (different
+ * streams) must not share a workspace.
+ */
+#ifndef T2I_HIP_H
+#define T2I_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define T2I_ABI_VERSION 1
+
+#define T2I_OK 0
+#define T2I_ERR_NULL (-1)      /* a required pointer is NULL */
+#define T2I_ERR_SHAPE (-2)     /* a size is not supported (K % 128, N % 64, M range, ...) */
+#define T2I_ERR_ALIGN (-3)     /* a pointer is not 16-byte aligned */
+#define T2I_ERR_GROUP (-4)     /* group size other than 128 */
+#define T2I_ERR_WORKSPACE (-5) /* workspace missing or too small */
+#define T2I_ERR_VALUE (-6)     /* a scalar argument is out of range */
+
+int t2i_abi_version(void);
+const char* t2i_strerror(int code);
+const char* t2i_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * Dequantisation hook (bit-exact check of the unpack and zero convention).
+ * W_nk fp32 [N, K] = (q - z) * s, exact in fp32.
+ * Replaces: fast_qwen3/fast_packed_format.py:132-161 (_autogptq_linear_to_dense)
+ *           and quantized_qwen3/packed_format.py:88-106 (nibble unpack, zero + 1).
+ */
+int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,
+                          const uint16_t* scales, int32_t K, int32_t N,
+                          int32_t group_size, float* W_nk, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * W4A16 linear: y[M, N] = x[M, K] . W^T, fp32 accumulation, bf16 output.
+ * 1 <= M <= 64; K % 128 == 0; N % 64 == 0.  M = 1 is the GEMV case.
+ * residual (nullable, may alias y): y = bf16(bf16(x.W^T) + residual).
+ * Replaces: quantized_qwen3/operators/w4a16_gemv/op.py:22-126 (W4A16GEMV, M = 1)
+ *           quantized_qwen3/operators/w4a16_gemm/op.py:23-174, 267-333
+ *           (W4A16GEMM / W4A16KGroupGEMM, M = 4..32 on the NPU)
+ *           and the CPU oracle quantized_qwen3/model.py:133-146.
+ * Residual form replaces fast_qwen3/operators/q4nx_fused_linear_residual_projection/op.py:31-118.
+ */
+size_t t2i_w4a16_linear_workspace_bytes(int32_t M, int32_t K, int32_t N);
+int t2i_w4a16_linear(const uint16_t* x, int32_t M,
+                     const int32_t* qweight, const int32_t* qzeros,
+                     const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                     const uint16_t* residual, uint16_t* y,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Paired gate/up linear over one weight whose columns interleave gate and up
+ * in blocks of two (fused column 4i+e = gate 2i+e, 4i+2+e = up 2i+e, e in {0,1};
+ * N = 2*I).  swiglu != 0: h[M, I] = bf16(bf16(silu(bf16 gate)) * bf16 up) into y0,
+ * y1 unused.  swiglu == 0: y0 = gate [M, I], y1 = up [M, I].
+ * Replaces: quantized_qwen3/operators/w4a16_gemm/op.py:178-263 (W4A16PairedKGroupGEMM,
+ *           gate = pair 0, up = pair 1) + torch2iron/operators/silu_mul (SiLUMul).
+ */
+size_t t2i_w4a16_gate_up_workspace_bytes(int32_t M, int32_t K, int32_t N);
+int t2i_w4a16_gate_up(const uint16_t* x, int32_t M,
+                      const int32_t* qweight, const int32_t* qzeros,
+                      const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                      int32_t swiglu, uint16_t* y0, uint16_t* y1,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Weighted RMSNorm over rows of H: y = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * w).
+ * tokens != NULL: x rows are gathered from the bf16 table `x` ([V, H]) by token id
+ * and the gathered rows are also written to x_out (the residual stream); an id
+ * outside [0, V) gathers a zero row.  V is ignored when tokens == NULL.
+ * argmax_keys != NULL: its M uint64 entries are zeroed (the lm_head argmax reduction
+ * starts from zero).
+ * Replaces: torch2iron/operators/rms_norm (RMSNorm, weighted), quantized_qwen3/model.py:172-181,
+ *           and the host embedding of quantized_qwen3/qwen_npu.py:182-185.
+ */
+int t2i_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
+                const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y,
+                uint64_t* argmax_keys, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GQA decode attention with the current token folded in.
+ * qkv bf16 [B, (Hq + 2*Hkv)*D] is the raw fused q|k|v projection of the current token.
+ * Per sequence b (position p = positions[b]):
+ *   q, k <- per-head RMSNorm (q_norm / k_norm weights, eps) then RoPE from the bf16
+ *           cos/sin table rope[p] ([ctx_cap, D], cos at even, sin at odd columns);
+ *           rope_style 0 = halves (i, i+D/2), 1 = interleaved (2i, 2i+1);
+ *   k_cache[b][h][p] <- k, v_cache[b][h][p] <- v;
+ *   ctx[b][hq*D:] = softmax(q . K[0..p]^T / sqrt(D)) . V[0..p]   (fp32 softmax, bf16 out).
+ * A position outside [0, ctx_cap) writes no cache slot and yields a zero context row.
+ * Caches are bf16 [B, Hkv, ctx_cap, D].  D = 128; Hq % Hkv == 0; Hq/Hkv <= 8.
+ * Replaces: torch2iron/operators/rms_norm_rope (RMSNormRoPE), copy_present_packet_kv
+ *           (CopyPresentPacketKV) and llama_chunked_attention (LlamaChunkedAttention),
+ *           as wired per layer in quantized_qwen3/batch_decode_fused.py:426-463.
+ */
+size_t t2i_decode_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t ctx_cap);
+int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t B,
+                         int32_t Hq, int32_t Hkv, int32_t D,
+                         const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                         const uint16_t* rope, int32_t rope_style,
+                         uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
+                         uint16_t* ctx, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Tied bf16 lm_head with a fused greedy argmax.
+ * logits[m][v] = sum_k h[m][k] * E[v][k] in fp32 (E bf16 [V, K], K % 64 == 0, V % 16 == 0).
+ * argmax_keys (uint64 [M], zeroed beforehand, e.g. by t2i_rmsnorm) receives
+ * ordered(max logit) << 32 | (0xFFFFFFFF - index): the first index of the maximum
+ * wins ties, as torch.argmax.  logits (nullable) receives fp32 logits [M, V].
+ * Replaces: quantized_qwen3/operators/w4a16_gemm/op.py:337-399 (W4A16NShardGEMM lm_head)
+ *           and the host argmax of quantized_qwen3/qwen_npu.py:321.
+ */
+int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V,
+                       int32_t K, float* logits, uint64_t* argmax_keys, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Greedy bookkeeping between decode steps, on the device:
+ * tokens[b] = index decoded from argmax_keys[b]; history[b*hist_cap + step[0]] = tokens[b];
+ * positions[b] += 1; step[0] += 1 (by one thread after all rows).  Lets a captured
+ * decode step be replayed without host work.
+ * Replaces: the host loop of quantized_qwen3/qwen_npu.py:318-325.
+ */
+int t2i_greedy_advance(const uint64_t* argmax_keys, int32_t B, int32_t* tokens,
+                       int32_t* positions, int32_t* history, int32_t hist_cap,
+                       int32_t* step, void* stream);
+
+/* Teacher-forced prompt step: positions[b] += 1; tokens[b] = prompt[b*P + positions[b]]
+ * while positions[b] < P.  prompt is int32 [B, P].
+ * Replaces: the per-sequence prefill loop of quantized_qwen3/qwen_npu.py:309-315
+ *           (prompt consumed one position at a time through the decode path). */
+int t2i_prompt_advance(const int32_t* prompt, int32_t B, int32_t P, int32_t* tokens,
+                       int32_t* positions, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* T2I_HIP_H */

@@ -1,0 +1,96 @@
+"""The C ABI library: it loads, exports every declared entry point, and rejects
+bad arguments on the host before launching anything (CPU only, no GPU calls)."""
+
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT
+from torch2iron_amd import _lib
+from torch2iron_amd import ops
+from torch2iron_amd.formats import W4A16Weight, random_tensors
+
+HEADER = ROOT / "include" / "t2i_hip.h"
+FAKE = 0x10000          # an aligned, never-dereferenced address
+MISALIGNED = 0x10002
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^[a-z_ ]+?[\s\*](t2i_\w+)\(", text, flags=re.M)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert len(names) >= 12
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.t2i_abi_version() == 1
+    assert lib.t2i_strerror(-2) == b"unsupported shape"
+
+
+@pytest.mark.parametrize("M,K,N,group,x,code", [
+    (0, 1024, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
+    (65, 1024, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
+    (1, 1000, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
+    (1, 1024, 3000, 128, FAKE, _lib.T2I_ERR_SHAPE),
+    (1, 1024, 3072, 64, FAKE, _lib.T2I_ERR_GROUP),
+    (1, 1024, 3072, 128, MISALIGNED, _lib.T2I_ERR_ALIGN),
+    (1, 1024, 3072, 128, 0, _lib.T2I_ERR_NULL),
+])
+def test_linear_argument_errors(M, K, N, group, x, code):
+    lib = _lib.load()
+    rc = lib.t2i_w4a16_linear(x, M, FAKE, FAKE, FAKE, K, N, group, None, FAKE, None, 0, None)
+    assert rc == code
+    assert lib.t2i_last_error()
+
+
+def test_linear_requires_workspace_when_split():
+    lib = _lib.load()
+    need = lib.t2i_w4a16_linear_workspace_bytes(1, 2048, 1024)
+    assert need > 0, "a 1024-column linear splits K across workgroups"
+    rc = lib.t2i_w4a16_linear(FAKE, 1, FAKE, FAKE, FAKE, 2048, 1024, 128, None, FAKE, None, 0, None)
+    assert rc == _lib.T2I_ERR_WORKSPACE
+    rc = lib.t2i_w4a16_linear(FAKE, 1, FAKE, FAKE, FAKE, 2048, 1024, 128, None, FAKE, FAKE, need - 1, None)
+    assert rc == _lib.T2I_ERR_WORKSPACE
+
+
+def test_other_entry_points_validate():
+    lib = _lib.load()
+    assert lib.t2i_rmsnorm(FAKE, None, 0, 4, 1020, FAKE, 1e-6, None, FAKE, None, None) == _lib.T2I_ERR_SHAPE
+    assert lib.t2i_rmsnorm(FAKE, None, 0, 4, 1024, FAKE, 0.0, None, FAKE, None, None) == _lib.T2I_ERR_VALUE
+    assert lib.t2i_rmsnorm(FAKE, FAKE, 10, 4, 1024, FAKE, 1e-6, None, FAKE, None, None) == _lib.T2I_ERR_NULL
+    assert lib.t2i_rmsnorm(FAKE, FAKE, 0, 4, 1024, FAKE, 1e-6, FAKE, FAKE, None, None) == _lib.T2I_ERR_SHAPE
+    args = [FAKE, FAKE, 8, 16, 8, 64, FAKE, FAKE, 1e-6, FAKE, 0, FAKE, FAKE, 1088, FAKE, None, 0, None]
+    assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_SHAPE            # head_dim 64
+    args[5] = 128
+    args[3] = 12                                                             # 12 q heads over 8 kv heads
+    assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_SHAPE
+    args[3] = 16
+    assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_WORKSPACE        # split context needs workspace
+    assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151930, 1024, None, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151936, 1024, None, None, None) == _lib.T2I_ERR_NULL
+    assert lib.t2i_w4a16_dequant_f32(FAKE, FAKE, FAKE, 1024, 3072, 128, None, None) == _lib.T2I_ERR_NULL
+    assert lib.t2i_w4a16_gate_up(FAKE, 4, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None, 0, None) \
+        == _lib.T2I_ERR_NULL
+
+
+def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
+    w = W4A16Weight.from_numpy(*random_tensors(256, 64, seed=1))
+    x = torch.zeros(1, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.linear(x, w)
+    with pytest.raises(ValueError):
+        W4A16Weight(w.qweight, w.qzeros, w.scales[:1])
+
+
+def test_workspace_sizes_are_consistent():
+    lib = _lib.load()
+    for (m, k, n) in [(1, 1024, 3072), (16, 1024, 4096), (64, 2048, 1024), (64, 6144, 2048), (8, 3072, 1024)]:
+        b = lib.t2i_w4a16_linear_workspace_bytes(m, k, n)
+        assert b == 0 or b >= m * n * 4 * 2
+    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) > 0
+    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0

@@ -1,0 +1,123 @@
+"""W4A16 linear on the MI355X vs the CPU oracle (same seeded inputs).
+
+Bars: the dequantised weights are bit-exact; the linear output is within the
+max relative error 1e-2 of the fp64 oracle (max|y - ref| / max|ref|), and
+elementwise within one bf16 rounding (2^-8 relative) plus a 1e-4 * max|ref|
+accumulation allowance.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4a16 as ow
+from torch2iron_amd import ops
+from torch2iron_amd.formats import W4A16Weight, interleave_gate_up
+
+pytestmark = pytest.mark.gpu
+
+QWEN3_06B = [(1024, 4096), (2048, 1024), (1024, 6144), (3072, 1024)]
+QWEN3_17B = [(2048, 4096), (2048, 2048), (2048, 12288), (6144, 2048)]
+
+CASES = [(1, 1024, 3072)]
+CASES += [(m, k, n) for (k, n) in QWEN3_06B for m in (1, 8, 16, 32, 64)]
+CASES += [(m, k, n) for (k, n) in QWEN3_17B for m in (1, 16, 64)]
+CASES += [(3, 1024, 3072), (17, 2048, 1024), (50, 1024, 4096), (33, 3072, 1024), (5, 128, 64)]
+
+
+def _inputs(m, k, n, seed):
+    qw, qz, sc = ow.synthetic_tensors(k, n, seed=seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    return qw, qz, sc, x
+
+
+def check_linear(y: torch.Tensor, ref: np.ndarray):
+    yf = y.float().cpu().numpy().astype(np.float64)
+    scale = np.abs(ref).max()
+    err = np.abs(yf - ref)
+    assert err.max() / scale <= 1e-2, f"max relative error {err.max() / scale:.3e}"
+    bound = 2.0 ** -8 * np.abs(ref) * 1.01 + 1e-4 * scale
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} elements beyond one bf16 rounding; worst {err.max():.4e}"
+
+
+@pytest.mark.parametrize("m,k,n", CASES, ids=[f"M{m}-K{k}-N{n}" for m, k, n in CASES])
+def test_linear_matches_oracle(gpu, m, k, n):
+    qw, qz, sc, x = _inputs(m, k, n, seed=1000 + m + k + n)
+    ref = ow.linear(x.float().numpy(), qw, qz, sc, accumulate="fp64")
+    w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
+    y = ops.linear(x.to(gpu), w)
+    check_linear(y, ref)
+    # a second call reuses the workspace (counters must have been reset)
+    y2 = ops.linear(x.to(gpu), w)
+    assert torch.equal(y, y2), "repeat call differs: split-K reduction is not deterministic"
+
+
+def test_gemv_vector_input(gpu):
+    qw, qz, sc, x = _inputs(1, 1024, 3072, seed=7)
+    ref = ow.linear(x.float().numpy(), qw, qz, sc)
+    y = ops.linear(x[0].to(gpu), W4A16Weight.from_numpy(qw, qz, sc, device=gpu))
+    assert y.shape == (3072,)
+    check_linear(y.view(1, -1), ref)
+
+
+@pytest.mark.parametrize("m,k,n", [(16, 2048, 1024), (64, 1024, 4096), (1, 3072, 1024)])
+def test_linear_residual(gpu, m, k, n):
+    qw, qz, sc, x = _inputs(m, k, n, seed=31 + m)
+    res = torch.randn(m, n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    lin = ow.linear(x.float().numpy(), qw, qz, sc)
+    ref = lin + res.float().numpy()
+    out = res.clone().to(gpu)
+    y = ops.linear(x.to(gpu), W4A16Weight.from_numpy(qw, qz, sc, device=gpu), residual=out, out=out)  # in place
+    check_linear_residual = np.abs(y.float().cpu().numpy() - ref)
+    # two bf16 roundings (the projection, then the sum)
+    bound = 2.0 ** -8 * (np.abs(lin) + np.abs(ref)) * 1.01 + 1e-4 * np.abs(ref).max()
+    assert (check_linear_residual <= bound).all()
+
+
+@pytest.mark.parametrize("k,n", [(1024, 3072), (2048, 1024), (3072, 1024), (128, 64), (6144, 2048)])
+def test_dequant_bit_exact(gpu, k, n):
+    qw, qz, sc = ow.synthetic_tensors(k, n, seed=k + n)
+    ref = ow.dequantize(qw, qz, sc)
+    w = ops.dequantize(W4A16Weight.from_numpy(qw, qz, sc, device=gpu)).cpu().numpy()
+    assert np.array_equal(w.view(np.uint32), ref.view(np.uint32))
+
+
+def test_dequant_special_words(gpu):
+    """All-zero, all-one and counting words, every zero nibble value."""
+    k, n = 128, 64
+    qw = np.zeros((k // 8, n), dtype=np.uint32)
+    qw[0::3] = 0x76543210
+    qw[1::3] = 0xFFFFFFFF
+    qw[2::3] = 0xFEDCBA98
+    qz = np.tile(np.array([0x76543210, 0xFEDCBA98], dtype=np.uint32), (1, n // 16)).reshape(1, n // 8)
+    sc = np.linspace(0.005, 0.02, n, dtype=np.float16).reshape(1, n)
+    qw, qz = qw.view(np.int32), qz.view(np.int32)
+    ref = ow.dequantize(qw, qz, sc)
+    w = ops.dequantize(W4A16Weight.from_numpy(qw, qz, sc, device=gpu)).cpu().numpy()
+    assert np.array_equal(w.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,inter", [(1, 1024, 3072), (16, 1024, 3072), (64, 1024, 3072), (8, 2048, 6144)])
+def test_gate_up_paired_and_swiglu(gpu, m, k, inter):
+    gate = ow.synthetic_tensors(k, inter, seed=11)
+    up = ow.synthetic_tensors(k, inter, seed=12)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    xf = x.float().numpy()
+    g_ref = ow.linear(xf, *gate)
+    u_ref = ow.linear(xf, *up)
+    w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
+    g, u = ops.gate_up(x.to(gpu), w, swiglu=False)
+    check_linear(g, g_ref)
+    check_linear(u, u_ref)
+    h = ops.gate_up(x.to(gpu), w, swiglu=True).float().cpu().numpy()
+    # h from the GPU's own rounded gate/up must match the reference rounding chain exactly
+    gb = g.float().cpu()
+    ub = u.float().cpu()
+    h_chain = (torch.nn.functional.silu(gb).to(torch.bfloat16).float() * ub).to(torch.bfloat16).float().numpy()
+    assert np.abs(h - h_chain).max() <= 2.0 ** -7 * np.abs(h_chain).max()
+    assert (h == h_chain).mean() > 0.999
+    # and the fp64 truth within tolerance
+    truth = (g_ref / (1 + np.exp(-g_ref))) * u_ref
+    assert np.abs(h - truth).max() / np.abs(truth).max() <= 1e-2

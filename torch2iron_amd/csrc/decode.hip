@@ -1,0 +1,599 @@
+// Decode-layer kernels around the W4A16 linears, for gfx950:
+//   * weighted RMSNorm (optionally gathering rows from the embedding table);
+//   * GQA decode attention with q/k RMSNorm, RoPE and the KV-cache write of the
+//     current token folded into its prologue (split over the context, combined
+//     by the last workgroup to finish);
+//   * the tied bf16 lm_head on MFMA with a fused greedy argmax;
+//   * device-side greedy / prompt bookkeeping so a decode step can be replayed
+//     from a captured graph without host work.
+//
+// Elementwise rounding follows the reference runtime in bf16 compute
+// (quantized_qwen3/model.py:172-196, 215-216, 322-327): every product and sum
+// that the reference rounds to bf16 is rounded here at the same point.
+#include <math.h>
+
+#include "t2i_common.h"
+
+namespace t2i {
+
+// ============================================================================
+// RMSNorm
+// ============================================================================
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_MAX_CHUNKS = 4;   // 16-byte chunks per thread: H <= 8192
+
+__global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const int32_t* __restrict__ tokens, int V, int H,
+    const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ x_out,
+    uint16_t* __restrict__ y, unsigned long long* __restrict__ keys) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  int src_row = row;
+  bool zero_row = false;
+  if (tokens) {
+    src_row = tokens[row];
+    if (src_row < 0 || src_row >= V) { src_row = 0; zero_row = true; }   // out-of-range id: zero row
+  }
+  const uint16_t* src = x + (size_t)src_row * H;
+  const int chunks = H / 8;
+  u32x4 v[NORM_MAX_CHUNKS];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_CHUNKS; ++i) {
+    const int ch = tid + i * NORM_THREADS;
+    if (ch < chunks) {
+      v[i] = zero_row ? u32x4{0u, 0u, 0u, 0u} : *reinterpret_cast<const u32x4*>(src + ch * 8);
+      const uint32_t a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = bf16_lo(a[j]), hi = bf16_hi(a[j]);
+        ss = fmaf(lo, lo, ss);
+        ss = fmaf(hi, hi, ss);
+      }
+    }
+  }
+  __shared__ float part[NORM_THREADS / 64];
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) part[tid >> 6] = ss;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NORM_THREADS / 64; ++i) total += part[i];
+  const float inv = round_bf16(1.0f / sqrtf(total / (float)H + eps));
+#pragma unroll
+  for (int i = 0; i < NORM_MAX_CHUNKS; ++i) {
+    const int ch = tid + i * NORM_THREADS;
+    if (ch < chunks) {
+      const u32x4 g = *reinterpret_cast<const u32x4*>(w + ch * 8);
+      const uint32_t a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+      const uint32_t b[4] = {g.x, g.y, g.z, g.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = round_bf16(round_bf16(bf16_lo(a[j]) * inv) * bf16_lo(b[j]));
+        const float hi = round_bf16(round_bf16(bf16_hi(a[j]) * inv) * bf16_hi(b[j]));
+        o[j] = pack_bf16x2(lo, hi);
+      }
+      *reinterpret_cast<u32x4*>(y + (size_t)row * H + ch * 8) = u32x4{o[0], o[1], o[2], o[3]};
+      if (x_out) *reinterpret_cast<u32x4*>(x_out + (size_t)row * H + ch * 8) = v[i];
+    }
+  }
+  if (keys && tid == 0) keys[row] = 0ull;
+}
+
+// ============================================================================
+// GQA decode attention
+// ============================================================================
+constexpr int ATT_D = 128;
+constexpr int ATT_THREADS = 256;
+constexpr int ATT_MAX_CHUNK = 256;
+constexpr int ATT_TOK_PER_ITER = 16;   // 4 waves x 4 row groups of 16 lanes
+
+struct AttnParams {
+  const uint16_t* qkv;
+  const int32_t* pos;
+  const uint16_t* qn;
+  const uint16_t* kn;
+  const uint16_t* rope;
+  uint16_t* kc;
+  uint16_t* vc;
+  uint16_t* out;
+  float* part_o;        // [B*Hkv][S][Q][D]
+  float* part_ml;       // [B*Hkv][S][Q][2]
+  uint32_t* counters;   // [B*Hkv]
+  int Hq, Hkv, ctx_cap, chunk, splits, style;
+  float eps, scale;
+};
+
+__device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
+  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+}
+
+template <int Q>
+__global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const AttnParams p) {
+  constexpr int D = ATT_D;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hkv;
+  const int h = bh - b * p.Hkv;
+  const int split = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+
+  __shared__ float s_q[Q][D];
+  __shared__ __align__(16) uint16_t s_kv[2][D];   // current k (after norm + RoPE) and v
+  __shared__ float s_p[Q][ATT_MAX_CHUNK];  // scores, then exp(score - max)
+  __shared__ float s_red[4][Q][D];
+  __shared__ float s_stat[Q][2];
+  __shared__ uint32_t s_prev;
+
+  // a position outside the cache attends to nothing and writes nothing (zero output)
+  const int pos_raw = p.pos[b];
+  const bool valid = pos_raw >= 0 && pos_raw < p.ctx_cap;
+  const int pos = valid ? pos_raw : 0;
+  const int L = valid ? pos + 1 : 0;
+  const int t0 = split * p.chunk;
+  const int t1 = min(t0 + p.chunk, L);
+  const size_t qkv_row = (size_t)b * (p.Hq + 2 * p.Hkv) * D;
+  const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.ctx_cap * D;
+
+  if (t0 < t1) {
+    // ---- prologue: q heads h*Q .. h*Q+Q-1, current k and v ----
+    const int i0 = p.style == 0 ? lane : 2 * lane;        // pair (i0, i1) rotates together
+    const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
+    for (int vi = wave; vi < Q + 2; vi += 4) {
+      const uint16_t* src;
+      const uint16_t* gamma = nullptr;
+      if (vi < Q) { src = p.qkv + qkv_row + (size_t)(h * Q + vi) * D; gamma = p.qn; }
+      else if (vi == Q) { src = p.qkv + qkv_row + (size_t)(p.Hq + h) * D; gamma = p.kn; }
+      else { src = p.qkv + qkv_row + (size_t)(p.Hq + p.Hkv + h) * D; }
+      float x0 = bf16_to_f32(src[i0]);
+      float x1 = bf16_to_f32(src[i1]);
+      if (gamma) {
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+        x0 = round_bf16(round_bf16(x0 * inv) * bf16_to_f32(gamma[i0]));
+        x1 = round_bf16(round_bf16(x1 * inv) * bf16_to_f32(gamma[i1]));
+        const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
+        const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+        const float y0 = round_bf16(round_bf16(x0 * cs) + round_bf16(-x1 * sn));
+        const float y1 = round_bf16(round_bf16(x1 * cs) + round_bf16(x0 * sn));
+        x0 = y0;
+        x1 = y1;
+      }
+      if (vi < Q) {
+        s_q[vi][i0] = x0;
+        s_q[vi][i1] = x1;
+      } else {
+        const int which = vi - Q;   // 0 = k, 1 = v
+        const uint16_t b0 = (uint16_t)f32_to_bf16(x0), b1 = (uint16_t)f32_to_bf16(x1);
+        s_kv[which][i0] = b0;
+        s_kv[which][i1] = b1;
+        if (pos < t1) {   // this workgroup owns the current slot: persist it
+          uint16_t* dst = (which == 0 ? p.kc : p.vc) + cache_base + (size_t)pos * D;
+          dst[i0] = b0;
+          dst[i1] = b1;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- scores: 16 lanes per token, 8 dims per lane ----
+    const int c = lane & 15;
+    const int rg = lane >> 4;
+    float qf[Q][8];
+#pragma unroll
+    for (int j = 0; j < Q; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[j][e] = s_q[j][8 * c + e];
+    const u32x4* kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0]);
+    const u32x4* vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0]);
+    for (int tb = t0; tb < t1; tb += ATT_TOK_PER_ITER) {
+      const int t = tb + wave * 4 + rg;
+      float kf[8];
+      if (t < t1) {
+        const u32x4 kv = (t == pos) ? kcur[c]
+                                    : *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)t * D + 8 * c);
+        unpack8(kv, kf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] = 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < Q; ++j) {
+        float d = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qf[j][e], kf[e], d);
+        d = row_sum16(d);
+        if (c == 0 && t < t1) s_p[j][t - t0] = d * p.scale;
+      }
+    }
+    __syncthreads();
+
+    // ---- chunk softmax statistics ----
+    const int n = t1 - t0;
+    for (int j = wave; j < Q; j += 4) {
+      float mx = -INFINITY;
+      for (int i = lane; i < n; i += 64) mx = fmaxf(mx, s_p[j][i]);
+      mx = row_max16(mx);
+      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      float sum = 0.0f;
+      for (int i = lane; i < n; i += 64) {
+        const float e = expf(s_p[j][i] - mx);
+        s_p[j][i] = e;
+        sum += e;
+      }
+      sum = wave_sum(sum);
+      if (lane == 0) { s_stat[j][0] = mx; s_stat[j][1] = sum; }
+    }
+    __syncthreads();
+
+    // ---- P . V ----
+    float acc[Q][8];
+#pragma unroll
+    for (int j = 0; j < Q; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+    for (int tb = t0; tb < t1; tb += ATT_TOK_PER_ITER) {
+      const int t = tb + wave * 4 + rg;
+      if (t < t1) {
+        const u32x4 vv = (t == pos) ? vcur[c]
+                                    : *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)t * D + 8 * c);
+        float vf[8];
+        unpack8(vv, vf);
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+          const float pj = s_p[j][t - t0];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < Q; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float a = acc[j][e];
+        a += __shfl_xor(a, 16, 64);
+        a += __shfl_xor(a, 32, 64);
+        acc[j][e] = a;
+      }
+    if (rg == 0) {
+#pragma unroll
+      for (int j = 0; j < Q; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_red[wave][j][8 * c + e] = acc[j][e];
+    }
+    __syncthreads();
+    for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
+      const int j = idx / D, d = idx - (idx / D) * D;
+      const float o = s_red[0][j][d] + s_red[1][j][d] + s_red[2][j][d] + s_red[3][j][d];
+      if (p.splits == 1) {
+        p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] = (uint16_t)f32_to_bf16(o / s_stat[j][1]);
+      } else {
+        p.part_o[(((size_t)bh * p.splits + split) * Q + j) * D + d] = o;
+      }
+    }
+    if (p.splits > 1 && tid < Q) {
+      float* ml = p.part_ml + (((size_t)bh * p.splits + split) * Q + tid) * 2;
+      ml[0] = s_stat[tid][0];
+      ml[1] = s_stat[tid][1];
+    }
+  } else if (p.splits > 1) {
+    if (tid < Q) {
+      float* ml = p.part_ml + (((size_t)bh * p.splits + split) * Q + tid) * 2;
+      ml[0] = -INFINITY;
+      ml[1] = 0.0f;
+    }
+  } else {
+    for (int idx = tid; idx < Q * D; idx += ATT_THREADS)
+      p.out[(size_t)b * p.Hq * D + (size_t)h * Q * D + idx] = 0;
+  }
+  if (p.splits == 1) return;
+
+  // ---- last workgroup of (b, h) combines the splits in split order ----
+  __threadfence();
+  __syncthreads();
+  if (tid == 0)
+    s_prev = __hip_atomic_fetch_add(&p.counters[bh], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  if (s_prev != (uint32_t)(p.splits - 1)) return;
+  __threadfence();
+  for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
+    const int j = idx / D, d = idx - (idx / D) * D;
+    float mx = -INFINITY;
+    for (int s = 0; s < p.splits; ++s) {
+      const float* ml = p.part_ml + (((size_t)bh * p.splits + s) * Q + j) * 2;
+      if (ml[1] > 0.0f) mx = fmaxf(mx, ml[0]);
+    }
+    float lsum = 0.0f, o = 0.0f;
+    for (int s = 0; s < p.splits; ++s) {
+      const float* ml = p.part_ml + (((size_t)bh * p.splits + s) * Q + j) * 2;
+      if (ml[1] > 0.0f) {
+        const float f = expf(ml[0] - mx);
+        lsum = fmaf(ml[1], f, lsum);
+        o = fmaf(p.part_o[(((size_t)bh * p.splits + s) * Q + j) * D + d], f, o);
+      }
+    }
+    p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] =
+        lsum > 0.0f ? (uint16_t)f32_to_bf16(o / lsum) : (uint16_t)0;
+  }
+  if (tid == 0) __hip_atomic_store(&p.counters[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ============================================================================
+// lm_head (bf16 tied embedding) + greedy argmax
+// ============================================================================
+constexpr int LMH_WAVES = 4;
+constexpr int LMH_COLS = 64;      // vocab columns per wave (4 MFMA n-tiles)
+constexpr int LMH_MAX_K = 4096;   // 16 x (K + 8) bf16 of LDS
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
+  const uint32_t u = __float_as_uint(v);
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)ord << 32) | (unsigned long long)(0xFFFFFFFFu - idx);
+}
+
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
+// One workgroup: 4 waves x 64 vocab rows; the activation rows (M <= 16) are
+// staged once in LDS and shared by the waves.
+__global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
+    const uint16_t* __restrict__ hin, int M, const uint16_t* __restrict__ E, int V, int K,
+    float* __restrict__ logits, unsigned long long* __restrict__ keys) {
+  extern __shared__ uint16_t s_h[];                 // [16][K + 8]
+  const int ldh = K + 8;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 15;
+  const int r = lane >> 4;
+  // stage h (rows >= M are zero)
+  for (int idx = tid; idx < 16 * (K / 8); idx += 64 * LMH_WAVES) {
+    const int m = idx / (K / 8), ch = idx - m * (K / 8);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (m < M) v = *reinterpret_cast<const u32x4*>(hin + (size_t)m * K + ch * 8);
+    *reinterpret_cast<u32x4*>(s_h + m * ldh + ch * 8) = v;
+  }
+  __syncthreads();
+
+  const int n0 = (blockIdx.x * LMH_WAVES + wave) * LMH_COLS;
+  f32x4 acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bool tile_ok[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) tile_ok[t] = (n0 + 16 * t) < V;
+
+  for (int k0 = 0; k0 < K; k0 += 64) {
+    u32x4 bv[4][2];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (tile_ok[t]) {
+        const uint16_t* src = E + (size_t)(n0 + 16 * t + c) * K + k0 + 16 * r;
+        bv[t][0] = *reinterpret_cast<const u32x4*>(src);
+        bv[t][1] = *reinterpret_cast<const u32x4*>(src + 8);
+      } else {
+        bv[t][0] = bv[t][1] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    const uint16_t* ha = s_h + c * ldh + k0 + 16 * r;
+    const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ha));
+    const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ha + 8));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bv[t][0]), acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, bv[t][1]), acc[t], 0, 0, 0);
+    }
+  }
+
+  // lane holds logits[m = 4r + i][n = n0 + 16t + c]
+  __shared__ unsigned long long s_best[LMH_WAVES][16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = 4 * r + i;
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (!tile_ok[t]) continue;
+      const int n = n0 + 16 * t + c;
+      if (logits && m < M) logits[(size_t)m * V + n] = acc[t][i];
+      best = umax64(best, argmax_key(acc[t][i], (uint32_t)n));
+    }
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) {
+      const unsigned long long o = __shfl_xor(best, off, 64);
+      best = umax64(best, o);
+    }
+    if (c == 0) s_best[wave][m] = best;
+  }
+  __syncthreads();
+  if (tid < M) {
+    unsigned long long best = s_best[0][tid];
+#pragma unroll
+    for (int w = 1; w < LMH_WAVES; ++w) best = umax64(best, s_best[w][tid]);
+    if (best) atomicMax(&keys[tid], best);
+  }
+}
+
+__global__ void greedy_advance_kernel(const unsigned long long* __restrict__ keys, int B, int32_t* tokens,
+                                      int32_t* positions, int32_t* history, int hist_cap, int32_t* step) {
+  const int s = *step;
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(keys[b] & 0xFFFFFFFFull));
+    tokens[b] = tok;
+    if (history && s < hist_cap) history[(size_t)b * hist_cap + s] = tok;
+    positions[b] += 1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *step = s + 1;
+}
+
+__global__ void prompt_advance_kernel(const int32_t* __restrict__ prompt, int B, int P, int32_t* tokens,
+                                      int32_t* positions) {
+  for (int b = threadIdx.x; b < B; b += blockDim.x) {
+    const int np = positions[b] + 1;
+    positions[b] = np;
+    if (np < P) tokens[b] = prompt[(size_t)b * P + np];
+  }
+}
+
+}  // namespace t2i
+
+// ============================================================================
+// host side
+// ============================================================================
+namespace {
+using namespace t2i;
+using t2i_host::aligned16;
+using t2i_host::fail;
+
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct AttnPlan {
+  int chunk, splits;
+  size_t off_ml, off_o, bytes;
+};
+
+AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
+  AttnPlan pl{};
+  pl.chunk = 128;
+  pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
+  if (pl.splits > 64) {
+    pl.chunk = ATT_MAX_CHUNK;
+    pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
+  }
+  const int Q = Hq / Hkv;
+  const size_t units = (size_t)B * Hkv;
+  if (pl.splits > 1) {
+    pl.off_ml = align256(units * 4);
+    pl.off_o = pl.off_ml + align256(units * pl.splits * Q * 2 * 4);
+    pl.bytes = pl.off_o + units * pl.splits * Q * ATT_D * 4;
+  }
+  return pl;
+}
+
+}  // namespace
+
+extern "C" int t2i_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
+                           const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y,
+                           uint64_t* argmax_keys, void* stream) {
+  if (!x || !weight || !y) return fail(T2I_ERR_NULL, "x, weight and y must not be NULL");
+  if (tokens && !x_out) return fail(T2I_ERR_NULL, "x_out is required with tokens");
+  if (tokens && V < 1) return fail(T2I_ERR_SHAPE, "V=%d must be positive with tokens", V);
+  if (M < 1) return fail(T2I_ERR_SHAPE, "M=%d must be positive", M);
+  if (H < 8 || H % 8 || H > 8 * NORM_THREADS * NORM_MAX_CHUNKS)
+    return fail(T2I_ERR_SHAPE, "H=%d must be a multiple of 8 in [8, %d]", H, 8 * NORM_THREADS * NORM_MAX_CHUNKS);
+  if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(y) || (x_out && !aligned16(x_out)))
+    return fail(T2I_ERR_ALIGN, "rmsnorm pointers must be 16-byte aligned");
+  hipLaunchKernelGGL(t2i::rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, reinterpret_cast<hipStream_t>(stream),
+                     x, tokens, V, H, weight, eps, x_out, y, reinterpret_cast<unsigned long long*>(argmax_keys));
+  return t2i_host::hip_status(hipGetLastError(), "rmsnorm launch");
+}
+
+extern "C" size_t t2i_decode_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t ctx_cap) {
+  if (B < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv || ctx_cap < 1) return 0;
+  return plan_attention(B, Hq, Hkv, ctx_cap).bytes;
+}
+
+extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t B, int32_t Hq,
+                                    int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
+                                    float eps, const uint16_t* rope, int32_t rope_style, uint16_t* k_cache,
+                                    uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  if (!qkv || !positions || !q_norm || !k_norm || !rope || !k_cache || !v_cache || !ctx)
+    return fail(T2I_ERR_NULL, "attention pointers must not be NULL");
+  if (D != ATT_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
+  if (B < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(T2I_ERR_SHAPE, "B=%d Hq=%d Hkv=%d invalid", B, Hq, Hkv);
+  const int Q = Hq / Hkv;
+  if (Q != 1 && Q != 2 && Q != 4 && Q != 8) return fail(T2I_ERR_SHAPE, "Hq/Hkv=%d must be 1, 2, 4 or 8", Q);
+  if (ctx_cap < 1) return fail(T2I_ERR_SHAPE, "ctx_cap=%d must be positive", ctx_cap);
+  if (rope_style != 0 && rope_style != 1) return fail(T2I_ERR_VALUE, "rope_style must be 0 or 1");
+  if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  if (!aligned16(qkv) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(ctx))
+    return fail(T2I_ERR_ALIGN, "attention tensors must be 16-byte aligned");
+  const AttnPlan pl = plan_attention(B, Hq, Hkv, ctx_cap);
+  if (pl.bytes) {
+    if (!workspace) return fail(T2I_ERR_WORKSPACE, "workspace of %zu bytes required", pl.bytes);
+    if (workspace_bytes < pl.bytes) return fail(T2I_ERR_WORKSPACE, "workspace %zu < required %zu", workspace_bytes, pl.bytes);
+    if (!aligned16(workspace)) return fail(T2I_ERR_ALIGN, "workspace must be 16-byte aligned");
+  }
+  AttnParams p{};
+  p.qkv = qkv; p.pos = positions; p.qn = q_norm; p.kn = k_norm; p.rope = rope;
+  p.kc = k_cache; p.vc = v_cache; p.out = ctx;
+  char* ws = reinterpret_cast<char*>(workspace);
+  p.counters = reinterpret_cast<uint32_t*>(ws);
+  p.part_ml = ws ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
+  p.part_o = ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
+  p.Hq = Hq; p.Hkv = Hkv; p.ctx_cap = ctx_cap; p.chunk = pl.chunk; p.splits = pl.splits; p.style = rope_style;
+  p.eps = eps;
+  p.scale = (float)(1.0 / sqrt((double)D));
+  dim3 grid(B * Hkv, pl.splits);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (Q) {
+    case 1: hipLaunchKernelGGL((decode_attention_kernel<1>), grid, dim3(ATT_THREADS), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((decode_attention_kernel<2>), grid, dim3(ATT_THREADS), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((decode_attention_kernel<4>), grid, dim3(ATT_THREADS), 0, s, p); break;
+    default: hipLaunchKernelGGL((decode_attention_kernel<8>), grid, dim3(ATT_THREADS), 0, s, p); break;
+  }
+  return t2i_host::hip_status(hipGetLastError(), "attention launch");
+}
+
+extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,
+                                  float* logits, uint64_t* argmax_keys, void* stream) {
+  if (!h || !E || !argmax_keys) return fail(T2I_ERR_NULL, "h, E and argmax_keys must not be NULL");
+  if (M < 1) return fail(T2I_ERR_SHAPE, "M=%d must be positive", M);
+  if (V < 16 || V % 16) return fail(T2I_ERR_SHAPE, "V=%d must be a positive multiple of 16", V);
+  if (K < 64 || K % 64 || K > LMH_MAX_K) return fail(T2I_ERR_SHAPE, "K=%d must be a multiple of 64 in [64, %d]", K, LMH_MAX_K);
+  if (!aligned16(h) || !aligned16(E) || (logits && !aligned16(logits)))
+    return fail(T2I_ERR_ALIGN, "lm_head tensors must be 16-byte aligned");
+  const int cols_per_wg = LMH_WAVES * LMH_COLS;
+  dim3 grid((V + cols_per_wg - 1) / cols_per_wg);
+  const size_t lds = (size_t)16 * (K + 8) * sizeof(uint16_t);
+  if (lds > 65536) {
+    static thread_local size_t raised = 0;
+    if (lds > raised) {
+      int rc = t2i_host::hip_status(
+          hipFuncSetAttribute(reinterpret_cast<const void*>(t2i::lm_head_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
+          "lm_head LDS attribute");
+      if (rc) return rc;
+      raised = lds;
+    }
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  for (int m0 = 0; m0 < M; m0 += 16) {
+    const int mc = (M - m0) < 16 ? (M - m0) : 16;
+    hipLaunchKernelGGL(t2i::lm_head_kernel, grid, dim3(64 * LMH_WAVES), lds, s, h + (size_t)m0 * K, mc, E, V, K,
+                       logits ? logits + (size_t)m0 * V : nullptr,
+                       reinterpret_cast<unsigned long long*>(argmax_keys) + m0);
+    int rc = t2i_host::hip_status(hipGetLastError(), "lm_head launch");
+    if (rc) return rc;
+  }
+  return T2I_OK;
+}
+
+extern "C" int t2i_greedy_advance(const uint64_t* argmax_keys, int32_t B, int32_t* tokens, int32_t* positions,
+                                  int32_t* history, int32_t hist_cap, int32_t* step, void* stream) {
+  if (!argmax_keys || !tokens || !positions || !step) return fail(T2I_ERR_NULL, "greedy_advance pointers must not be NULL");
+  if (B < 1 || B > 1024) return fail(T2I_ERR_SHAPE, "B=%d must be in [1, 1024]", B);
+  if (history && hist_cap < 1) return fail(T2I_ERR_VALUE, "hist_cap must be positive");
+  hipLaunchKernelGGL(t2i::greedy_advance_kernel, dim3(1), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const unsigned long long*>(argmax_keys), B, tokens, positions, history,
+                     hist_cap, step);
+  return t2i_host::hip_status(hipGetLastError(), "greedy_advance launch");
+}
+
+extern "C" int t2i_prompt_advance(const int32_t* prompt, int32_t B, int32_t P, int32_t* tokens, int32_t* positions,
+                                  void* stream) {
+  if (!prompt || !tokens || !positions) return fail(T2I_ERR_NULL, "prompt_advance pointers must not be NULL");
+  if (B < 1 || B > 1024 || P < 1) return fail(T2I_ERR_SHAPE, "B=%d P=%d invalid", B, P);
+  hipLaunchKernelGGL(t2i::prompt_advance_kernel, dim3(1), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     prompt, B, P, tokens, positions);
+  return t2i_host::hip_status(hipGetLastError(), "prompt_advance launch");
+}

@@ -1,0 +1,135 @@
+"""AutoGPTQ group-128 W4A16 tensors as the MI355X kernels read them.
+
+The kernels consume the checkpoint layout unchanged (``qweight [K/8, N]``,
+``qzeros [K/g, N/8]``, fp16 ``scales [K/g, N]``), so a linear is just these
+three device tensors.  The only offline repacks are column permutations done
+at the nibble level, which are exact:
+
+* ``concat_columns`` fuses q|k|v into one ``N = (Hq + 2 Hkv) * D`` linear;
+* ``interleave_gate_up`` fuses gate|up into one linear whose column ``4i + e``
+  is gate ``2i + e`` and column ``4i + 2 + e`` is up ``2i + e``, so a lane that
+  owns four consecutive output columns owns matching gate/up pairs (the
+  reference pairs gate and up offline the same way,
+  ``packed_format.py:360-369, 548-582``, gate = pair 0).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+GROUP_SIZE = 128
+
+
+@dataclass
+class W4A16Weight:
+    """One AutoGPTQ linear: ``W[n, k] = (q[k, n] - (z[k/g, n] + 1)) * s[k/g, n]``."""
+
+    qweight: torch.Tensor   # int32 [K/8, N]
+    qzeros: torch.Tensor    # int32 [K/g, N/8]
+    scales: torch.Tensor    # fp16  [K/g, N]
+    group_size: int = GROUP_SIZE
+
+    def __post_init__(self):
+        if self.qweight.dtype != torch.int32 or self.qzeros.dtype != torch.int32:
+            raise ValueError("qweight and qzeros must be int32")
+        if self.scales.dtype != torch.float16:
+            raise ValueError("scales must be float16")
+        k8, n = self.qweight.shape
+        if self.scales.shape != (k8 * 8 // self.group_size, n):
+            raise ValueError(f"scales shape {tuple(self.scales.shape)} does not match qweight {tuple(self.qweight.shape)}")
+        if self.qzeros.shape != (self.scales.shape[0], n // 8):
+            raise ValueError(f"qzeros shape {tuple(self.qzeros.shape)} does not match qweight {tuple(self.qweight.shape)}")
+
+    @property
+    def K(self) -> int:
+        return int(self.qweight.shape[0]) * 8
+
+    @property
+    def N(self) -> int:
+        return int(self.qweight.shape[1])
+
+    @property
+    def nbytes(self) -> int:
+        return sum(t.numel() * t.element_size() for t in (self.qweight, self.qzeros, self.scales))
+
+    def to(self, device) -> "W4A16Weight":
+        return W4A16Weight(self.qweight.to(device).contiguous(), self.qzeros.to(device).contiguous(),
+                           self.scales.to(device).contiguous(), self.group_size)
+
+    @classmethod
+    def from_numpy(cls, qweight, qzeros, scales, device="cpu", group_size: int = GROUP_SIZE) -> "W4A16Weight":
+        return cls(torch.from_numpy(np.ascontiguousarray(qweight).view(np.int32)).to(device),
+                   torch.from_numpy(np.ascontiguousarray(qzeros).view(np.int32)).to(device),
+                   torch.from_numpy(np.ascontiguousarray(scales).astype(np.float16)).to(device),
+                   group_size)
+
+    def numpy(self):
+        return (self.qweight.cpu().numpy(), self.qzeros.cpu().numpy(), self.scales.cpu().numpy())
+
+
+def random_tensors(K: int, N: int, seed: int, group_size: int = GROUP_SIZE):
+    """Seeded AutoGPTQ arrays: uniform random words (uniform nibbles 0..15),
+    fp16 scales uniform in [0.005, 0.02]."""
+    rng = np.random.default_rng(seed)
+    qweight = rng.integers(0, 2**32, size=(K // 8, N), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    qzeros = rng.integers(0, 2**32, size=(K // group_size, N // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    scales = rng.uniform(0.005, 0.02, size=(K // group_size, N)).astype(np.float16)
+    return qweight, qzeros, scales
+
+
+def random_weight(K: int, N: int, seed: int, device="cpu") -> W4A16Weight:
+    return W4A16Weight.from_numpy(*random_tensors(K, N, seed), device=device)
+
+
+# ---- nibble-level column permutations (exact repacks) ----
+
+def _words_to_nibbles(words: np.ndarray) -> np.ndarray:
+    w = np.ascontiguousarray(words).view(np.uint32).astype(np.uint64)
+    return ((w[..., None] >> (4 * np.arange(8, dtype=np.uint64))) & 0xF).astype(np.uint8)
+
+
+def _nibbles_to_words(nib: np.ndarray) -> np.ndarray:
+    acc = np.zeros(nib.shape[:-1], dtype=np.uint64)
+    for j in range(8):
+        acc |= nib[..., j].astype(np.uint64) << np.uint64(4 * j)
+    return acc.astype(np.uint32).view(np.int32)
+
+
+def _permute_columns(qweight, qzeros, scales, perm: np.ndarray):
+    """New column n takes old column perm[n]."""
+    qz_nib = _words_to_nibbles(qzeros).reshape(qzeros.shape[0], -1)[:, perm]
+    qzeros_new = _nibbles_to_words(qz_nib.reshape(qzeros.shape[0], -1, 8))
+    return (np.ascontiguousarray(np.asarray(qweight)[:, perm]), qzeros_new,
+            np.ascontiguousarray(np.asarray(scales)[:, perm]))
+
+
+def concat_columns(*parts):
+    """Concatenate AutoGPTQ linears (numpy triples) along N."""
+    qw = np.concatenate([p[0] for p in parts], axis=1)
+    qz = np.concatenate([p[1] for p in parts], axis=1)
+    sc = np.concatenate([p[2] for p in parts], axis=1)
+    return qw, qz, sc
+
+
+def gate_up_permutation(intermediate: int) -> np.ndarray:
+    """Index map of the fused gate|up weight into concat(gate, up) columns."""
+    n = 2 * intermediate
+    perm = np.empty(n, dtype=np.int64)
+    f = np.arange(n)
+    blk, e = f // 4, f % 4
+    perm[:] = np.where(e < 2, 2 * blk + e, intermediate + 2 * blk + (e - 2))
+    return perm
+
+
+def interleave_gate_up(gate, up):
+    """Fuse gate and up (numpy triples with equal K, N) into the paired layout."""
+    inter = int(np.asarray(gate[0]).shape[1])
+    if int(np.asarray(up[0]).shape[1]) != inter:
+        raise ValueError("gate and up must have the same number of columns")
+    if inter % 64:
+        raise ValueError("intermediate size must be a multiple of 64")
+    cat = concat_columns(gate, up)
+    return _permute_columns(*cat, gate_up_permutation(inter))

@@ -1,0 +1,255 @@
+"""Device operators of the W4A16 hot path (PyTorch-ROCm tensors in, HIP kernels run).
+
+Functional layer over the C ABI (``include/t2i_hip.h``).  Tensors must be CUDA
+(HIP) tensors; every call launches on torch's current stream and returns
+without synchronising.  Argument errors raise ``ValueError`` and HIP errors
+``RuntimeError``, as the reference's operators do.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from torch2iron_amd import _lib
+from torch2iron_amd.formats import W4A16Weight
+
+BF16 = torch.bfloat16
+
+ROPE_HALVES = 0
+ROPE_INTERLEAVED = 1
+
+
+class Workspace:
+    """Zero-initialised device scratch buffers keyed by (purpose, bytes).
+
+    The kernels that reduce across workgroups keep arrival counters here and
+    reset them to zero when they finish, so a buffer is zeroed only once.  A
+    buffer must not be used by two launches that overlap in time.
+    """
+
+    def __init__(self):
+        self._bufs: dict = {}
+
+    def get(self, key, nbytes: int, device) -> torch.Tensor | None:
+        if nbytes == 0:
+            return None
+        k = (key, torch.device(device))
+        buf = self._bufs.get(k)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            self._bufs[k] = buf
+        return buf
+
+
+DEFAULT_WORKSPACE = Workspace()
+
+
+def _check_dev(name: str, t: torch.Tensor, dtype=None):
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the W4A16 path has no CPU fallback)")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_weight(w: W4A16Weight):
+    if not isinstance(w, W4A16Weight):
+        raise ValueError("weight must be a W4A16Weight")
+    for n, t in (("qweight", w.qweight), ("qzeros", w.qzeros), ("scales", w.scales)):
+        _check_dev(n, t)
+
+
+def dequantize(w: W4A16Weight) -> torch.Tensor:
+    """Exact fp32 ``W [N, K]`` on the device (test hook for bit-exact parity)."""
+    _check_weight(w)
+    lib = _lib.load()
+    out = torch.empty(w.N, w.K, dtype=torch.float32, device=w.qweight.device)
+    rc = lib.t2i_w4a16_dequant_f32(w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(),
+                                   w.K, w.N, w.group_size, out.data_ptr(), _lib.stream_handle(out.device))
+    _lib.check(rc, "t2i_w4a16_dequant_f32")
+    return out
+
+
+def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None,
+           out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """``y = x @ W^T`` (+ residual, rounded as bf16(bf16(x W^T) + residual)).
+
+    ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case), 1 <= M <= 64.
+    """
+    _check_weight(w)
+    _check_dev("x", x, BF16)
+    squeeze = x.dim() == 1
+    x2 = x.view(1, -1) if squeeze else x
+    if x2.dim() != 2 or x2.shape[1] != w.K:
+        raise ValueError(f"x shape {tuple(x.shape)} does not match K={w.K}")
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty(m, w.N, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != m * w.N:
+        raise ValueError(f"out must hold {m}x{w.N} elements")
+    if residual is not None:
+        _check_dev("residual", residual, BF16)
+        if residual.numel() != m * w.N:
+            raise ValueError(f"residual must hold {m}x{w.N} elements")
+    lib = _lib.load()
+    nbytes = lib.t2i_w4a16_linear_workspace_bytes(m, w.K, w.N)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("linear", m, w.K, w.N), nbytes, x.device)
+    rc = lib.t2i_w4a16_linear(x2.data_ptr(), m, w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(),
+                              w.K, w.N, w.group_size, _lib.ptr(residual), out.data_ptr(),
+                              _lib.ptr(ws), nbytes, _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_w4a16_linear")
+    return out.view(-1) if squeeze else out.view(m, w.N)
+
+
+def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torch.Tensor | None = None,
+            out_up: torch.Tensor | None = None, workspace: Workspace | None = None):
+    """Paired gate/up projection over an ``interleave_gate_up`` weight.
+
+    ``swiglu=True``: returns ``h = silu(gate) * up`` bf16 ``[M, N/2]``.
+    ``swiglu=False``: returns ``(gate, up)``, each ``[M, N/2]``.
+    """
+    _check_weight(w_pair)
+    _check_dev("x", x, BF16)
+    x2 = x.view(1, -1) if x.dim() == 1 else x
+    if x2.dim() != 2 or x2.shape[1] != w_pair.K:
+        raise ValueError(f"x shape {tuple(x.shape)} does not match K={w_pair.K}")
+    m, inter = x2.shape[0], w_pair.N // 2
+    if out is None:
+        out = torch.empty(m, inter, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if not swiglu:
+        if out_up is None:
+            out_up = torch.empty(m, inter, dtype=BF16, device=x.device)
+        _check_dev("out_up", out_up, BF16)
+    lib = _lib.load()
+    nbytes = lib.t2i_w4a16_gate_up_workspace_bytes(m, w_pair.K, w_pair.N)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("linear", m, w_pair.K, w_pair.N), nbytes, x.device)
+    rc = lib.t2i_w4a16_gate_up(x2.data_ptr(), m, w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
+                               w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)),
+                               out.data_ptr(), _lib.ptr(out_up), _lib.ptr(ws), nbytes,
+                               _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_w4a16_gate_up")
+    return out if swiglu else (out, out_up)
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
+            tokens: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+            argmax_keys: torch.Tensor | None = None) -> torch.Tensor:
+    """Weighted RMSNorm of the rows of ``x`` (bf16 rounding as the reference's bf16 path).
+
+    With ``tokens`` (int32 ``[M]``), ``x`` is an embedding table ``[V, H]`` and
+    the gathered rows are also written to ``x_out``.
+    """
+    _check_dev("x", x, BF16)
+    _check_dev("weight", weight, BF16)
+    h = x.shape[-1]
+    if weight.numel() != h:
+        raise ValueError("weight length must equal the row length")
+    if tokens is not None:
+        _check_dev("tokens", tokens, torch.int32)
+        m = tokens.numel()
+        if x_out is None:
+            raise ValueError("x_out is required with tokens")
+        _check_dev("x_out", x_out, BF16)
+    else:
+        m = x.numel() // h
+    if out is None:
+        out = torch.empty(m, h, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if argmax_keys is not None:
+        _check_dev("argmax_keys", argmax_keys, torch.int64)
+    lib = _lib.load()
+    rc = lib.t2i_rmsnorm(x.data_ptr(), _lib.ptr(tokens), x.shape[0] if tokens is not None else 0, m, h,
+                         weight.data_ptr(), float(eps), _lib.ptr(x_out),
+                         out.data_ptr(), _lib.ptr(argmax_keys), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_rmsnorm")
+    return out
+
+
+def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n_kv_heads: int,
+                     q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float, rope: torch.Tensor,
+                     k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
+                     out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """q/k-norm + RoPE + KV write + GQA attention of one token per sequence.
+
+    ``qkv`` bf16 ``[B, (Hq + 2 Hkv) * D]``, caches bf16 ``[B, Hkv, ctx_cap, D]``,
+    ``rope`` bf16 ``[ctx_cap, D]`` (cos even / sin odd), ``positions`` int32 ``[B]``.
+    Returns the context ``[B, Hq * D]`` (bf16).
+    """
+    _check_dev("qkv", qkv, BF16)
+    _check_dev("positions", positions, torch.int32)
+    for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_dev(n, t, BF16)
+    b = positions.numel()
+    d = q_norm.numel()
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must be [B, Hkv, ctx_cap, D] of equal shape")
+    if tuple(k_cache.shape[:2]) != (b, n_kv_heads) or k_cache.shape[3] != d:
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} does not match B={b}, Hkv={n_kv_heads}, D={d}")
+    ctx_cap = k_cache.shape[2]
+    if rope.shape[0] < ctx_cap or rope.shape[1] != d:
+        raise ValueError("rope table must be [>= ctx_cap, D]")
+    if qkv.numel() != b * (n_heads + 2 * n_kv_heads) * d:
+        raise ValueError("qkv must be [B, (Hq + 2 Hkv) * D]")
+    if out is None:
+        out = torch.empty(b, n_heads * d, dtype=BF16, device=qkv.device)
+    _check_dev("out", out, BF16)
+    lib = _lib.load()
+    nbytes = lib.t2i_decode_attention_workspace_bytes(b, n_heads, n_kv_heads, ctx_cap)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("attn", b, n_kv_heads, ctx_cap), nbytes, qkv.device)
+    rc = lib.t2i_decode_attention(qkv.data_ptr(), positions.data_ptr(), b, n_heads, n_kv_heads, d,
+                                  q_norm.data_ptr(), k_norm.data_ptr(), float(eps), rope.data_ptr(), int(rope_style),
+                                  k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap, out.data_ptr(),
+                                  _lib.ptr(ws), nbytes, _lib.stream_handle(qkv.device))
+    _lib.check(rc, "t2i_decode_attention")
+    return out
+
+
+def lm_head_argmax(h: torch.Tensor, embed: torch.Tensor, keys: torch.Tensor,
+                   logits: torch.Tensor | None = None) -> torch.Tensor:
+    """Tied bf16 lm_head + greedy argmax into ``keys`` (int64 ``[M]``, zeroed beforehand)."""
+    _check_dev("h", h, BF16)
+    _check_dev("embed", embed, BF16)
+    _check_dev("keys", keys, torch.int64)
+    m, k = h.shape
+    v = embed.shape[0]
+    if embed.shape[1] != k:
+        raise ValueError("embed must be [V, K] with K = h.shape[1]")
+    if logits is not None:
+        _check_dev("logits", logits, torch.float32)
+        if logits.numel() != m * v:
+            raise ValueError("logits must be [M, V]")
+    lib = _lib.load()
+    rc = lib.t2i_lm_head_argmax(h.data_ptr(), m, embed.data_ptr(), v, k, _lib.ptr(logits), keys.data_ptr(),
+                                _lib.stream_handle(h.device))
+    _lib.check(rc, "t2i_lm_head_argmax")
+    return keys
+
+
+def keys_to_tokens(keys: torch.Tensor) -> torch.Tensor:
+    """Decode argmax keys (``ordered << 32 | (0xFFFFFFFF - index)``) into indices."""
+    low = keys & 0xFFFFFFFF
+    return (0xFFFFFFFF - low).to(torch.int64)
+
+
+def greedy_advance(keys, tokens, positions, history, step):
+    """Device-side greedy bookkeeping between captured decode steps."""
+    lib = _lib.load()
+    b = tokens.numel()
+    rc = lib.t2i_greedy_advance(keys.data_ptr(), b, tokens.data_ptr(), positions.data_ptr(),
+                                history.data_ptr(), history.shape[1], step.data_ptr(),
+                                _lib.stream_handle(tokens.device))
+    _lib.check(rc, "t2i_greedy_advance")
+
+
+def prompt_advance(prompt, tokens, positions):
+    """Teacher-forced prompt bookkeeping (``prompt`` int32 ``[B, P]``)."""
+    lib = _lib.load()
+    b, plen = prompt.shape
+    rc = lib.t2i_prompt_advance(prompt.data_ptr(), b, plen, tokens.data_ptr(), positions.data_ptr(),
+                                _lib.stream_handle(tokens.device))
+    _lib.check(rc, "t2i_prompt_advance")
