@@ -1,0 +1,247 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X W4A16 hot path (one GPU).
+
+Workload (one "step"): the W4A16 group-128 linear over every Qwen3-0.6B linear
+shape -- fused qkv K=1024 N=4096, o_proj K=2048 N=1024, fused gate_up K=1024
+N=6144, down K=3072 N=1024 -- at M in {1, 8, 16, 32, 64} (batched decode), each
+(M, shape) pair launched once per weight copy of a pool larger than the
+256 MB MALL, so weights stream from HBM (HBM-cold).  The launches are
+captured in HIP graphs; inputs are resident in HBM before the timed region.
+
+``value`` = algorithmic bytes of all launches / wall time of the timed steps
+(TB/s).  Algorithmic bytes per launch: K*N/2 (int4) + (K/128)*N*2 (fp16
+scales) + (K/128)*(N/8)*4 (int32 zeros) + M*K*2 + M*N*2 (bf16 in/out).
+
+Extra fields: the MALL-warm rate (one weight copy reused), the per-(M, shape)
+breakdown, the Qwen3-1.7B sweep, a roofline entry for the linear kernel and
+the CPU baseline (the oracle's dequant + fp32 matmul on the host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+METRIC = "W4A16 linear achieved HBM TB/s (% of peak); batch-decode tokens/s"
+PEAK_GBPS = 8000.0
+QWEN3_06B = [("qkv", 1024, 4096), ("o_proj", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)]
+QWEN3_17B = [("qkv", 2048, 4096), ("o_proj", 2048, 2048), ("gate_up", 2048, 12288), ("down", 6144, 2048)]
+MALL_BYTES = 256 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--pool-mb", type=int, default=320, help="weight pool per sweep (> 256 MB MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-extra", action="store_true", help="only the headline sweep")
+    return ap.parse_args()
+
+
+class Sweep:
+    """Graph-captured launches of one (M, shape) grid over a weight pool."""
+
+    def __init__(self, shapes, ms, pool_bytes, dev, seed):
+        import torch
+        from torch2iron_amd import ops
+        from torch2iron_amd.formats import algorithmic_bytes, random_weight_on_device
+
+        self.torch = torch
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        per_copy = sum(k * n // 2 + (k // 128) * n * 2 + (k // 128) * (n // 8) * 4 for _, k, n in shapes)
+        self.per_copy = per_copy
+        self.copies = max(1, -(-pool_bytes // per_copy)) if pool_bytes else 1
+        self.weights = {name: [random_weight_on_device(k, n, gen, dev) for _ in range(self.copies)]
+                        for name, k, n in shapes}
+        self.groups = []   # (label, M, K, N, graph, bytes, launches)
+        for m in ms:
+            for name, k, n in shapes:
+                x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
+                y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+                ops.linear(x, self.weights[name][0], out=y)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    for w in self.weights[name]:
+                        ops.linear(x, w, out=y)
+                self.groups.append(dict(label=f"{name}/M{m}", M=m, K=k, N=n, graph=g, x=x, y=y,
+                                        bytes=algorithmic_bytes(m, k, n) * self.copies, launches=self.copies))
+        self.bytes_per_step = sum(gr["bytes"] for gr in self.groups)
+        self.launches_per_step = sum(gr["launches"] for gr in self.groups)
+
+    def run(self, steps, warmup):
+        torch = self.torch
+        for _ in range(warmup):
+            for gr in self.groups:
+                gr["graph"].replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        marks = [[torch.cuda.Event(enable_timing=True) for _ in self.groups] for _ in range(steps)]
+        start.record()
+        for s in range(steps):
+            for i, gr in enumerate(self.groups):
+                gr["graph"].replay()
+                marks[s][i].record()
+        torch.cuda.synchronize()
+        total_ms = start.elapsed_time(marks[-1][-1])
+        per_group = [0.0] * len(self.groups)
+        for s in range(steps):
+            prev = start if s == 0 else marks[s - 1][-1]
+            for i in range(len(self.groups)):
+                per_group[i] += prev.elapsed_time(marks[s][i])
+                prev = marks[s][i]
+        per_group = [t / steps for t in per_group]
+        return total_ms, per_group
+
+
+def cpu_baseline(seconds: float):
+    """The oracle (numpy) on the host: per-call dequant + fp32 matmul, M=16,
+    over the four Qwen3-0.6B shapes in turn, for about ``seconds``."""
+    import numpy as np
+    from oracle import w4a16 as ow
+    from torch2iron_amd.formats import algorithmic_bytes
+
+    try:
+        from threadpoolctl import threadpool_info
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # noqa: BLE001
+        cores = os.cpu_count() or 1
+    m = 16
+    data = []
+    for i, (_, k, n) in enumerate(QWEN3_06B):
+        qw, qz, sc = ow.synthetic_tensors(k, n, seed=100 + i)
+        x = np.random.default_rng(i).standard_normal((m, k)).astype(np.float32)
+        data.append((x, qw, qz, sc, algorithmic_bytes(m, k, n)))
+    calls, nbytes = 0, 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        x, qw, qz, sc, b = data[calls % len(data)]
+        ow.linear(x, qw, qz, sc, accumulate="fp32")
+        calls += 1
+        nbytes += b
+    dt = time.perf_counter() - t0
+    # cached dense weights (the reference caches its unpacked weight)
+    dense = [(x, ow.dequantize(qw, qz, sc), b) for x, qw, qz, sc, b in data]
+    ccalls, cbytes = 0, 0
+    t1 = time.perf_counter()
+    while time.perf_counter() - t1 < min(seconds, 5.0):
+        x, w, b = dense[ccalls % len(dense)]
+        _ = x @ w.T
+        ccalls += 1
+        cbytes += b
+    cdt = time.perf_counter() - t1
+    return {
+        "value": nbytes / dt / 1e12, "unit": "TB/s", "cores": int(cores), "kind": "port",
+        "sample": f"{calls} calls of oracle dequant+fp32 matmul (M=16, Qwen3-0.6B shapes in turn) in {dt:.1f} s",
+        "cached_weights_value": cbytes / cdt / 1e12,
+        "cached_weights_sample": f"{ccalls} fp32 matmuls with cached dense weights in {cdt:.1f} s",
+        "cpu_count": os.cpu_count(),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the W4A16 path would shard by output columns, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from torch2iron_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    ms = [1, 8, 16, 32, 64]
+    log(f"building HBM-cold sweep (pool {args.pool_mb} MB)")
+    cold = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1)
+    log(f"{cold.copies} weight copies, {cold.launches_per_step} launches/step, "
+        f"{cold.bytes_per_step / 1e6:.1f} MB/step")
+    total_ms, per_group = cold.run(args.steps, args.warmup)
+    torch.cuda.synchronize()
+    # barrier-equivalent for one process: synchronised on both sides of the timed region
+    ms_per_step = total_ms / args.steps
+    value = cold.bytes_per_step / (ms_per_step * 1e-3) / 1e12
+    avg_launch_us = ms_per_step * 1e3 / cold.launches_per_step
+    log(f"HBM-cold sweep: {value:.3f} TB/s, {ms_per_step:.3f} ms/step, avg launch {avg_launch_us:.2f} us")
+    breakdown = {}
+    for gr, t in zip(cold.groups, per_group):
+        breakdown[gr["label"]] = {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
+                                  "us_per_launch": round(t * 1e3 / gr["launches"], 3)}
+
+    extra = {}
+    if not args.skip_extra:
+        log("MALL-warm sweep (one weight copy)")
+        warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2)
+        w_ms, _ = warm.run(args.steps, args.warmup)
+        extra["mall_warm_TBps"] = round(warm.bytes_per_step / (w_ms / args.steps * 1e-3) / 1e12, 4)
+        del warm
+        log("Qwen3-1.7B sweep (HBM-cold)")
+        big = Sweep(QWEN3_17B, [1, 16, 64], args.pool_mb << 20, dev, seed=3)
+        b_ms, b_groups = big.run(max(2, args.steps // 2), 1)
+        extra["qwen3_1_7b_sweep_TBps"] = round(big.bytes_per_step / (b_ms / max(2, args.steps // 2) * 1e-3) / 1e12, 4)
+        extra["qwen3_1_7b_breakdown"] = {gr["label"]: round(gr["bytes"] / (t * 1e-3) / 1e12, 4)
+                                         for gr, t in zip(big.groups, b_groups)}
+        del big
+    torch.cuda.synchronize()
+
+    cpu = None
+    if not args.skip_cpu:
+        log(f"CPU baseline ({args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    achieved_gbps = value * 1e3
+    line = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "W4A16 group-128 linear sweep, Qwen3-0.6B qkv/o_proj/gate_up/down x M in {1,8,16,32,64}, "
+                        f"HBM-cold ({cold.copies}-copy weight pool, {cold.copies * cold.per_copy / 1e6:.0f} MB)",
+            "weights": "int4 AutoGPTQ (uniform nibbles, fp16 scales U[0.005,0.02])",
+            "activations": "bf16 N(0,1)",
+            "launches_per_step": cold.launches_per_step,
+            "bytes_per_step": cold.bytes_per_step,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbps, 1),
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbps / PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": "w4a16_mfma_kernel",
+            "avg_launch_us": round(avg_launch_us, 3),
+        },
+        "cpu_baseline": cpu,
+        "breakdown": breakdown,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

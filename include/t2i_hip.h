@@ -17,8 +17,9 @@
  * W[n][k] = (q[k][n] - z[k/g][n]) * s[k/g][n].  Group size g = 128.
  * Activations are bf16 (uint16_t bit patterns), row-major, 16-byte aligned.
  *
- * Workspace: entry points that reduce across workgroups take a caller-owned
- * workspace sized by the matching *_workspace_bytes() query.  It must be
+ * Workspace: entry points that reduce across workgroups (the split-context
+ * attention) take a caller-owned workspace sized by the matching
+ * *_workspace_bytes() query.  It must be
  * zero-filled once before its first use; the kernels leave their counters at
  * zero again when they finish.  Calls that overlap in time (different
  * streams) must not share a workspace.
@@ -67,27 +68,22 @@ int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,
  *           and the CPU oracle quantized_qwen3/model.py:133-146.
  * Residual form replaces fast_qwen3/operators/q4nx_fused_linear_residual_projection/op.py:31-118.
  */
-size_t t2i_w4a16_linear_workspace_bytes(int32_t M, int32_t K, int32_t N);
 int t2i_w4a16_linear(const uint16_t* x, int32_t M,
                      const int32_t* qweight, const int32_t* qzeros,
                      const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
-                     const uint16_t* residual, uint16_t* y,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     const uint16_t* residual, uint16_t* y, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Paired gate/up linear over one weight whose columns interleave gate and up
- * in blocks of two (fused column 4i+e = gate 2i+e, 4i+2+e = up 2i+e, e in {0,1};
- * N = 2*I).  swiglu != 0: h[M, I] = bf16(bf16(silu(bf16 gate)) * bf16 up) into y0,
+ * Paired gate/up linear over one weight whose columns alternate gate and up
+ * (fused column 2i = gate i, 2i+1 = up i; N = 2*I, N % 64 == 0).  swiglu != 0: h[M, I] = bf16(bf16(silu(bf16 gate)) * bf16 up) into y0,
  * y1 unused.  swiglu == 0: y0 = gate [M, I], y1 = up [M, I].
  * Replaces: quantized_qwen3/operators/w4a16_gemm/op.py:178-263 (W4A16PairedKGroupGEMM,
  *           gate = pair 0, up = pair 1) + torch2iron/operators/silu_mul (SiLUMul).
  */
-size_t t2i_w4a16_gate_up_workspace_bytes(int32_t M, int32_t K, int32_t N);
 int t2i_w4a16_gate_up(const uint16_t* x, int32_t M,
                       const int32_t* qweight, const int32_t* qzeros,
                       const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
-                      int32_t swiglu, uint16_t* y0, uint16_t* y1,
-                      void* workspace, size_t workspace_bytes, void* stream);
+                      int32_t swiglu, uint16_t* y0, uint16_t* y1, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Weighted RMSNorm over rows of H: y = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * w).

@@ -310,6 +310,18 @@ class DenseQwen3:
         return self.logits(x)
 
     @torch.no_grad()
+    def forced_logits(self, prompt: torch.Tensor, forced: torch.Tensor) -> torch.Tensor:
+        """Logits after the prompt and after each of the ``forced [B, S]`` tokens
+        (teacher forcing): ``[B, S + 1, V]``."""
+        b, t = prompt.shape
+        out = [self.prefill(prompt)]
+        positions = torch.full((b,), t, dtype=torch.long)
+        for j in range(forced.shape[1]):
+            out.append(self.decode_step(forced[:, j], positions))
+            positions = positions + 1
+        return torch.stack(out, dim=1)
+
+    @torch.no_grad()
     def generate(self, prompt: torch.Tensor, new_tokens: int, return_margins: bool = False):
         """Greedy decode as ``qwen_npu.py:309-325``: the first new token comes
         from the prompt pass, then ``new_tokens - 1`` decode steps."""

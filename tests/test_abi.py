@@ -18,7 +18,7 @@ MISALIGNED = 0x10002
 
 def declared_functions():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^[a-z_ ]+?[\s\*](t2i_\w+)\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:const\s+)?\w+\s*\*?\s*(t2i_\w+)\(", text, flags=re.M)))
 
 
 def test_library_loads_and_exports_every_declared_symbol():
@@ -43,19 +43,19 @@ def test_library_loads_and_exports_every_declared_symbol():
 ])
 def test_linear_argument_errors(M, K, N, group, x, code):
     lib = _lib.load()
-    rc = lib.t2i_w4a16_linear(x, M, FAKE, FAKE, FAKE, K, N, group, None, FAKE, None, 0, None)
+    rc = lib.t2i_w4a16_linear(x, M, FAKE, FAKE, FAKE, K, N, group, None, FAKE, None)
     assert rc == code
     assert lib.t2i_last_error()
 
 
-def test_linear_requires_workspace_when_split():
+def test_linear_residual_and_pair_validation():
     lib = _lib.load()
-    need = lib.t2i_w4a16_linear_workspace_bytes(1, 2048, 1024)
-    assert need > 0, "a 1024-column linear splits K across workgroups"
-    rc = lib.t2i_w4a16_linear(FAKE, 1, FAKE, FAKE, FAKE, 2048, 1024, 128, None, FAKE, None, 0, None)
-    assert rc == _lib.T2I_ERR_WORKSPACE
-    rc = lib.t2i_w4a16_linear(FAKE, 1, FAKE, FAKE, FAKE, 2048, 1024, 128, None, FAKE, FAKE, need - 1, None)
-    assert rc == _lib.T2I_ERR_WORKSPACE
+    assert lib.t2i_w4a16_linear(FAKE, 1, FAKE, FAKE, FAKE, 2048, 1024, 128, MISALIGNED, FAKE, None) \
+        == _lib.T2I_ERR_ALIGN
+    assert lib.t2i_w4a16_gate_up(FAKE, 1, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None) \
+        == _lib.T2I_ERR_NULL
+    assert lib.t2i_w4a16_gate_up(FAKE, 1, FAKE, FAKE, FAKE, 1024, 6144, 64, 1, FAKE, None, None) \
+        == _lib.T2I_ERR_GROUP
 
 
 def test_other_entry_points_validate():
@@ -74,8 +74,6 @@ def test_other_entry_points_validate():
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151930, 1024, None, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151936, 1024, None, None, None) == _lib.T2I_ERR_NULL
     assert lib.t2i_w4a16_dequant_f32(FAKE, FAKE, FAKE, 1024, 3072, 128, None, None) == _lib.T2I_ERR_NULL
-    assert lib.t2i_w4a16_gate_up(FAKE, 4, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None, 0, None) \
-        == _lib.T2I_ERR_NULL
 
 
 def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
@@ -89,8 +87,5 @@ def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
 
 def test_workspace_sizes_are_consistent():
     lib = _lib.load()
-    for (m, k, n) in [(1, 1024, 3072), (16, 1024, 4096), (64, 2048, 1024), (64, 6144, 2048), (8, 3072, 1024)]:
-        b = lib.t2i_w4a16_linear_workspace_bytes(m, k, n)
-        assert b == 0 or b >= m * n * 4 * 2
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) > 0
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0

@@ -121,3 +121,14 @@ def test_gate_up_paired_and_swiglu(gpu, m, k, inter):
     # and the fp64 truth within tolerance
     truth = (g_ref / (1 + np.exp(-g_ref))) * u_ref
     assert np.abs(h - truth).max() / np.abs(truth).max() <= 1e-2
+
+
+def test_golden_fixture_on_gpu(gpu):
+    """The brute-force fixture (tests/golden/make_golden.py): bit-exact weights, linear within tolerance."""
+    from pathlib import Path
+    g = np.load(Path(__file__).resolve().parent / "golden" / "w4a16_small.npz")
+    w = W4A16Weight.from_numpy(g["qweight"], g["qzeros"], g["scales"], device=gpu)
+    assert np.array_equal(ops.dequantize(w).cpu().numpy().view(np.uint32), g["W"].view(np.uint32))
+    x = torch.from_numpy(g["x"]).to(torch.bfloat16)
+    assert torch.equal(x.float(), torch.from_numpy(g["x"])), "fixture activations are bf16 values"
+    check_linear(ops.linear(x.to(gpu), w), g["y"])

@@ -29,12 +29,10 @@ SIGNATURES = {
     "t2i_strerror": (ctypes.c_char_p, [c_int32]),
     "t2i_last_error": (ctypes.c_char_p, []),
     "t2i_w4a16_dequant_f32": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
-    "t2i_w4a16_linear_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "t2i_w4a16_linear": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
-                                   c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
-    "t2i_w4a16_gate_up_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+                                   c_void_p, c_void_p, c_void_p]),
     "t2i_w4a16_gate_up": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
-                                    c_int32, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+                                    c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_float, c_void_p,
                               c_void_p, c_void_p, c_void_p]),
     "t2i_decode_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),

@@ -3,32 +3,33 @@
 // Weights stay in the AutoGPTQ layout.  One int32 word of qweight holds the
 // 8 consecutive k of one column, which is exactly the 8 bf16 values one lane
 // feeds to v_mfma_f32_16x16x32_bf16 as its B operand, so weights go from a
-// 128-bit global load straight into registers with no LDS staging:
+// global load straight into registers with no LDS staging:
 //
 //   * lane (c = lane % 16, r = lane / 16) loads, for qweight row 4*kstep + r,
 //     LW consecutive words at columns ncol .. ncol+LW-1 (ncol = n0 + LW*c);
 //     word t feeds n-tile t, whose MFMA column c is output column ncol + t;
 //   * a nibble becomes bf16 (128 + q) with one AND-OR against 0x43004300
-//     (bf16 128.0 has a unit of least precision of exactly 1), four
-//     AND-ORs and three shifts per word, in k order (0,4,1,5,2,6,3,7);
+//     (bf16 128.0 has a unit of least precision of exactly 1): four AND-ORs
+//     and three shifts per word, giving k order (0,4,1,5,2,6,3,7);
 //   * the activation operand is permuted into the same k order (the
 //     contraction only needs A and B to agree on it);
-//   * per group of 128 k the MFMA sums acc = sum x*(128+q) and, with an
-//     all-ones B, xs = sum x; the group's exact contribution is then
-//     s * (acc - (128 + z) * xs), accumulated in fp32 (scale after dot).
+//   * per chunk of k-steps inside one group the MFMA sums acc = sum x*(128+q)
+//     and, against an all-ones B, xs = sum x; the chunk's exact contribution
+//     is s * (acc - (128 + z) * xs), accumulated in fp32 (scale after dot).
 //
-// A workgroup of W waves shares one column block and splits the block's K
-// range between its waves; their fp32 sums meet in LDS.  When there are too
-// few column blocks to fill the GPU, `splits` workgroups share a column block
-// and the last one to finish (atomic counter in the workspace) adds the fp32
-// partials in split order, so the result does not depend on timing.
+// A workgroup of W waves owns one column block of 16*LW columns and one tile
+// of 16 rows (more rows go to grid.z and share the weights through L2); its
+// waves split the K range (double-buffered chunks of CK k-steps) and their
+// fp32 sums meet in LDS in a fixed tree, so results do not depend on timing.
+#include <stdio.h>
+#include <stdlib.h>
+
 #include "t2i_common.h"
 
 namespace t2i {
 
 constexpr int GS = 128;             // quantisation group along K
-constexpr int KS = GS / 32;         // MFMA k-steps per group
-constexpr int WAVES = 4;            // waves per workgroup
+constexpr int KSG = GS / 32;        // MFMA k-steps per group
 constexpr uint32_t MAGIC = 0x43004300u;  // two bf16 128.0
 constexpr uint32_t NIB2 = 0x000F000Fu;
 
@@ -42,13 +43,10 @@ struct LinearParams {
   const uint16_t* residual;
   uint16_t* y0;
   uint16_t* y1;
-  float* partial;       // [splits][M][N] fp32
-  uint32_t* counters;   // one per column block
   int M, K, N;
   int ldx, ldy;
-  int n_groups;         // K / GS
-  int gpw;              // groups per wave
-  int splits;           // workgroups per column block
+  int chunks;           // K / (32 * CK)
+  int epi;
 };
 
 __device__ __forceinline__ bf16x8 b_operand(uint32_t w) {
@@ -80,242 +78,233 @@ __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)
 template <int LW>
 __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&w)[LW]) {
   if constexpr (LW == 8) {
-    u32x4 a = *reinterpret_cast<const u32x4*>(src);
-    u32x4 b = *reinterpret_cast<const u32x4*>(src + 4);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(src + 4);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
     w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
-  } else {
-    u32x4 a = *reinterpret_cast<const u32x4*>(src);
+  } else if constexpr (LW == 4) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
     w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (LW == 2) {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(src);
+    w[0] = a.x; w[1] = a.y;
+  } else {
+    w[0] = *src;
   }
 }
 
 template <int LW>
 __device__ __forceinline__ void load_scales(const uint16_t* src, float (&s)[LW]) {
   if constexpr (LW == 8) {
-    u32x4 a = *reinterpret_cast<const u32x4*>(src);
-    uint32_t v[4] = {a.x, a.y, a.z, a.w};
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) { s[2 * i] = f16_to_f32(v[i] & 0xFFFFu); s[2 * i + 1] = f16_to_f32(v[i] >> 16); }
-  } else {
-    u32x2 a = *reinterpret_cast<const u32x2*>(src);
+  } else if constexpr (LW == 4) {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(src);
     s[0] = f16_to_f32(a.x & 0xFFFFu); s[1] = f16_to_f32(a.x >> 16);
     s[2] = f16_to_f32(a.y & 0xFFFFu); s[3] = f16_to_f32(a.y >> 16);
+  } else if constexpr (LW == 2) {
+    const uint32_t a = *reinterpret_cast<const uint32_t*>(src);
+    s[0] = f16_to_f32(a & 0xFFFFu); s[1] = f16_to_f32(a >> 16);
+  } else {
+    s[0] = f16_to_f32(*src);
   }
 }
 
-template <int MT, int LW, int EPI>
-__global__ __launch_bounds__(64 * WAVES) void w4a16_mfma_kernel(const LinearParams p) {
-  constexpr int NT = LW;
-  constexpr int E = MT * NT * 4;      // fp32 results per lane
+// Operands of one chunk (CK k-steps, all inside one quantisation group).
+template <int MT, int LW, int CK>
+struct Chunk {
+  uint32_t w[CK][LW];
+  u32x4 x[MT][CK];
+  float s[LW];
+  uint32_t z;   // zero nibbles of this lane's columns, column ncol + t at bits 4t
+};
+
+template <int MT, int LW, int CK>
+__device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
+                                           Chunk<MT, LW, CK>& b) {
+  const int ks0 = ch * CK;
+#pragma unroll
+  for (int j = 0; j < CK; ++j)
+    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    const int m = mbase + mi * 16 + c;
+#pragma unroll
+    for (int j = 0; j < CK; ++j) {
+      if (m < p.M)
+        b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+      else
+        b.x[mi][j] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  const int g = ks0 / KSG;
+  load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s);
+  b.z = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)] >> ((ncol & 7) * 4);
+}
+
+template <int MT, int LW, int CK>
+__device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4]) {
+  const bf16x8 ones = ones_operand();
+  f32x4 acc[MT][LW];
+  f32x4 xs[MT];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < LW; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+    bf16x8 bop[LW];
+#pragma unroll
+    for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t]);
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+      const bf16x8 a = a_operand(b.x[mi][j]);
+      xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < LW; ++t)
+        acc[mi][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop[t], acc[mi][t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < LW; ++t) {
+    const float zb = -(float)(128 + 1 + ((b.z >> (4 * t)) & 0xFu));
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        total[mi][t][i] = fmaf(b.s[t], fmaf(zb, xs[mi][i], acc[mi][t][i]), total[mi][t][i]);
+  }
+}
+
+template <int MT, int LW>
+__device__ __forceinline__ void epilogue(const LinearParams& p, int ncol, int r, int mbase,
+                                         const float (&total)[MT][LW][4]) {
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = mbase + mi * 16 + r * 4 + i;
+      if (m >= p.M) continue;
+      if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
+        float v[LW];
+#pragma unroll
+        for (int t = 0; t < LW; ++t) v[t] = total[mi][t][i];
+        if (p.epi == EPI_RESIDUAL) {
+          const uint16_t* res = p.residual + (size_t)m * p.ldy + ncol;
+#pragma unroll
+          for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32(res[t]);
+        }
+        uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
+        if constexpr (LW == 1) {
+          dst[0] = (uint16_t)f32_to_bf16(v[0]);
+        } else {
+          uint32_t packed[LW / 2];
+#pragma unroll
+          for (int j = 0; j < LW / 2; ++j) packed[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+          if constexpr (LW == 8) *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+          else if constexpr (LW == 4) *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
+          else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+        }
+      } else if constexpr (LW >= 2) {
+        // fused column 2q = gate q, 2q + 1 = up q
+        float o0[LW / 2], o1[LW / 2];
+#pragma unroll
+        for (int q = 0; q < LW / 2; ++q) {
+          const float g = round_bf16(total[mi][2 * q][i]);
+          const float u = round_bf16(total[mi][2 * q + 1][i]);
+          if (p.epi == EPI_SWIGLU) {
+            o0[q] = round_bf16(silu_f32(g)) * u;
+            o1[q] = 0.0f;
+          } else {
+            o0[q] = g;
+            o1[q] = u;
+          }
+        }
+        const size_t off = (size_t)m * p.ldy + (ncol >> 1);
+        if constexpr (LW == 8) {
+          *reinterpret_cast<u32x2*>(p.y0 + off) = u32x2{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3])};
+          if (p.epi == EPI_PAIRED)
+            *reinterpret_cast<u32x2*>(p.y1 + off) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+        } else if constexpr (LW == 4) {
+          *reinterpret_cast<uint32_t*>(p.y0 + off) = pack_bf16x2(o0[0], o0[1]);
+          if (p.epi == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = pack_bf16x2(o1[0], o1[1]);
+        } else {
+          p.y0[off] = (uint16_t)f32_to_bf16(o0[0]);
+          if (p.epi == EPI_PAIRED) p.y1[off] = (uint16_t)f32_to_bf16(o1[0]);
+        }
+      }
+    }
+}
+
+template <int MT, int LW, int W, int CK>
+__global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p) {
+  constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int r = lane >> 4;
   const int ncol = blockIdx.x * (16 * LW) + LW * c;
-  const int g_begin = (blockIdx.y * WAVES + wave) * p.gpw;
-  const int g_end = min(g_begin + p.gpw, p.n_groups);
+  const int mbase = blockIdx.z * (16 * MT);   // row tile of this workgroup
 
-  float total[MT][NT][4];
+  // this wave's chunks: a contiguous slice of K
+  const int per_wave = (p.chunks + W - 1) / W;
+  const int c_begin = wave * per_wave;
+  const int c_end = min(c_begin + per_wave, p.chunks);
+
+  float total[MT][LW][4];
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < LW; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
 
-  const bf16x8 ones = ones_operand();
-
-  for (int g = g_begin; g < g_end; ++g) {
-    uint32_t wv[KS][LW];
-    u32x4 xv[MT][KS];
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const uint32_t* src = p.qw + (size_t)(g * (GS / 8) + ks * 4 + r) * p.N + ncol;
-      load_words<LW>(src, wv[ks]);
-    }
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-      const int m = mi * 16 + c;
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (m < p.M) {
-          xv[mi][ks] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + g * GS + ks * 32 + r * 8);
-        } else {
-          xv[mi][ks] = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
-    }
-    float s[LW];
-    load_scales<LW>(p.sc + (size_t)g * p.N + ncol, s);
-    const uint32_t zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)] >> ((ncol & 7) * 4);
-
-    f32x4 acc[MT][NT];
-    f32x4 xs[MT];
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi) {
-      xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < NT; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      bf16x8 bop[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) bop[t] = b_operand(wv[ks][t]);
-#pragma unroll
-      for (int mi = 0; mi < MT; ++mi) {
-        const bf16x8 a = a_operand(xv[mi][ks]);
-        xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
-#pragma unroll
-        for (int t = 0; t < NT; ++t)
-          acc[mi][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop[t], acc[mi][t], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const float zb = -(float)(128 + 1 + ((zw >> (4 * t)) & 0xFu));
-#pragma unroll
-      for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          total[mi][t][i] = fmaf(s[t], fmaf(zb, xs[mi][i], acc[mi][t][i]), total[mi][t][i]);
+  if (c_begin < c_end) {
+    Chunk<MT, LW, CK> A, B;
+    load_chunk(p, c_begin, ncol, c, r, mbase, A);
+    for (int ch = c_begin; ch < c_end; ch += 2) {
+      if (ch + 1 < c_end) load_chunk(p, ch + 1, ncol, c, r, mbase, B);
+      compute_chunk(A, total);
+      if (ch + 1 >= c_end) break;
+      if (ch + 2 < c_end) load_chunk(p, ch + 2, ncol, c, r, mbase, A);
+      compute_chunk(B, total);
     }
   }
 
-  // ---- reduce the waves of this workgroup in LDS (fixed order) ----
-  __shared__ float red[(WAVES - 1) * E * 64];
-  if (wave > 0) {
+  // ---- reduce the waves of this workgroup in LDS (fixed tree) ----
+  if constexpr (W > 1) {
+    __shared__ float red[(W / 2) * E * 64];
 #pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
+    for (int half = W / 2; half >= 1; half >>= 1) {
+      if (wave >= half && wave < 2 * half) {
+        float* dst = red + (wave - half) * E * 64 + lane;
 #pragma unroll
-      for (int t = 0; t < NT; ++t)
+        for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          red[(((wave - 1) * E) + (mi * NT + t) * 4 + i) * 64 + lane] = total[mi][t][i];
+          for (int t = 0; t < LW; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
+      }
+      __syncthreads();
+      if (wave < half) {
+        const float* src = red + wave * E * 64 + lane;
+#pragma unroll
+        for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+          for (int t = 0; t < LW; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) total[mi][t][i] += src[((mi * LW + t) * 4 + i) * 64];
+      }
+      __syncthreads();
+    }
   }
-  __syncthreads();
   if (wave != 0) return;
-#pragma unroll
-  for (int w = 1; w < WAVES; ++w)
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          total[mi][t][i] += red[(((w - 1) * E) + (mi * NT + t) * 4 + i) * 64 + lane];
 
-  // ---- cross-workgroup split-K: last finisher sums partials in split order ----
-  if (p.splits > 1) {
-    float* part = p.partial + (size_t)blockIdx.y * p.M * p.N;
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = mi * 16 + r * 4 + i;
-        if (m < p.M) {
-          float* dst = part + (size_t)m * p.N + ncol;
-#pragma unroll
-          for (int t = 0; t < NT; t += 4)
-            *reinterpret_cast<f32x4*>(dst + t) =
-                f32x4{total[mi][t][i], total[mi][t + 1][i], total[mi][t + 2][i], total[mi][t + 3][i]};
-        }
-      }
-    __threadfence();
-    uint32_t prev = 0;
-    if (lane == 0)
-      prev = __hip_atomic_fetch_add(&p.counters[blockIdx.x], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __shfl(prev, 0, 64);
-    if (prev != (uint32_t)(p.splits - 1)) return;
-    __threadfence();
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int t = 0; t < NT; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
-    for (int sp = 0; sp < p.splits; ++sp) {
-      const float* src = p.partial + (size_t)sp * p.M * p.N;
-#pragma unroll
-      for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = mi * 16 + r * 4 + i;
-          if (m < p.M) {
-            const float* s4 = src + (size_t)m * p.N + ncol;
-#pragma unroll
-            for (int t = 0; t < NT; t += 4) {
-              f32x4 v = *reinterpret_cast<const f32x4*>(s4 + t);
-              total[mi][t][i] += v.x; total[mi][t + 1][i] += v.y;
-              total[mi][t + 2][i] += v.z; total[mi][t + 3][i] += v.w;
-            }
-          }
-        }
-    }
-    if (lane == 0) __hip_atomic_store(&p.counters[blockIdx.x], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  // ---- epilogue (C layout: lane holds rows mi*16 + 4r + i, columns ncol .. ncol+LW-1) ----
-#pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = mi * 16 + r * 4 + i;
-      if (m >= p.M) continue;
-      if constexpr (EPI == EPI_STORE || EPI == EPI_RESIDUAL) {
-        uint32_t packed[LW / 2];
-        if constexpr (EPI == EPI_RESIDUAL) {
-          const uint16_t* res = p.residual + (size_t)m * p.ldy + ncol;
-          uint32_t rv[LW / 2];
-          if constexpr (LW == 8) {
-            u32x4 a = *reinterpret_cast<const u32x4*>(res);
-            rv[0] = a.x; rv[1] = a.y; rv[2] = a.z; rv[3] = a.w;
-          } else {
-            u32x2 a = *reinterpret_cast<const u32x2*>(res);
-            rv[0] = a.x; rv[1] = a.y;
-          }
-#pragma unroll
-          for (int j = 0; j < LW / 2; ++j)
-            packed[j] = pack_bf16x2(round_bf16(total[mi][2 * j][i]) + bf16_lo(rv[j]),
-                                    round_bf16(total[mi][2 * j + 1][i]) + bf16_hi(rv[j]));
-        } else {
-#pragma unroll
-          for (int j = 0; j < LW / 2; ++j)
-            packed[j] = pack_bf16x2(total[mi][2 * j][i], total[mi][2 * j + 1][i]);
-        }
-        uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
-        if constexpr (LW == 8) {
-          *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-        } else {
-          *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
-        }
-      } else {
-        // fused columns 4j+e = gate 2j+e, 4j+2+e = up 2j+e
-        uint32_t out0[LW / 4], out1[LW / 4];
-#pragma unroll
-        for (int j = 0; j < LW / 4; ++j) {
-          const float g0 = round_bf16(total[mi][4 * j][i]);
-          const float g1 = round_bf16(total[mi][4 * j + 1][i]);
-          const float u0 = round_bf16(total[mi][4 * j + 2][i]);
-          const float u1 = round_bf16(total[mi][4 * j + 3][i]);
-          if constexpr (EPI == EPI_SWIGLU) {
-            out0[j] = pack_bf16x2(round_bf16(silu_f32(g0)) * u0, round_bf16(silu_f32(g1)) * u1);
-          } else {
-            out0[j] = pack_bf16x2(g0, g1);
-            out1[j] = pack_bf16x2(u0, u1);
-          }
-        }
-        const size_t off = (size_t)m * p.ldy + (ncol >> 1);
-        if constexpr (LW == 8) {
-          *reinterpret_cast<u32x2*>(p.y0 + off) = u32x2{out0[0], out0[1]};
-          if constexpr (EPI == EPI_PAIRED) *reinterpret_cast<u32x2*>(p.y1 + off) = u32x2{out1[0], out1[1]};
-        } else {
-          *reinterpret_cast<uint32_t*>(p.y0 + off) = out0[0];
-          if constexpr (EPI == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = out1[0];
-        }
-      }
-    }
+  epilogue<MT, LW>(p, ncol, r, mbase, total);
 }
 
 __global__ void dequant_f32_kernel(const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
@@ -346,53 +335,83 @@ using namespace t2i;
 using t2i_host::aligned16;
 using t2i_host::fail;
 
+// Compiled tile configurations: (MT m-tiles, LW words per lane, W waves, CK k-steps per chunk).
+// Row tiles beyond 16 rows go to grid.z (measured faster than multi-tile waves
+// on every Qwen3 shape at M = 32 and 64).
+#define T2I_LINEAR_CONFIGS(X) \
+  X(1, 1, 16, 4)              \
+  X(1, 2, 16, 4)              \
+  X(1, 2, 8, 4)               \
+  X(1, 4, 16, 2)              \
+  X(1, 4, 8, 4)               \
+  X(1, 4, 4, 4)               \
+  X(1, 8, 4, 4)
+
 struct Plan {
-  int MT, LW, cbs, gpw, splits;
-  size_t ws_bytes;
+  int MT, LW, W, CK;
+  int mz;       // row tiles of 16*MT rows (grid.z)
+  int cbs;      // column blocks (grid.x)
+  int chunks;   // K / (32 * CK)
 };
 
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+bool config_exists(int MT, int LW, int W, int CK) {
+#define T2I_MATCH(a, b, c, d) if (MT == a && LW == b && W == c && CK == d) return true;
+  T2I_LINEAR_CONFIGS(T2I_MATCH)
+#undef T2I_MATCH
+  return false;
+}
 
-// Tile / split choice.  Column blocks of 16*LW columns; each workgroup's four
-// waves take consecutive groups of K; `splits` workgroups share a column block
-// when there are too few column blocks to give every CU work.
-Plan plan_linear(int M, int K, int N, bool need_lw8_or_4) {
-  (void)need_lw8_or_4;
-  Plan pl{};
-  pl.MT = (M + 15) / 16;
-  if (pl.MT == 3) pl.MT = 4;
-  pl.LW = (pl.MT == 1 && N % 128 == 0) ? 8 : 4;
+void finish_plan(Plan& pl, int M, int K, int N) {
+  pl.mz = (M + 16 * pl.MT - 1) / (16 * pl.MT);
   pl.cbs = N / (16 * pl.LW);
-  const int G = K / GS;
-  const int target_wgs = 512;
-  int max_splits = (G + WAVES - 1) / WAVES;
-  int splits = (target_wgs + pl.cbs - 1) / pl.cbs;
-  if (splits > max_splits) splits = max_splits;
-  if (splits < 1) splits = 1;
-  int gpw = (G + splits * WAVES - 1) / (splits * WAVES);
-  splits = (G + gpw * WAVES - 1) / (gpw * WAVES);
-  pl.gpw = gpw;
-  pl.splits = splits;
-  pl.ws_bytes = splits > 1 ? align256((size_t)pl.cbs * 4) + (size_t)splits * M * N * 4 : 0;
+  pl.chunks = K / (32 * pl.CK);
+}
+
+// Tile choice, from an HBM-cold sweep over the Qwen3-0.6B/1.7B linear shapes
+// at M in {1, 8, 16, 32, 64}: one 16-row tile per workgroup (more rows go to
+// grid.z and share the weights through L2), and column blocks sized so that
+// the column-tile x row-tile count gives a few hundred workgroups.  Splitting
+// K across workgroups (fp32 partials + an arrival counter) was measured
+// slower at every one of these shapes: its extra memory round trips cost more
+// than the parallelism it adds, so K is only split between the waves of a
+// workgroup.
+Plan plan_linear(int M, int K, int N, bool paired) {
+  Plan pl{};
+  pl.MT = 1;
+  pl.CK = 4;
+  const int mz = (M + 15) / 16;
+  if (((N / 16) * mz <= 256 || N % 32) && !paired) {
+    pl.LW = 1; pl.W = 16;
+  } else if ((N / 32) * mz <= (mz >= 4 ? 384 : 768) || N % 64) {
+    pl.LW = 2; pl.W = 8;
+  } else {
+    pl.LW = 4; pl.W = 8;
+  }
+#ifdef T2I_TUNING
+  // tuning builds only: T2I_PLAN="MT,LW,W,CK" overrides the choice
+  if (const char* env = getenv("T2I_PLAN")) {
+    Plan o = pl;
+    if (sscanf(env, "%d,%d,%d,%d", &o.MT, &o.LW, &o.W, &o.CK) == 4 && config_exists(o.MT, o.LW, o.W, o.CK) &&
+        N % (16 * o.LW) == 0 && (!paired || o.LW >= 2))
+      pl = o;
+  }
+#endif
+  finish_plan(pl, M, K, N);
   return pl;
 }
 
-template <int MT, int LW, int EPI>
+template <int MT, int LW, int W, int CK>
 hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, EPI>), grid, dim3(64 * WAVES), 0, s, p);
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK>), grid, dim3(64 * W), 0, s, p);
   return hipGetLastError();
 }
 
-template <int EPI>
-hipError_t launch_epi(const Plan& pl, const LinearParams& p, hipStream_t s) {
-  dim3 grid(pl.cbs, pl.splits);
-  if (pl.LW == 8) {
-    if (pl.MT == 1) return launch_t<1, 8, EPI>(p, grid, s);
-  } else {
-    if (pl.MT == 1) return launch_t<1, 4, EPI>(p, grid, s);
-    if (pl.MT == 2) return launch_t<2, 4, EPI>(p, grid, s);
-    if (pl.MT == 4) return launch_t<4, 4, EPI>(p, grid, s);
-  }
+hipError_t launch_plan(const Plan& pl, const LinearParams& p, hipStream_t s) {
+  const dim3 grid(pl.cbs, 1, pl.mz);
+#define T2I_LAUNCH(a, b, c, d) \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_t<a, b, c, d>(p, grid, s);
+  T2I_LINEAR_CONFIGS(T2I_LAUNCH)
+#undef T2I_LAUNCH
   return hipErrorInvalidValue;
 }
 
@@ -409,7 +428,7 @@ int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
 
 int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const int32_t* qzeros,
                const uint16_t* scales, int K, int N, int group_size, const uint16_t* residual,
-               uint16_t* y0, uint16_t* y1, void* ws, size_t ws_bytes, void* stream) {
+               uint16_t* y0, uint16_t* y1, void* stream) {
   int rc = check_weights(qweight, qzeros, scales, K, N, group_size);
   if (rc) return rc;
   if (!x || !y0) return fail(T2I_ERR_NULL, "x and y must not be NULL");
@@ -418,14 +437,8 @@ int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const 
   if (M < 1 || M > 64) return fail(T2I_ERR_SHAPE, "M=%d must be in [1, 64]", M);
   if (!aligned16(x) || !aligned16(y0) || (y1 && !aligned16(y1)) || (residual && !aligned16(residual)))
     return fail(T2I_ERR_ALIGN, "activation pointers must be 16-byte aligned");
-  if ((epi == EPI_SWIGLU || epi == EPI_PAIRED) && N % 128)
-    return fail(T2I_ERR_SHAPE, "gate/up N=%d must be a multiple of 128", N);
-  const Plan pl = plan_linear(M, K, N, false);
-  if (pl.ws_bytes) {
-    if (!ws) return fail(T2I_ERR_WORKSPACE, "workspace of %zu bytes required", pl.ws_bytes);
-    if (ws_bytes < pl.ws_bytes) return fail(T2I_ERR_WORKSPACE, "workspace %zu < required %zu", ws_bytes, pl.ws_bytes);
-    if (!aligned16(ws)) return fail(T2I_ERR_ALIGN, "workspace must be 16-byte aligned");
-  }
+  const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
+  const Plan pl = plan_linear(M, K, N, paired);
   LinearParams p{};
   p.x = x;
   p.qw = reinterpret_cast<const uint32_t*>(qweight);
@@ -434,52 +447,30 @@ int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const 
   p.residual = residual;
   p.y0 = y0;
   p.y1 = y1;
-  p.counters = reinterpret_cast<uint32_t*>(ws);
-  p.partial = ws ? reinterpret_cast<float*>(reinterpret_cast<char*>(ws) + align256((size_t)pl.cbs * 4)) : nullptr;
   p.M = M; p.K = K; p.N = N;
   p.ldx = K;
-  p.ldy = (epi == EPI_SWIGLU || epi == EPI_PAIRED) ? N / 2 : N;
-  p.n_groups = K / GS;
-  p.gpw = pl.gpw;
-  p.splits = pl.splits;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
-  switch (epi) {
-    case EPI_STORE: e = launch_epi<EPI_STORE>(pl, p, s); break;
-    case EPI_RESIDUAL: e = launch_epi<EPI_RESIDUAL>(pl, p, s); break;
-    case EPI_SWIGLU: e = launch_epi<EPI_SWIGLU>(pl, p, s); break;
-    default: e = launch_epi<EPI_PAIRED>(pl, p, s); break;
-  }
-  return t2i_host::hip_status(e, "w4a16 linear launch");
+  p.ldy = paired ? N / 2 : N;
+  p.chunks = pl.chunks;
+  p.epi = epi;
+  return t2i_host::hip_status(launch_plan(pl, p, reinterpret_cast<hipStream_t>(stream)), "w4a16 linear launch");
 }
 
 }  // namespace
 
-extern "C" size_t t2i_w4a16_linear_workspace_bytes(int32_t M, int32_t K, int32_t N) {
-  if (M < 1 || M > 64 || K <= 0 || K % GS || N <= 0 || N % 64) return 0;
-  return plan_linear(M, K, N, false).ws_bytes;
-}
-
-extern "C" size_t t2i_w4a16_gate_up_workspace_bytes(int32_t M, int32_t K, int32_t N) {
-  return t2i_w4a16_linear_workspace_bytes(M, K, N);
-}
-
 extern "C" int t2i_w4a16_linear(const uint16_t* x, int32_t M, const int32_t* qweight,
                                 const int32_t* qzeros, const uint16_t* scales, int32_t K,
                                 int32_t N, int32_t group_size, const uint16_t* residual,
-                                uint16_t* y, void* workspace, size_t workspace_bytes,
-                                void* stream) {
+                                uint16_t* y, void* stream) {
   return run_linear(residual ? EPI_RESIDUAL : EPI_STORE, x, M, qweight, qzeros, scales, K, N,
-                    group_size, residual, y, nullptr, workspace, workspace_bytes, stream);
+                    group_size, residual, y, nullptr, stream);
 }
 
 extern "C" int t2i_w4a16_gate_up(const uint16_t* x, int32_t M, const int32_t* qweight,
                                  const int32_t* qzeros, const uint16_t* scales, int32_t K,
                                  int32_t N, int32_t group_size, int32_t swiglu, uint16_t* y0,
-                                 uint16_t* y1, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
+                                 uint16_t* y1, void* stream) {
   return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, qweight, qzeros, scales, K, N,
-                    group_size, nullptr, y0, y1, workspace, workspace_bytes, stream);
+                    group_size, nullptr, y0, y1, stream);
 }
 
 extern "C" int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,

@@ -6,11 +6,11 @@ three device tensors.  The only offline repacks are column permutations done
 at the nibble level, which are exact:
 
 * ``concat_columns`` fuses q|k|v into one ``N = (Hq + 2 Hkv) * D`` linear;
-* ``interleave_gate_up`` fuses gate|up into one linear whose column ``4i + e``
-  is gate ``2i + e`` and column ``4i + 2 + e`` is up ``2i + e``, so a lane that
-  owns four consecutive output columns owns matching gate/up pairs (the
-  reference pairs gate and up offline the same way,
-  ``packed_format.py:360-369, 548-582``, gate = pair 0).
+* ``interleave_gate_up`` fuses gate|up into one linear whose column ``2i``
+  is gate ``i`` and column ``2i + 1`` is up ``i``, so a lane that owns two
+  consecutive output columns owns a matching gate/up pair (the reference
+  pairs gate and up offline the same way, ``packed_format.py:360-369,
+  548-582``, gate = pair 0).
 """
 
 from __future__ import annotations
@@ -116,12 +116,8 @@ def concat_columns(*parts):
 
 def gate_up_permutation(intermediate: int) -> np.ndarray:
     """Index map of the fused gate|up weight into concat(gate, up) columns."""
-    n = 2 * intermediate
-    perm = np.empty(n, dtype=np.int64)
-    f = np.arange(n)
-    blk, e = f // 4, f % 4
-    perm[:] = np.where(e < 2, 2 * blk + e, intermediate + 2 * blk + (e - 2))
-    return perm
+    f = np.arange(2 * intermediate)
+    return np.where(f % 2 == 0, f // 2, intermediate + f // 2).astype(np.int64)
 
 
 def interleave_gate_up(gate, up):
@@ -129,7 +125,28 @@ def interleave_gate_up(gate, up):
     inter = int(np.asarray(gate[0]).shape[1])
     if int(np.asarray(up[0]).shape[1]) != inter:
         raise ValueError("gate and up must have the same number of columns")
-    if inter % 64:
-        raise ValueError("intermediate size must be a multiple of 64")
+    if inter % 32:
+        raise ValueError("intermediate size must be a multiple of 32")
     cat = concat_columns(gate, up)
     return _permute_columns(*cat, gate_up_permutation(inter))
+
+
+def random_weight_on_device(K: int, N: int, generator: torch.Generator, device) -> W4A16Weight:
+    """Seeded random AutoGPTQ weight drawn directly on the device (benchmarks).
+
+    Same distributions as ``random_tensors``: uniform 32-bit words, fp16
+    scales uniform in [0.005, 0.02].
+    """
+    g = GROUP_SIZE
+    qweight = torch.randint(-2**31, 2**31, (K // 8, N), dtype=torch.int64, device=device,
+                            generator=generator).to(torch.int32)
+    qzeros = torch.randint(-2**31, 2**31, (K // g, N // 8), dtype=torch.int64, device=device,
+                           generator=generator).to(torch.int32)
+    scales = (torch.rand((K // g, N), device=device, generator=generator) * 0.015 + 0.005).to(torch.float16)
+    return W4A16Weight(qweight, qzeros, scales, g)
+
+
+def algorithmic_bytes(M: int, K: int, N: int, group_size: int = GROUP_SIZE) -> int:
+    """Bytes a W4A16 linear must move at minimum: int4 weights, fp16 scales,
+    int32 zero words, bf16 activations in and out."""
+    return K * N // 2 + (K // group_size) * N * 2 + (K // group_size) * (N // 8) * 4 + M * K * 2 + M * N * 2

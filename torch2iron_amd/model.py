@@ -1,0 +1,380 @@
+"""W4A16 Qwen3 decoder on one MI355X: the fused decode layer and batched greedy decode.
+
+Per layer and decode step (batch B, one token per sequence), seven launches:
+
+1. ``t2i_rmsnorm``           input RMSNorm (layer 0: gathers the embedding rows)
+2. ``t2i_w4a16_linear``      fused q|k|v projection (N = (Hq + 2 Hkv) * D)
+3. ``t2i_decode_attention``  q/k RMSNorm + RoPE + KV-cache write + GQA attention
+4. ``t2i_w4a16_linear``      o_proj with the residual add folded in (in place)
+5. ``t2i_rmsnorm``           post-attention RMSNorm
+6. ``t2i_w4a16_gate_up``     fused gate|up projection with the SwiGLU epilogue
+7. ``t2i_w4a16_linear``      down projection with the residual add (in place)
+
+then the final RMSNorm, the tied bf16 lm_head with the fused argmax, and the
+device-side token bookkeeping.  This is the per-layer runlist of the
+reference's NPU batch decoder (``quantized_qwen3/batch_decode_fused.py:426-539``)
+re-cut for the GPU: q/k/v are one linear, gate/up one linear with SwiGLU, and
+the RoPE, q/k-norm and KV write live in the attention prologue.
+
+A whole decode step is captured once into a HIP graph and replayed; token ids,
+positions and the output history stay on the device between steps.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from torch2iron_amd import ops
+from torch2iron_amd.formats import W4A16Weight, concat_columns, interleave_gate_up
+
+BF16 = torch.bfloat16
+
+
+@dataclass(frozen=True)
+class Qwen3Config:
+    """Shape of a Qwen3 decoder (``quantized_qwen3/model.py:330-348`` fields)."""
+
+    hidden: int = 1024
+    n_heads: int = 16
+    n_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 3072
+    n_layers: int = 28
+    vocab: int = 151936
+    eps: float = 1e-6
+    rope_theta: float = 1e6
+    group_size: int = 128
+    rope_style: str = "halves"
+
+    @property
+    def qkv_dim(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+QWEN3_0_6B = Qwen3Config()
+QWEN3_1_7B = Qwen3Config(hidden=2048, intermediate=6144)
+
+
+def _rand_words(rng, shape):
+    return rng.integers(0, 2**32, size=shape, dtype=np.uint64).astype(np.uint32).view(np.int32)
+
+
+def _centered_words(rng, shape):
+    nib = rng.integers(1, 16, size=(*shape, 8), dtype=np.uint64)
+    acc = np.zeros(shape, dtype=np.uint64)
+    for j in range(8):
+        acc |= nib[..., j] << np.uint64(4 * j)
+    return acc.astype(np.uint32).view(np.int32)
+
+
+def random_qwen3_tensors(cfg: Qwen3Config, seed: int = 0, embed_std: float = 1.0,
+                         weights: str = "uniform") -> dict:
+    """Random-init Qwen3 tensors under HF names (numpy).
+
+    Linears: AutoGPTQ group-128, fp16 scales U[0.005, 0.02].
+    ``weights="uniform"``: uniform random words (nibbles and stored zeros
+    uniform in 0..15, so ``q - z`` has mean -1).
+    ``weights="centered"``: symmetric-checkpoint style, stored zero 7 (z = 8)
+    and nibbles uniform in 1..15, so ``q - z`` is uniform in [-7, 7]; with
+    the uniform draw, the non-zero mean of every weight row makes greedy decode
+    collapse onto one token for every prompt, which leaves token parity nearly
+    vacuous.
+    RMSNorm weights U[0.9, 1.1] (bf16 values).  Embedding (also the tied
+    lm_head) N(0, embed_std) rounded to bf16.
+    """
+    if weights not in ("uniform", "centered"):
+        raise ValueError("weights must be 'uniform' or 'centered'")
+    rng = np.random.default_rng(seed)
+    g = cfg.group_size
+    t = {}
+
+    def lin(name, k, n):
+        if weights == "uniform":
+            t[f"{name}.qweight"] = _rand_words(rng, (k // 8, n))
+            t[f"{name}.qzeros"] = _rand_words(rng, (k // g, n // 8))
+        else:
+            t[f"{name}.qweight"] = _centered_words(rng, (k // 8, n))
+            t[f"{name}.qzeros"] = np.full((k // g, n // 8), 0x77777777, dtype=np.int64).astype(np.int32)
+        t[f"{name}.scales"] = rng.uniform(0.005, 0.02, size=(k // g, n)).astype(np.float16)
+
+    def bf16_values(a):
+        return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(BF16).float().numpy()
+
+    h, d = cfg.hidden, cfg.head_dim
+    for i in range(cfg.n_layers):
+        p = f"model.layers.{i}"
+        lin(f"{p}.self_attn.q_proj", h, cfg.n_heads * d)
+        lin(f"{p}.self_attn.k_proj", h, cfg.n_kv_heads * d)
+        lin(f"{p}.self_attn.v_proj", h, cfg.n_kv_heads * d)
+        lin(f"{p}.self_attn.o_proj", cfg.n_heads * d, h)
+        lin(f"{p}.mlp.gate_proj", h, cfg.intermediate)
+        lin(f"{p}.mlp.up_proj", h, cfg.intermediate)
+        lin(f"{p}.mlp.down_proj", cfg.intermediate, h)
+        t[f"{p}.input_layernorm.weight"] = bf16_values(rng.uniform(0.9, 1.1, h))
+        t[f"{p}.post_attention_layernorm.weight"] = bf16_values(rng.uniform(0.9, 1.1, h))
+        t[f"{p}.self_attn.q_norm.weight"] = bf16_values(rng.uniform(0.9, 1.1, d))
+        t[f"{p}.self_attn.k_norm.weight"] = bf16_values(rng.uniform(0.9, 1.1, d))
+    t["model.norm.weight"] = bf16_values(rng.uniform(0.9, 1.1, h))
+    emb = torch.randn(cfg.vocab, h, generator=torch.Generator().manual_seed(seed + 7)) * embed_std
+    t["model.embed_tokens.weight"] = emb.to(BF16).float().numpy()
+    return t
+
+
+def rope_table(head_dim: int, ctx: int, theta: float, device) -> torch.Tensor:
+    """bf16 ``[ctx, head_dim]``: cos at even, sin at odd columns of frequency i.
+
+    Angles as ``quantized_qwen3/model.py:351-358`` (fp32 ``inv_freq``, fp32
+    outer product), then rounded to bf16 as that runtime does in bf16 compute
+    (``model.py:421-425``).
+    """
+    inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2).float() / head_dim))
+    freqs = torch.outer(torch.arange(ctx).float(), inv_freq)
+    ang = torch.empty(ctx, head_dim)
+    ang[:, ::2] = torch.cos(freqs)
+    ang[:, 1::2] = torch.sin(freqs)
+    return ang.to(BF16).to(device)
+
+
+def _bf16_dev(a, device) -> torch.Tensor:
+    return torch.as_tensor(np.asarray(a, dtype=np.float32)).to(BF16).to(device).contiguous()
+
+
+class Qwen3LayerWeights:
+    """Device weights of one layer, fused for the GPU kernels."""
+
+    def __init__(self, tensors: dict, layer: int, cfg: Qwen3Config, device):
+        p = f"model.layers.{layer}"
+
+        def trip(name):
+            return (tensors[f"{name}.qweight"], tensors[f"{name}.qzeros"], tensors[f"{name}.scales"])
+
+        qkv = concat_columns(trip(f"{p}.self_attn.q_proj"), trip(f"{p}.self_attn.k_proj"),
+                             trip(f"{p}.self_attn.v_proj"))
+        self.qkv = W4A16Weight.from_numpy(*qkv, device=device)
+        self.o = W4A16Weight.from_numpy(*trip(f"{p}.self_attn.o_proj"), device=device)
+        self.gate_up = W4A16Weight.from_numpy(*interleave_gate_up(trip(f"{p}.mlp.gate_proj"),
+                                                                 trip(f"{p}.mlp.up_proj")), device=device)
+        self.down = W4A16Weight.from_numpy(*trip(f"{p}.mlp.down_proj"), device=device)
+        self.ln1 = _bf16_dev(tensors[f"{p}.input_layernorm.weight"], device)
+        self.ln2 = _bf16_dev(tensors[f"{p}.post_attention_layernorm.weight"], device)
+        self.q_norm = _bf16_dev(tensors[f"{p}.self_attn.q_norm.weight"], device)
+        self.k_norm = _bf16_dev(tensors[f"{p}.self_attn.k_norm.weight"], device)
+
+
+class DecodeBuffers:
+    """Activations of one decode step for a batch of B sequences (preallocated, graph-safe)."""
+
+    def __init__(self, cfg: Qwen3Config, batch: int, device):
+        h = cfg.hidden
+        self.x = torch.zeros(batch, h, dtype=BF16, device=device)        # residual stream
+        self.xn = torch.zeros(batch, h, dtype=BF16, device=device)       # normed activations
+        self.qkv = torch.zeros(batch, cfg.qkv_dim, dtype=BF16, device=device)
+        self.ctx = torch.zeros(batch, cfg.n_heads * cfg.head_dim, dtype=BF16, device=device)
+        self.hmlp = torch.zeros(batch, cfg.intermediate, dtype=BF16, device=device)
+        self.workspace = ops.Workspace()
+
+
+class Qwen3DecodeLayer:
+    """The fused decode layer: ``layer(x, positions, k_cache, v_cache)`` updates ``x`` in place.
+
+    ``x`` bf16 ``[B, hidden]`` (the residual stream), ``positions`` int32
+    ``[B]``, caches bf16 ``[B, Hkv, ctx_cap, D]``.  Mirrors the per-layer
+    sequence of the reference's fused decode runlist
+    (``batch_decode_fused.py:426-530``) and the reference layer semantics
+    (``quantized_qwen3/model.py:316-327``).
+    """
+
+    def __init__(self, weights: Qwen3LayerWeights, cfg: Qwen3Config, rope: torch.Tensor):
+        self.w = weights
+        self.cfg = cfg
+        self.rope = rope
+        self.rope_style = ops.ROPE_HALVES if cfg.rope_style == "halves" else ops.ROPE_INTERLEAVED
+
+    def attention_half(self, buf: DecodeBuffers, positions, k_cache, v_cache, normed: bool = False):
+        c, w = self.cfg, self.w
+        if not normed:
+            ops.rmsnorm(buf.x, w.ln1, c.eps, out=buf.xn)
+        ops.linear(buf.xn, w.qkv, out=buf.qkv)
+        ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, self.rope,
+                             k_cache, v_cache, rope_style=self.rope_style, out=buf.ctx, workspace=buf.workspace)
+        ops.linear(buf.ctx, w.o, residual=buf.x, out=buf.x)
+
+    def mlp_half(self, buf: DecodeBuffers):
+        c, w = self.cfg, self.w
+        ops.rmsnorm(buf.x, w.ln2, c.eps, out=buf.xn)
+        ops.gate_up(buf.xn, w.gate_up, swiglu=True, out=buf.hmlp)
+        ops.linear(buf.hmlp, w.down, residual=buf.x, out=buf.x)
+
+    def __call__(self, buf: DecodeBuffers, positions, k_cache, v_cache, normed: bool = False):
+        self.attention_half(buf, positions, k_cache, v_cache, normed)
+        self.mlp_half(buf)
+
+
+class Qwen3Model:
+    """Random-init (or given) W4A16 Qwen3 with batched greedy decode on the GPU.
+
+    Weights: AutoGPTQ linears (fused per layer), bf16 norms, bf16 tied
+    embedding/lm_head.  KV cache: bf16 ``[layers, B, Hkv, ctx_cap, D]``.
+    """
+
+    def __init__(self, tensors: dict, cfg: Qwen3Config, batch: int, ctx_cap: int, device):
+        self.cfg = cfg
+        self.batch = batch
+        self.ctx_cap = ctx_cap
+        self.device = torch.device(device)
+        self.rope = rope_table(cfg.head_dim, ctx_cap, cfg.rope_theta, self.device)
+        self.embed = _bf16_dev(tensors["model.embed_tokens.weight"], self.device)
+        self.norm = _bf16_dev(tensors["model.norm.weight"], self.device)
+        self.layers = [Qwen3DecodeLayer(Qwen3LayerWeights(tensors, i, cfg, self.device), cfg, self.rope)
+                       for i in range(cfg.n_layers)]
+        shape = (cfg.n_layers, batch, cfg.n_kv_heads, ctx_cap, cfg.head_dim)
+        self.k_cache = torch.zeros(shape, dtype=BF16, device=self.device)
+        self.v_cache = torch.zeros(shape, dtype=BF16, device=self.device)
+        self.buf = DecodeBuffers(cfg, batch, self.device)
+        self.tokens = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        self.positions = torch.zeros(batch, dtype=torch.int32, device=self.device)
+        self.keys = torch.zeros(batch, dtype=torch.int64, device=self.device)
+        self.step = torch.zeros(1, dtype=torch.int32, device=self.device)
+        self.history = None
+        self.prompt = None
+        self.logits = None
+        self._graphs = {}
+
+    # ---- one step, eager ----
+    def forward_step(self, with_head: bool = True, want_logits: bool = False):
+        """Embed ``self.tokens`` at ``self.positions``, run every layer, and (optionally)
+        the final norm + lm_head argmax into ``self.keys``."""
+        c, b = self.cfg, self.buf
+        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens, x_out=b.x)
+        for i, layer in enumerate(self.layers):
+            layer(b, self.positions, self.k_cache[i], self.v_cache[i], normed=(i == 0))
+        if with_head:
+            ops.rmsnorm(b.x, self.norm, c.eps, out=b.xn, argmax_keys=self.keys)
+            if want_logits and self.logits is None:
+                self.logits = torch.empty(self.batch, c.vocab, dtype=torch.float32, device=self.device)
+            ops.lm_head_argmax(b.xn, self.embed, self.keys, logits=self.logits if want_logits else None)
+
+    def decode_step(self, tokens, positions, want_logits: bool = False):
+        """One greedy decode step from host token ids/positions; returns ``(next_tokens, logits|None)``
+        (the ``decode_step`` contract of ``qwen_npu.py:166-236``)."""
+        tokens = torch.as_tensor(tokens, dtype=torch.int32)
+        positions = torch.as_tensor(positions, dtype=torch.int32)
+        if tokens.numel() != self.batch or positions.numel() != self.batch:
+            raise ValueError("token batch size does not match the model batch size")
+        if int(positions.max()) >= self.ctx_cap or int(positions.min()) < 0:
+            raise ValueError(f"decode position exceeds the cache capacity {self.ctx_cap}")
+        if int(tokens.min()) < 0 or int(tokens.max()) >= self.cfg.vocab:
+            raise ValueError("token id out of range")
+        self.tokens.copy_(tokens.to(self.device))
+        self.positions.copy_(positions.to(self.device))
+        self.forward_step(with_head=True, want_logits=want_logits)
+        nxt = ops.keys_to_tokens(self.keys)
+        return nxt.cpu(), (self.logits.clone() if want_logits else None)
+
+    # ---- graph-captured greedy generation ----
+    def _capture(self, kind: str):
+        if kind in self._graphs:
+            return self._graphs[kind]
+        stream = torch.cuda.Stream(self.device)
+        stream.wait_stream(torch.cuda.current_stream(self.device))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(g, stream=stream):
+                if kind == "prompt":
+                    self.forward_step(with_head=False)
+                    ops.prompt_advance(self.prompt, self.tokens, self.positions)
+                else:
+                    self.forward_step(with_head=True)
+                    ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+        torch.cuda.current_stream(self.device).wait_stream(stream)
+        self._graphs[kind] = g
+        return g
+
+    def reset(self):
+        self.k_cache.zero_()
+        self.v_cache.zero_()
+
+    def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True, timings: dict | None = None):
+        """Greedy decode as ``qwen_npu.py:309-325``: consume the prompt, then emit
+        ``new_tokens`` tokens per sequence (the first from the last prompt position).
+
+        The prompt is consumed one position at a time through the decode path
+        (teacher forcing).  Returns int64 ``[B, new_tokens]`` on the host.
+        """
+        prompt = torch.as_tensor(prompt)
+        b, plen = prompt.shape
+        if b != self.batch:
+            raise ValueError("prompt batch does not match the model batch size")
+        if plen + new_tokens - 1 > self.ctx_cap:
+            raise ValueError(f"prompt {plen} + {new_tokens} tokens exceed the cache capacity {self.ctx_cap}")
+        if int(prompt.min()) < 0 or int(prompt.max()) >= self.cfg.vocab:
+            raise ValueError("prompt token id out of range")
+        self.reset()
+        self.prompt = prompt.to(torch.int32).to(self.device).contiguous()
+        if self.history is None or self.history.shape[1] < new_tokens:
+            self.history = torch.zeros(b, new_tokens, dtype=torch.int32, device=self.device)
+        self.tokens.copy_(self.prompt[:, 0])
+        self.positions.zero_()
+        self.step.zero_()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+        if use_graph:
+            if not self._graphs:
+                # one eager step first: it allocates the attention workspace outside the capture
+                self.forward_step(with_head=True)
+                torch.cuda.synchronize(self.device)
+            g_prompt = self._capture("prompt")
+            g_decode = self._capture("decode")
+            # restore the state the replays start from
+            self.tokens.copy_(self.prompt[:, 0])
+            self.positions.zero_()
+            self.step.zero_()
+            self.reset()
+            torch.cuda.synchronize(self.device)
+            ev[0].record()
+            for _ in range(plen - 1):
+                g_prompt.replay()
+            g_decode.replay()              # last prompt position -> first new token
+            ev[1].record()
+            for _ in range(new_tokens - 1):
+                g_decode.replay()
+            ev[2].record()
+        else:
+            ev[0].record()
+            for _ in range(plen - 1):
+                self.forward_step(with_head=False)
+                ops.prompt_advance(self.prompt, self.tokens, self.positions)
+            self.forward_step(with_head=True)
+            ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+            ev[1].record()
+            for _ in range(new_tokens - 1):
+                self.forward_step(with_head=True)
+                ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+            ev[2].record()
+        torch.cuda.synchronize(self.device)
+        if timings is not None:
+            timings["prompt_ms"] = ev[0].elapsed_time(ev[1])
+            timings["decode_ms"] = ev[1].elapsed_time(ev[2])
+        return self.history[:, :new_tokens].to(torch.int64).cpu()
+
+
+def smoke_decode(device) -> None:
+    """A 2-layer Qwen3-shaped model: 8 greedy tokens on the GPU vs the CPU oracle."""
+    from oracle import qwen3 as oq
+
+    cfg = Qwen3Config(n_layers=2, vocab=4096)
+    t = random_qwen3_tensors(cfg, seed=3, weights="centered")
+    b, plen, new = 4, 8, 8
+    prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(4))
+    gpu = Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=device)
+    got = gpu.generate(prompt, new)
+    ref = oq.DenseQwen3(t, oq.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__}),
+                        mode="bf16", ctx_cap=64).generate(prompt, new)
+    match = (got == ref).all(dim=1).float().mean().item()
+    print(f"smoke: 2-layer Qwen3 greedy decode, {b} sequences x {new} tokens, "
+          f"sequences matching the oracle: {match:.2f}", flush=True)
+    if match < 0.75:
+        raise AssertionError(f"greedy tokens diverge from the oracle: gpu {got.tolist()} ref {ref.tolist()}")

@@ -74,7 +74,7 @@ def dequantize(w: W4A16Weight) -> torch.Tensor:
 
 
 def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None,
-           out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+           out: torch.Tensor | None = None) -> torch.Tensor:
     """``y = x @ W^T`` (+ residual, rounded as bf16(bf16(x W^T) + residual)).
 
     ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case), 1 <= M <= 64.
@@ -96,17 +96,15 @@ def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None
         if residual.numel() != m * w.N:
             raise ValueError(f"residual must hold {m}x{w.N} elements")
     lib = _lib.load()
-    nbytes = lib.t2i_w4a16_linear_workspace_bytes(m, w.K, w.N)
-    ws = (workspace or DEFAULT_WORKSPACE).get(("linear", m, w.K, w.N), nbytes, x.device)
     rc = lib.t2i_w4a16_linear(x2.data_ptr(), m, w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(),
                               w.K, w.N, w.group_size, _lib.ptr(residual), out.data_ptr(),
-                              _lib.ptr(ws), nbytes, _lib.stream_handle(x.device))
+                              _lib.stream_handle(x.device))
     _lib.check(rc, "t2i_w4a16_linear")
     return out.view(-1) if squeeze else out.view(m, w.N)
 
 
 def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torch.Tensor | None = None,
-            out_up: torch.Tensor | None = None, workspace: Workspace | None = None):
+            out_up: torch.Tensor | None = None):
     """Paired gate/up projection over an ``interleave_gate_up`` weight.
 
     ``swiglu=True``: returns ``h = silu(gate) * up`` bf16 ``[M, N/2]``.
@@ -126,12 +124,9 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
             out_up = torch.empty(m, inter, dtype=BF16, device=x.device)
         _check_dev("out_up", out_up, BF16)
     lib = _lib.load()
-    nbytes = lib.t2i_w4a16_gate_up_workspace_bytes(m, w_pair.K, w_pair.N)
-    ws = (workspace or DEFAULT_WORKSPACE).get(("linear", m, w_pair.K, w_pair.N), nbytes, x.device)
     rc = lib.t2i_w4a16_gate_up(x2.data_ptr(), m, w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
                                w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)),
-                               out.data_ptr(), _lib.ptr(out_up), _lib.ptr(ws), nbytes,
-                               _lib.stream_handle(x.device))
+                               out.data_ptr(), _lib.ptr(out_up), _lib.stream_handle(x.device))
     _lib.check(rc, "t2i_w4a16_gate_up")
     return out if swiglu else (out, out_up)
 
