@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true", help="only the headline sweep")
+    ap.add_argument("--skip-decode", action="store_true", help="skip the decode layer / greedy decode runs")
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--new-tokens", type=int, default=128)
+    ap.add_argument("--batch", type=int, default=16)
     return ap.parse_args()
 
 
@@ -107,6 +111,108 @@ class Sweep:
                 prev = marks[s][i]
         per_group = [t / steps for t in per_group]
         return total_ms, per_group
+
+
+def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int, batch: int):
+    """Config 3 (one fused decode layer, batch 8, 1024 cached tokens) and config 4
+    (full Qwen3-0.6B, batch 16 greedy decode) on random-init weights."""
+    import torch
+    from torch2iron_amd import model as gm
+
+    cfg = gm.QWEN3_0_6B
+    log("generating random-init Qwen3-0.6B weights (uniform AutoGPTQ words, N(0,1) bf16 embedding)")
+    tensors = gm.random_qwen3_tensors(cfg, seed=0)
+    out = {}
+
+    # ---- config 3: one decode layer, B = 8, context 1024 (write at 1024) ----
+    b3, cap3 = 8, 1088
+    rope = gm.rope_table(cfg.head_dim, cap3, cfg.rope_theta, dev)
+    layer = gm.Qwen3DecodeLayer(gm.Qwen3LayerWeights(tensors, 0, cfg, dev), cfg, rope)
+    buf = gm.DecodeBuffers(cfg, b3, dev)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    kc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+    pos = torch.full((b3,), 1024, dtype=torch.int32, device=dev)
+    x0 = torch.randn(b3, cfg.hidden, generator=gen, device=dev).to(torch.bfloat16)
+    buf.x.copy_(x0)
+    layer(buf, pos, kc, vc)                      # eager warm-up (allocates the attention workspace)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer(buf, pos, kc, vc)
+    reps = max(steps, 10) * 5
+    for _ in range(warmup):
+        buf.x.copy_(x0)
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    layer_us = e0.elapsed_time(e1) * 1e3 / reps
+    w = layer.w
+    layer_bytes = (w.qkv.nbytes + w.o.nbytes + w.gate_up.nbytes + w.down.nbytes + 4 * 2 * cfg.hidden
+                   + 2 * 2 * cfg.head_dim + b3 * cfg.n_kv_heads * 1025 * cfg.head_dim * 2 * 2
+                   + b3 * cfg.n_kv_heads * cfg.head_dim * 2 * 2 + b3 * cfg.hidden * 2 * 2)
+    out["decode_layer"] = {"workload": "one fused Qwen3-0.6B decode layer, batch 8, context 1024",
+                           "us": round(layer_us, 2), "algorithmic_bytes": layer_bytes,
+                           "TBps": round(layer_bytes / (layer_us * 1e-6) / 1e12, 4),
+                           "frac_of_8TBps": round(layer_bytes / (layer_us * 1e-6) / 8e12, 4)}
+    log(f"decode layer (B=8, ctx 1024): {layer_us:.1f} us, {out['decode_layer']['TBps']} TB/s")
+    del g, buf, layer, kc, vc
+    torch.cuda.empty_cache()
+
+    # ---- config 4: full model, batch 16, prompt 512, 128 new tokens ----
+    cap4 = prompt_len + new_tokens
+    model = gm.Qwen3Model(tensors, cfg, batch=batch, ctx_cap=cap4, device=dev)
+    prompt = torch.randint(0, cfg.vocab, (batch, prompt_len), generator=torch.Generator().manual_seed(7))
+    log(f"greedy decode: batch {batch}, prompt {prompt_len}, {new_tokens} new tokens (graph replays)")
+    model.generate(prompt[:, :8], 4)             # warm-up and capture
+    tm = {}
+    toks = model.generate(prompt, new_tokens, timings=tm)
+    dec_s = tm["decode_ms"] * 1e-3
+    e2e_s = (tm["prompt_ms"] + tm["decode_ms"]) * 1e-3
+    step_ms = tm["decode_ms"] / (new_tokens - 1)
+    out["batch_decode"] = {
+        "workload": f"random-init Qwen3-0.6B (28 layers, W4A16 g128, bf16 tied lm_head), batch {batch}, "
+                    f"prompt {prompt_len} (teacher-forced through the decode path), {new_tokens} new tokens",
+        "decode_tokens_per_s": round(batch * (new_tokens - 1) / dec_s, 1),
+        "end_to_end_tokens_per_s": round(batch * new_tokens / e2e_s, 1),
+        "ms_per_decode_step": round(step_ms, 4),
+        "prompt_ms": round(tm["prompt_ms"], 2),
+        "decode_ms": round(tm["decode_ms"], 2),
+        "first_tokens": toks[:2, :8].tolist(),
+    }
+    log(f"decode: {out['batch_decode']['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step")
+    return out, tensors, prompt, toks
+
+
+def cpu_decode_baseline(tensors, seconds: float, batch: int):
+    """The oracle (torch fp32 on the host cores) decoding a batch: a bounded sample."""
+    import torch
+    from oracle import qwen3 as oq
+    from torch2iron_amd import model as gm
+
+    cfg = gm.QWEN3_0_6B
+    ocfg = oq.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__})
+    torch.set_num_threads(os.cpu_count() or 1)
+    m = oq.DenseQwen3(tensors, ocfg, mode="fp32", ctx_cap=640)
+    prompt = torch.randint(0, cfg.vocab, (batch, 16), generator=torch.Generator().manual_seed(7))
+    logits = m.prefill(prompt)
+    pos = torch.full((batch,), 16, dtype=torch.long)
+    steps = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        nxt = torch.argmax(logits, dim=-1)
+        logits = m.decode_step(nxt, pos)
+        pos = pos + 1
+        steps += 1
+    dt = time.perf_counter() - t0
+    return {"value": round(batch * steps / dt, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{steps} batch-{batch} fp32 decode steps of the oracle after a 16-token prompt, {dt:.1f} s"}
 
 
 def cpu_baseline(seconds: float):
@@ -199,10 +305,20 @@ def main():
         del big
     torch.cuda.synchronize()
 
+    decode = None
+    tensors = None
+    if not args.skip_decode:
+        decode, tensors, _, _ = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens,
+                                             args.batch)
+        torch.cuda.synchronize()
+
     cpu = None
     if not args.skip_cpu:
         log(f"CPU baseline ({args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(args.cpu_seconds)
+        if tensors is not None:
+            log(f"CPU decode baseline ({args.cpu_seconds:.0f} s)")
+            cpu["decode"] = cpu_decode_baseline(tensors, args.cpu_seconds, args.batch)
 
     achieved_gbps = value * 1e3
     line = {
@@ -239,6 +355,7 @@ def main():
         "cpu_baseline": cpu,
         "breakdown": breakdown,
         **extra,
+        **(decode or {}),
     }
     print(json.dumps(line), flush=True)
 

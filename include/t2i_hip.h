@@ -17,12 +17,10 @@
  * W[n][k] = (q[k][n] - z[k/g][n]) * s[k/g][n].  Group size g = 128.
  * Activations are bf16 (uint16_t bit patterns), row-major, 16-byte aligned.
  *
- * Workspace: entry points that reduce across workgroups (the split-context
- * attention) take a caller-owned workspace sized by the matching
- * *_workspace_bytes() query.  It must be
- * zero-filled once before its first use; the kernels leave their counters at
- * zero again when they finish.  Calls that overlap in time (different
- * streams) must not share a workspace.
+ * Workspace: the split-context attention keeps per-split partial results in a
+ * caller-owned workspace sized by t2i_decode_attention_workspace_bytes().
+ * Every launch overwrites what it reads, so no initialisation is needed; calls
+ * that overlap in time (different streams) must not share a workspace.
  */
 #ifndef T2I_HIP_H
 #define T2I_HIP_H

@@ -49,9 +49,9 @@ def test_linear_matches_oracle(gpu, m, k, n):
     w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
     y = ops.linear(x.to(gpu), w)
     check_linear(y, ref)
-    # a second call reuses the workspace (counters must have been reset)
+    # the in-workgroup reduction has a fixed order: a second call gives the same bits
     y2 = ops.linear(x.to(gpu), w)
-    assert torch.equal(y, y2), "repeat call differs: split-K reduction is not deterministic"
+    assert torch.equal(y, y2), "repeat call differs"
 
 
 def test_gemv_vector_input(gpu):

@@ -1,8 +1,8 @@
 // Decode-layer kernels around the W4A16 linears, for gfx950:
 //   * weighted RMSNorm (optionally gathering rows from the embedding table);
 //   * GQA decode attention with q/k RMSNorm, RoPE and the KV-cache write of the
-//     current token folded into its prologue (split over the context, combined
-//     by the last workgroup to finish);
+//     current token folded into its prologue (split over the context, the
+//     splits combined by a second small launch);
 //   * the tied bf16 lm_head on MFMA with a fused greedy argmax;
 //   * device-side greedy / prompt bookkeeping so a decode step can be replayed
 //     from a captured graph without host work.
@@ -86,8 +86,8 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
 // ============================================================================
 constexpr int ATT_D = 128;
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_MAX_CHUNK = 256;
-constexpr int ATT_TOK_PER_ITER = 16;   // 4 waves x 4 row groups of 16 lanes
+constexpr int ATT_CHUNK = 128;                 // context slots per workgroup
+constexpr int ATT_ROWS = ATT_CHUNK / 16;       // slots per lane: 4 waves x 4 rows of 16 lanes per pass
 
 struct AttnParams {
   const uint16_t* qkv;
@@ -98,9 +98,8 @@ struct AttnParams {
   uint16_t* kc;
   uint16_t* vc;
   uint16_t* out;
-  float* part_o;        // [B*Hkv][S][Q][D]
-  float* part_ml;       // [B*Hkv][S][Q][2]
-  uint32_t* counters;   // [B*Hkv]
+  float* part_o;        // [B*Hkv][S][Q][D]  unnormalised context of each split
+  float* part_ml;       // [B*Hkv][S][Q][2]  (running max, sum of exponentials) of each split
   int Hq, Hkv, ctx_cap, chunk, splits, style;
   float eps, scale;
 };
@@ -123,10 +122,9 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
 
   __shared__ float s_q[Q][D];
   __shared__ __align__(16) uint16_t s_kv[2][D];   // current k (after norm + RoPE) and v
-  __shared__ float s_p[Q][ATT_MAX_CHUNK];  // scores, then exp(score - max)
+  __shared__ float s_p[Q][ATT_CHUNK];      // scores, then exp(score - max)
   __shared__ float s_red[4][Q][D];
   __shared__ float s_stat[Q][2];
-  __shared__ uint32_t s_prev;
 
   // a position outside the cache attends to nothing and writes nothing (zero output)
   const int pos_raw = p.pos[b];
@@ -139,6 +137,22 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
   const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.ctx_cap * D;
 
   if (t0 < t1) {
+    const int c = lane & 15;    // 8 dims 8c .. 8c+7 of a slot
+    const int rg = lane >> 4;   // slot row within the wave
+    // The chunk's K and V rows do not depend on the prologue: issue all of them
+    // first so the whole chunk is in flight while q/k are normalised and rotated.
+    u32x4 kreg[ATT_ROWS], vreg[ATT_ROWS];
+#pragma unroll
+    for (int it = 0; it < ATT_ROWS; ++it) {
+      const int t = t0 + it * 16 + wave * 4 + rg;
+      if (t < t1 && t != pos) {
+        kreg[it] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)t * D + 8 * c);
+        vreg[it] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)t * D + 8 * c);
+      } else {
+        kreg[it] = vreg[it] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+
     // ---- prologue: q heads h*Q .. h*Q+Q-1, current k and v ----
     const int i0 = p.style == 0 ? lane : 2 * lane;        // pair (i0, i1) rotates together
     const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
@@ -179,9 +193,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     }
     __syncthreads();
 
-    // ---- scores: 16 lanes per token, 8 dims per lane ----
-    const int c = lane & 15;
-    const int rg = lane >> 4;
+    // ---- scores: 16 lanes per slot, 8 dims per lane ----
     float qf[Q][8];
 #pragma unroll
     for (int j = 0; j < Q; ++j)
@@ -189,17 +201,12 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
       for (int e = 0; e < 8; ++e) qf[j][e] = s_q[j][8 * c + e];
     const u32x4* kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0]);
     const u32x4* vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0]);
-    for (int tb = t0; tb < t1; tb += ATT_TOK_PER_ITER) {
-      const int t = tb + wave * 4 + rg;
-      float kf[8];
-      if (t < t1) {
-        const u32x4 kv = (t == pos) ? kcur[c]
-                                    : *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)t * D + 8 * c);
-        unpack8(kv, kf);
-      } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] = 0.0f;
-      }
+    for (int it = 0; it < ATT_ROWS; ++it) {
+      const int t = t0 + it * 16 + wave * 4 + rg;
+      if (t == pos) { kreg[it] = kcur[c]; vreg[it] = vcur[c]; }
+      float kf[8];
+      unpack8(kreg[it], kf);
 #pragma unroll
       for (int j = 0; j < Q; ++j) {
         float d = 0.0f;
@@ -236,13 +243,12 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     for (int j = 0; j < Q; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
-    for (int tb = t0; tb < t1; tb += ATT_TOK_PER_ITER) {
-      const int t = tb + wave * 4 + rg;
+#pragma unroll
+    for (int it = 0; it < ATT_ROWS; ++it) {
+      const int t = t0 + it * 16 + wave * 4 + rg;
       if (t < t1) {
-        const u32x4 vv = (t == pos) ? vcur[c]
-                                    : *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)t * D + 8 * c);
         float vf[8];
-        unpack8(vv, vf);
+        unpack8(vreg[it], vf);
 #pragma unroll
         for (int j = 0; j < Q; ++j) {
           const float pj = s_p[j][t - t0];
@@ -291,36 +297,37 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     for (int idx = tid; idx < Q * D; idx += ATT_THREADS)
       p.out[(size_t)b * p.Hq * D + (size_t)h * Q * D + idx] = 0;
   }
-  if (p.splits == 1) return;
+}
 
-  // ---- last workgroup of (b, h) combines the splits in split order ----
-  __threadfence();
-  __syncthreads();
-  if (tid == 0)
-    s_prev = __hip_atomic_fetch_add(&p.counters[bh], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  if (s_prev != (uint32_t)(p.splits - 1)) return;
-  __threadfence();
-  for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
+// Combine the context splits of one (sequence, kv head) in split order:
+// M = max m_s, L = sum l_s e^(m_s - M), O = sum o_s e^(m_s - M) / L.
+// A separate launch: the kernel boundary makes the partials visible, which is
+// far cheaper than a device-scope release fence in every attention workgroup.
+__global__ __launch_bounds__(ATT_THREADS) void attention_combine_kernel(const AttnParams p, int Q) {
+  constexpr int D = ATT_D;
+  const int bh = blockIdx.x;
+  const int b = bh / p.Hkv;
+  const int h = bh - b * p.Hkv;
+  for (int idx = threadIdx.x; idx < Q * D; idx += ATT_THREADS) {
     const int j = idx / D, d = idx - (idx / D) * D;
+    const float* ml = p.part_ml + ((size_t)bh * p.splits * Q + j) * 2;
     float mx = -INFINITY;
     for (int s = 0; s < p.splits; ++s) {
-      const float* ml = p.part_ml + (((size_t)bh * p.splits + s) * Q + j) * 2;
-      if (ml[1] > 0.0f) mx = fmaxf(mx, ml[0]);
+      const float* e = ml + (size_t)s * Q * 2;
+      if (e[1] > 0.0f) mx = fmaxf(mx, e[0]);
     }
     float lsum = 0.0f, o = 0.0f;
     for (int s = 0; s < p.splits; ++s) {
-      const float* ml = p.part_ml + (((size_t)bh * p.splits + s) * Q + j) * 2;
-      if (ml[1] > 0.0f) {
-        const float f = expf(ml[0] - mx);
-        lsum = fmaf(ml[1], f, lsum);
+      const float* e = ml + (size_t)s * Q * 2;
+      if (e[1] > 0.0f) {
+        const float f = expf(e[0] - mx);
+        lsum = fmaf(e[1], f, lsum);
         o = fmaf(p.part_o[(((size_t)bh * p.splits + s) * Q + j) * D + d], f, o);
       }
     }
     p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] =
         lsum > 0.0f ? (uint16_t)f32_to_bf16(o / lsum) : (uint16_t)0;
   }
-  if (tid == 0) __hip_atomic_store(&p.counters[bh], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ============================================================================
@@ -456,22 +463,17 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct AttnPlan {
   int chunk, splits;
-  size_t off_ml, off_o, bytes;
+  size_t off_o, bytes;
 };
 
 AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
   AttnPlan pl{};
-  pl.chunk = 128;
+  pl.chunk = ATT_CHUNK;
   pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
-  if (pl.splits > 64) {
-    pl.chunk = ATT_MAX_CHUNK;
-    pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
-  }
   const int Q = Hq / Hkv;
   const size_t units = (size_t)B * Hkv;
   if (pl.splits > 1) {
-    pl.off_ml = align256(units * 4);
-    pl.off_o = pl.off_ml + align256(units * pl.splits * Q * 2 * 4);
+    pl.off_o = align256(units * pl.splits * Q * 2 * 4);
     pl.bytes = pl.off_o + units * pl.splits * Q * ATT_D * 4;
   }
   return pl;
@@ -527,8 +529,7 @@ extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* position
   p.qkv = qkv; p.pos = positions; p.qn = q_norm; p.kn = k_norm; p.rope = rope;
   p.kc = k_cache; p.vc = v_cache; p.out = ctx;
   char* ws = reinterpret_cast<char*>(workspace);
-  p.counters = reinterpret_cast<uint32_t*>(ws);
-  p.part_ml = ws ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
+  p.part_ml = ws ? reinterpret_cast<float*>(ws) : nullptr;
   p.part_o = ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
   p.Hq = Hq; p.Hkv = Hkv; p.ctx_cap = ctx_cap; p.chunk = pl.chunk; p.splits = pl.splits; p.style = rope_style;
   p.eps = eps;
@@ -541,7 +542,10 @@ extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* position
     case 4: hipLaunchKernelGGL((decode_attention_kernel<4>), grid, dim3(ATT_THREADS), 0, s, p); break;
     default: hipLaunchKernelGGL((decode_attention_kernel<8>), grid, dim3(ATT_THREADS), 0, s, p); break;
   }
-  return t2i_host::hip_status(hipGetLastError(), "attention launch");
+  int rc = t2i_host::hip_status(hipGetLastError(), "attention launch");
+  if (rc || pl.splits == 1) return rc;
+  hipLaunchKernelGGL(t2i::attention_combine_kernel, dim3(B * Hkv), dim3(ATT_THREADS), 0, s, p, Q);
+  return t2i_host::hip_status(hipGetLastError(), "attention combine launch");
 }
 
 extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,

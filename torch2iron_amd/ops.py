@@ -20,12 +20,9 @@ ROPE_INTERLEAVED = 1
 
 
 class Workspace:
-    """Zero-initialised device scratch buffers keyed by (purpose, bytes).
-
-    The kernels that reduce across workgroups keep arrival counters here and
-    reset them to zero when they finish, so a buffer is zeroed only once.  A
-    buffer must not be used by two launches that overlap in time.
-    """
+    """Device scratch buffers keyed by purpose (the split-context attention's
+    per-split partial results).  A buffer must not be used by two launches
+    that overlap in time."""
 
     def __init__(self):
         self._bufs: dict = {}
