@@ -54,13 +54,14 @@ def parse():
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--streams", default="1,2", help="micro-batch stream counts to measure for batch decode")
     return ap.parse_args()
 
 
 class Sweep:
     """Graph-captured launches of one (M, shape) grid over a weight pool."""
 
-    def __init__(self, shapes, ms, pool_bytes, dev, seed):
+    def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None):
         import torch
         from torch2iron_amd import ops
         from torch2iron_amd.formats import algorithmic_bytes, random_weight_on_device
@@ -72,6 +73,8 @@ class Sweep:
         self.copies = max(1, -(-pool_bytes // per_copy)) if pool_bytes else 1
         self.weights = {name: [random_weight_on_device(k, n, gen, dev) for _ in range(self.copies)]
                         for name, k, n in shapes}
+        # launches per graph: one per weight copy (HBM-cold), or ``reps`` of the one copy (MALL-warm)
+        self.reps = reps or self.copies
         self.groups = []   # (label, M, K, N, graph, bytes, launches)
         for m in ms:
             for name, k, n in shapes:
@@ -81,10 +84,10 @@ class Sweep:
                 torch.cuda.synchronize()
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
-                    for w in self.weights[name]:
-                        ops.linear(x, w, out=y)
+                    for i in range(self.reps):
+                        ops.linear(x, self.weights[name][i % self.copies], out=y)
                 self.groups.append(dict(label=f"{name}/M{m}", M=m, K=k, N=n, graph=g, x=x, y=y,
-                                        bytes=algorithmic_bytes(m, k, n) * self.copies, launches=self.copies))
+                                        bytes=algorithmic_bytes(m, k, n) * self.reps, launches=self.reps))
         self.bytes_per_step = sum(gr["bytes"] for gr in self.groups)
         self.launches_per_step = sum(gr["launches"] for gr in self.groups)
 
@@ -113,7 +116,8 @@ class Sweep:
         return total_ms, per_group
 
 
-def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int, batch: int):
+def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int, batch: int,
+                 streams=(1, 2, 4)):
     """Config 3 (one fused decode layer, batch 8, 1024 cached tokens) and config 4
     (full Qwen3-0.6B, batch 16 greedy decode) on random-init weights."""
     import torch
@@ -168,24 +172,40 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     cap4 = prompt_len + new_tokens
     model = gm.Qwen3Model(tensors, cfg, batch=batch, ctx_cap=cap4, device=dev)
     prompt = torch.randint(0, cfg.vocab, (batch, prompt_len), generator=torch.Generator().manual_seed(7))
-    log(f"greedy decode: batch {batch}, prompt {prompt_len}, {new_tokens} new tokens (graph replays)")
-    model.generate(prompt[:, :8], 4)             # warm-up and capture
-    tm = {}
-    toks = model.generate(prompt, new_tokens, timings=tm)
-    dec_s = tm["decode_ms"] * 1e-3
-    e2e_s = (tm["prompt_ms"] + tm["decode_ms"]) * 1e-3
-    step_ms = tm["decode_ms"] / (new_tokens - 1)
+    runs = {}
+    toks = None
+    for s in streams:
+        model.set_streams(s)
+        log(f"greedy decode: batch {batch}, prompt {prompt_len}, {new_tokens} new tokens, "
+            f"{model.n_streams} micro-batch stream(s) (graph replays)")
+        model.generate(prompt[:, :8], new_tokens)     # warm-up and capture
+        tm = {}
+        got = model.generate(prompt, new_tokens, timings=tm)
+        if toks is None:
+            toks = got
+        dec_s = tm["decode_ms"] * 1e-3
+        e2e_s = (tm["prompt_ms"] + tm["decode_ms"]) * 1e-3
+        step_ms = tm["decode_ms"] / (new_tokens - 1)
+        runs[s] = {
+            "streams": model.n_streams,
+            "decode_tokens_per_s": round(batch * (new_tokens - 1) / dec_s, 1),
+            "end_to_end_tokens_per_s": round(batch * new_tokens / e2e_s, 1),
+            "ms_per_decode_step": round(step_ms, 4),
+            "prompt_ms": round(tm["prompt_ms"], 2),
+            "decode_ms": round(tm["decode_ms"], 2),
+            "tokens_equal_to_first_run": bool(torch.equal(got, toks)),
+        }
+        log(f"decode ({model.n_streams} streams): {runs[s]['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step")
+    best = max(runs.values(), key=lambda r: r["decode_tokens_per_s"])
     out["batch_decode"] = {
         "workload": f"random-init Qwen3-0.6B (28 layers, W4A16 g128, bf16 tied lm_head), batch {batch}, "
                     f"prompt {prompt_len} (teacher-forced through the decode path), {new_tokens} new tokens",
-        "decode_tokens_per_s": round(batch * (new_tokens - 1) / dec_s, 1),
-        "end_to_end_tokens_per_s": round(batch * new_tokens / e2e_s, 1),
-        "ms_per_decode_step": round(step_ms, 4),
-        "prompt_ms": round(tm["prompt_ms"], 2),
-        "decode_ms": round(tm["decode_ms"], 2),
+        **best,
+        "by_streams": {str(k): v for k, v in runs.items()},
         "first_tokens": toks[:2, :8].tolist(),
     }
-    log(f"decode: {out['batch_decode']['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step")
+    del model
+    torch.cuda.empty_cache()
     return out, tensors, prompt, toks
 
 
@@ -292,7 +312,7 @@ def main():
     extra = {}
     if not args.skip_extra:
         log("MALL-warm sweep (one weight copy)")
-        warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2)
+        warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2, reps=cold.copies)
         w_ms, _ = warm.run(args.steps, args.warmup)
         extra["mall_warm_TBps"] = round(warm.bytes_per_step / (w_ms / args.steps * 1e-3) / 1e12, 4)
         del warm
@@ -309,7 +329,7 @@ def main():
     tensors = None
     if not args.skip_decode:
         decode, tensors, _, _ = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens,
-                                             args.batch)
+                                             args.batch, [int(v) for v in args.streams.split(",")])
         torch.cuda.synchronize()
 
     cpu = None

@@ -89,3 +89,15 @@ def test_workspace_sizes_are_consistent():
     lib = _lib.load()
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) > 0
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0
+
+
+def test_split_batch_covers_rows():
+    from torch2iron_amd.model import split_batch
+    for batch in (1, 3, 8, 16, 17):
+        for parts in (1, 2, 3, 4, 32):
+            r = split_batch(batch, parts)
+            assert r[0][0] == 0 and r[-1][1] == batch
+            assert all(a1 == b0 for (_, a1), (b0, _) in zip(r, r[1:]))
+            sizes = [b1 - b0 for b0, b1 in r]
+            assert min(sizes) >= 1 and max(sizes) - min(sizes) <= 1
+            assert len(r) == min(parts, batch)

@@ -166,12 +166,18 @@ class Qwen3LayerWeights:
 
 
 class DecodeBuffers:
-    """Activations of one decode step for a batch of B sequences (preallocated, graph-safe)."""
+    """Activations of one decode step for a batch of B sequences (preallocated, graph-safe).
 
-    def __init__(self, cfg: Qwen3Config, batch: int, device):
+    ``x`` / ``xn`` may be given as row slices of larger tensors, so several
+    micro-batches can write their residual streams into one ``[B, hidden]``
+    tensor that the lm_head then reads in one pass.
+    """
+
+    def __init__(self, cfg: Qwen3Config, batch: int, device, x: torch.Tensor | None = None,
+                 xn: torch.Tensor | None = None):
         h = cfg.hidden
-        self.x = torch.zeros(batch, h, dtype=BF16, device=device)        # residual stream
-        self.xn = torch.zeros(batch, h, dtype=BF16, device=device)       # normed activations
+        self.x = torch.zeros(batch, h, dtype=BF16, device=device) if x is None else x      # residual stream
+        self.xn = torch.zeros(batch, h, dtype=BF16, device=device) if xn is None else xn   # normed activations
         self.qkv = torch.zeros(batch, cfg.qkv_dim, dtype=BF16, device=device)
         self.ctx = torch.zeros(batch, cfg.n_heads * cfg.head_dim, dtype=BF16, device=device)
         self.hmlp = torch.zeros(batch, cfg.intermediate, dtype=BF16, device=device)
@@ -214,14 +220,46 @@ class Qwen3DecodeLayer:
         self.mlp_half(buf)
 
 
+class _Micro:
+    """One micro-batch: rows ``b0:b1`` of the batch, its stream, buffers and graphs."""
+
+    def __init__(self, b0: int, b1: int, buf: DecodeBuffers, stream):
+        self.b0, self.b1 = b0, b1
+        self.buf = buf
+        self.stream = stream
+        self.done = torch.cuda.Event()
+        self.graphs: dict = {}
+
+
+def split_batch(batch: int, parts: int) -> list[tuple[int, int]]:
+    """Contiguous, nearly equal row ranges covering ``range(batch)``."""
+    parts = max(1, min(parts, batch))
+    base, extra = divmod(batch, parts)
+    out, b0 = [], 0
+    for i in range(parts):
+        b1 = b0 + base + (1 if i < extra else 0)
+        out.append((b0, b1))
+        b0 = b1
+    return out
+
+
 class Qwen3Model:
     """Random-init (or given) W4A16 Qwen3 with batched greedy decode on the GPU.
 
     Weights: AutoGPTQ linears (fused per layer), bf16 norms, bf16 tied
     embedding/lm_head.  KV cache: bf16 ``[layers, B, Hkv, ctx_cap, D]``.
+
+    The batch is split into ``streams`` micro-batches of contiguous rows.  Each
+    runs its 28-layer step on its own HIP stream (its own activations,
+    attention workspace and KV-cache rows), so the fixed start/finish cost of
+    one micro-batch's small launches overlaps with another's work on the other
+    hardware queues.  The streams join once per step for the final RMSNorm and
+    the tied lm_head with its argmax, which read the embedding table once for
+    the whole batch.  Sequences never interact, so the tokens do not depend on
+    the split.
     """
 
-    def __init__(self, tensors: dict, cfg: Qwen3Config, batch: int, ctx_cap: int, device):
+    def __init__(self, tensors: dict, cfg: Qwen3Config, batch: int, ctx_cap: int, device, streams: int = 1):
         self.cfg = cfg
         self.batch = batch
         self.ctx_cap = ctx_cap
@@ -234,7 +272,9 @@ class Qwen3Model:
         shape = (cfg.n_layers, batch, cfg.n_kv_heads, ctx_cap, cfg.head_dim)
         self.k_cache = torch.zeros(shape, dtype=BF16, device=self.device)
         self.v_cache = torch.zeros(shape, dtype=BF16, device=self.device)
-        self.buf = DecodeBuffers(cfg, batch, self.device)
+        self.x = torch.zeros(batch, cfg.hidden, dtype=BF16, device=self.device)
+        self.xn = torch.zeros(batch, cfg.hidden, dtype=BF16, device=self.device)
+        self.set_streams(streams)
         self.tokens = torch.zeros(batch, dtype=torch.int32, device=self.device)
         self.positions = torch.zeros(batch, dtype=torch.int32, device=self.device)
         self.keys = torch.zeros(batch, dtype=torch.int64, device=self.device)
@@ -242,21 +282,63 @@ class Qwen3Model:
         self.history = None
         self.prompt = None
         self.logits = None
-        self._graphs = {}
+
+    def set_streams(self, streams: int) -> None:
+        """Split the batch into ``streams`` micro-batches (drops captured graphs)."""
+        if streams < 1:
+            raise ValueError("streams must be at least 1")
+        self.micro = []
+        for b0, b1 in split_batch(self.batch, streams):
+            buf = DecodeBuffers(self.cfg, b1 - b0, self.device, x=self.x[b0:b1], xn=self.xn[b0:b1])
+            stream = torch.cuda.Stream(self.device) if streams > 1 else None
+            self.micro.append(_Micro(b0, b1, buf, stream))
+        self._head_graph = None
+        self._captured = False
+
+    @property
+    def n_streams(self) -> int:
+        return len(self.micro)
+
+    # ---- the pieces of one step ----
+    def _micro_layers(self, m: _Micro):
+        """Embedding gather + every layer for the rows of one micro-batch."""
+        c, b = self.cfg, m.buf
+        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens[m.b0:m.b1], x_out=b.x)
+        pos = self.positions[m.b0:m.b1]
+        for i, layer in enumerate(self.layers):
+            layer(b, pos, self.k_cache[i, m.b0:m.b1], self.v_cache[i, m.b0:m.b1], normed=(i == 0))
+
+    def _micro_prompt_advance(self, m: _Micro):
+        ops.prompt_advance(self.prompt[m.b0:m.b1], self.tokens[m.b0:m.b1], self.positions[m.b0:m.b1])
+
+    def _head(self, want_logits: bool = False):
+        """Final RMSNorm of the whole batch and the tied lm_head with the fused argmax."""
+        c = self.cfg
+        ops.rmsnorm(self.x, self.norm, c.eps, out=self.xn, argmax_keys=self.keys)
+        if want_logits and self.logits is None:
+            self.logits = torch.empty(self.batch, c.vocab, dtype=torch.float32, device=self.device)
+        ops.lm_head_argmax(self.xn, self.embed, self.keys, logits=self.logits if want_logits else None)
+
+    def _fork(self, fn):
+        """Run ``fn(m)`` for every micro-batch on its stream, joined back to the current stream."""
+        if self.n_streams == 1:
+            fn(self.micro[0])
+            return
+        main = torch.cuda.current_stream(self.device)
+        for m in self.micro:
+            m.stream.wait_stream(main)
+            with torch.cuda.stream(m.stream):
+                fn(m)
+        for m in self.micro:
+            main.wait_stream(m.stream)
 
     # ---- one step, eager ----
     def forward_step(self, with_head: bool = True, want_logits: bool = False):
         """Embed ``self.tokens`` at ``self.positions``, run every layer, and (optionally)
         the final norm + lm_head argmax into ``self.keys``."""
-        c, b = self.cfg, self.buf
-        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens, x_out=b.x)
-        for i, layer in enumerate(self.layers):
-            layer(b, self.positions, self.k_cache[i], self.v_cache[i], normed=(i == 0))
+        self._fork(self._micro_layers)
         if with_head:
-            ops.rmsnorm(b.x, self.norm, c.eps, out=b.xn, argmax_keys=self.keys)
-            if want_logits and self.logits is None:
-                self.logits = torch.empty(self.batch, c.vocab, dtype=torch.float32, device=self.device)
-            ops.lm_head_argmax(b.xn, self.embed, self.keys, logits=self.logits if want_logits else None)
+            self._head(want_logits)
 
     def decode_step(self, tokens, positions, want_logits: bool = False):
         """One greedy decode step from host token ids/positions; returns ``(next_tokens, logits|None)``
@@ -276,23 +358,50 @@ class Qwen3Model:
         return nxt.cpu(), (self.logits.clone() if want_logits else None)
 
     # ---- graph-captured greedy generation ----
-    def _capture(self, kind: str):
-        if kind in self._graphs:
-            return self._graphs[kind]
-        stream = torch.cuda.Stream(self.device)
+    def _capture_graph(self, stream, fn):
         stream.wait_stream(torch.cuda.current_stream(self.device))
         g = torch.cuda.CUDAGraph()
         with torch.cuda.stream(stream):
             with torch.cuda.graph(g, stream=stream):
-                if kind == "prompt":
-                    self.forward_step(with_head=False)
-                    ops.prompt_advance(self.prompt, self.tokens, self.positions)
-                else:
-                    self.forward_step(with_head=True)
-                    ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+                fn()
         torch.cuda.current_stream(self.device).wait_stream(stream)
-        self._graphs[kind] = g
         return g
+
+    def _capture(self):
+        """One graph per micro-batch and kind ("prompt": layers + prompt bookkeeping;
+        "layers": layers only) and one head graph (norm, lm_head, greedy bookkeeping).
+        Each is captured on, and replayed on, its own stream."""
+        if self._captured:
+            return
+        for m in self.micro:
+            stream = m.stream if m.stream is not None else torch.cuda.Stream(self.device)
+            m.graphs["prompt"] = self._capture_graph(stream, lambda m=m: (self._micro_layers(m),
+                                                                          self._micro_prompt_advance(m)))
+            m.graphs["layers"] = self._capture_graph(stream, lambda m=m: self._micro_layers(m))
+        self._head_stream = torch.cuda.Stream(self.device)
+
+        def head():
+            self._head()
+            ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+
+        self._head_graph = self._capture_graph(self._head_stream, head)
+        self._captured = True
+
+    def _replay(self, kind: str):
+        """Replay one step: every micro-batch's graph on its stream; for a decode step
+        the streams then join on the current stream for the head graph."""
+        main = torch.cuda.current_stream(self.device)
+        if self.n_streams == 1:
+            self.micro[0].graphs[kind].replay()
+        else:
+            for m in self.micro:
+                m.stream.wait_stream(main)
+                with torch.cuda.stream(m.stream):
+                    m.graphs[kind].replay()
+            for m in self.micro:
+                main.wait_stream(m.stream)
+        if kind == "layers":
+            self._head_graph.replay()
 
     def reset(self):
         self.k_cache.zero_()
@@ -317,17 +426,17 @@ class Qwen3Model:
         self.prompt = prompt.to(torch.int32).to(self.device).contiguous()
         if self.history is None or self.history.shape[1] < new_tokens:
             self.history = torch.zeros(b, new_tokens, dtype=torch.int32, device=self.device)
+            self._captured = False      # the head graph holds the history pointer
         self.tokens.copy_(self.prompt[:, 0])
         self.positions.zero_()
         self.step.zero_()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
         if use_graph:
-            if not self._graphs:
-                # one eager step first: it allocates the attention workspace outside the capture
+            if not self._captured:
+                # one eager step first: it allocates the attention workspaces outside the capture
                 self.forward_step(with_head=True)
                 torch.cuda.synchronize(self.device)
-            g_prompt = self._capture("prompt")
-            g_decode = self._capture("decode")
+                self._capture()
             # restore the state the replays start from
             self.tokens.copy_(self.prompt[:, 0])
             self.positions.zero_()
@@ -336,17 +445,16 @@ class Qwen3Model:
             torch.cuda.synchronize(self.device)
             ev[0].record()
             for _ in range(plen - 1):
-                g_prompt.replay()
-            g_decode.replay()              # last prompt position -> first new token
+                self._replay("prompt")
+            self._replay("layers")          # last prompt position -> first new token
             ev[1].record()
             for _ in range(new_tokens - 1):
-                g_decode.replay()
+                self._replay("layers")
             ev[2].record()
         else:
             ev[0].record()
             for _ in range(plen - 1):
-                self.forward_step(with_head=False)
-                ops.prompt_advance(self.prompt, self.tokens, self.positions)
+                self._fork(lambda m: (self._micro_layers(m), self._micro_prompt_advance(m)))
             self.forward_step(with_head=True)
             ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
             ev[1].record()
