@@ -17,10 +17,12 @@
  * W[n][k] = (q[k][n] - z[k/g][n]) * s[k/g][n].  Group size g = 128.
  * Activations are bf16 (uint16_t bit patterns), row-major, 16-byte aligned.
  *
- * Workspace: the split-context attention keeps per-split partial results in a
- * caller-owned workspace sized by t2i_decode_attention_workspace_bytes().
- * Every launch overwrites what it reads, so no initialisation is needed; calls
- * that overlap in time (different streams) must not share a workspace.
+ * Workspace: the split-context attention keeps per-split partial results and
+ * one arrival counter per (sequence, kv head) in a caller-owned workspace sized
+ * by t2i_decode_attention_workspace_bytes().  The workspace must be zero-filled
+ * before its first use; every call leaves the counters at zero again, so a
+ * captured graph can replay the call without a memset.  Calls that overlap in
+ * time (different streams) must not share a workspace.
  */
 #ifndef T2I_HIP_H
 #define T2I_HIP_H
@@ -32,7 +34,7 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 1
+#define T2I_ABI_VERSION 2
 
 #define T2I_OK 0
 #define T2I_ERR_NULL (-1)      /* a required pointer is NULL */

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.t2i_abi_version() == 1
+    assert lib.t2i_abi_version() == 2
     assert lib.t2i_strerror(-2) == b"unsupported shape"
 
 
@@ -70,7 +70,11 @@ def test_other_entry_points_validate():
     args[3] = 12                                                             # 12 q heads over 8 kv heads
     assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_SHAPE
     args[3] = 16
+    args[2], args[13] = 2, 4096                                              # 2 sequences, 4096 slots: split
+    assert lib.t2i_decode_attention_workspace_bytes(2, 16, 8, 4096) > 0
     assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_WORKSPACE        # split context needs workspace
+    args[15], args[16] = FAKE, 64
+    assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_WORKSPACE        # workspace too small
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151930, 1024, None, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151936, 1024, None, None, None) == _lib.T2I_ERR_NULL
     assert lib.t2i_w4a16_dequant_f32(FAKE, FAKE, FAKE, 1024, 3072, 128, None, None) == _lib.T2I_ERR_NULL
@@ -87,8 +91,15 @@ def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
 
 def test_workspace_sizes_are_consistent():
     lib = _lib.load()
-    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) > 0
+    # one workgroup per (sequence, kv head) streams the context: no workspace
+    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) == 0
+    assert lib.t2i_decode_attention_workspace_bytes(16, 16, 8, 640) == 0
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0
+    # few (sequence, kv head) pairs over a long context, or 4+ q heads per kv head: split chunks
+    n = lib.t2i_decode_attention_workspace_bytes(2, 16, 8, 4096)
+    assert n >= 2 * 8 * 4 + 2 * 8 * (4096 // 128) * 2 * (2 * 4 + 128 * 4)
+    assert lib.t2i_decode_attention_workspace_bytes(4, 16, 4, 640) > 0
+    assert lib.t2i_decode_attention_workspace_bytes(0, 16, 8, 640) == 0
 
 
 def test_split_batch_covers_rows():

@@ -1,8 +1,8 @@
 // Decode-layer kernels around the W4A16 linears, for gfx950:
 //   * weighted RMSNorm (optionally gathering rows from the embedding table);
 //   * GQA decode attention with q/k RMSNorm, RoPE and the KV-cache write of the
-//     current token folded into its prologue (split over the context, the
-//     splits combined by a second small launch);
+//     current token folded into its prologue (split over the context; the last
+//     chunk of each sequence and kv head to finish merges the chunks);
 //   * the tied bf16 lm_head on MFMA with a fused greedy argmax;
 //   * device-side greedy / prompt bookkeeping so a decode step can be replayed
 //     from a captured graph without host work.
@@ -11,6 +11,8 @@
 // (quantized_qwen3/model.py:172-196, 215-216, 322-327): every product and sum
 // that the reference rounds to bf16 is rounded here at the same point.
 #include <math.h>
+#include <stdlib.h>
+#include <string.h>
 
 #include "t2i_common.h"
 
@@ -86,8 +88,11 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
 // ============================================================================
 constexpr int ATT_D = 128;
 constexpr int ATT_THREADS = 256;
-constexpr int ATT_CHUNK = 128;                 // context slots per workgroup
-constexpr int ATT_ROWS = ATT_CHUNK / 16;       // slots per lane: 4 waves x 4 rows of 16 lanes per pass
+
+// Context slots per lane: a workgroup covers 16 * rows slots (16 groups of 16
+// lanes, one slot per group and pass).  Fewer rows for more q heads per kv
+// head keeps the per-lane score and accumulator registers bounded.
+constexpr int att_rows(int q) { return q <= 2 ? 8 : (q == 4 ? 4 : 2); }
 
 struct AttnParams {
   const uint16_t* qkv;
@@ -99,8 +104,9 @@ struct AttnParams {
   uint16_t* vc;
   uint16_t* out;
   float* part_o;        // [B*Hkv][S][Q][D]  unnormalised context of each split
-  float* part_ml;       // [B*Hkv][S][Q][2]  (running max, sum of exponentials) of each split
-  int Hq, Hkv, ctx_cap, chunk, splits, style;
+  float* part_ml;       // [B*Hkv][S][Q][2]  (max score, sum of exponentials) of each split
+  unsigned* arrivals;   // [B*Hkv]           splits finished; zero between launches
+  int Hq, Hkv, ctx_cap, splits, style;
   float eps, scale;
 };
 
@@ -109,9 +115,29 @@ __device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
   f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
 }
 
-template <int Q>
+// exp(m - M) as the weight of a softmax state with running max m under a new max M;
+// an empty state (m = -inf) weighs nothing.
+__device__ __forceinline__ float state_weight(float m, float M) { return m > -INFINITY ? expf(m - M) : 0.0f; }
+
+// One workgroup per (sequence b, kv head h, chunk of 16 * ROWS context slots).
+// A single workgroup per (b, h) streaming the whole context was measured 2-4x
+// slower at every decode shape: one CU keeps about 64 KB of loads in flight,
+// which at HBM latency is some 30 GB/s, so the context must be spread over
+// enough workgroups to occupy every CU, and the chunks' states merged.
+//   1. prologue inputs (the raw q/k/v rows of this kv head, norm gammas, RoPE row) are
+//      loaded first, then the chunk's K and V rows: loads retire in issue order, so the
+//      q/k RMSNorm + RoPE below waits only for its own inputs while K/V are in flight;
+//   2. every 16-lane group scores its slots (8 dims per lane), keeps a softmax state
+//      (max, sum, unnormalised context) in registers, and the states are merged across
+//      the wave with lane shuffles and across the waves in LDS, in a fixed order;
+//   3. with several chunks per (b, h), each chunk stores its state agent-coherently and
+//      the last chunk to arrive merges all of them in chunk order (deterministic) and
+//      writes the bf16 context; it also resets the arrival counter for the next launch.
+template <int Q, int ROWS>
 __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const AttnParams p) {
   constexpr int D = ATT_D;
+  constexpr int CHUNK = 16 * ROWS;
+  constexpr int NV = (Q + 2 + 3) / 4;   // prologue vectors (q heads, k, v) per wave
   const int bh = blockIdx.x;
   const int b = bh / p.Hkv;
   const int h = bh - b * p.Hkv;
@@ -119,32 +145,55 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
+  const int c = lane & 15;              // dims 8c .. 8c+7 of a slot
+  const int rg = lane >> 4;
+  const int grp = wave * 4 + rg;        // slot group 0..15
 
   __shared__ float s_q[Q][D];
   __shared__ __align__(16) uint16_t s_kv[2][D];   // current k (after norm + RoPE) and v
-  __shared__ float s_p[Q][ATT_CHUNK];      // scores, then exp(score - max)
-  __shared__ float s_red[4][Q][D];
-  __shared__ float s_stat[Q][2];
+  __shared__ float s_wm[4][Q], s_wl[4][Q];
+  __shared__ float s_wacc[4][Q][D];
+  __shared__ int s_last;
 
   // a position outside the cache attends to nothing and writes nothing (zero output)
   const int pos_raw = p.pos[b];
   const bool valid = pos_raw >= 0 && pos_raw < p.ctx_cap;
   const int pos = valid ? pos_raw : 0;
   const int L = valid ? pos + 1 : 0;
-  const int t0 = split * p.chunk;
-  const int t1 = min(t0 + p.chunk, L);
+  const int t0 = split * CHUNK;
+  const int t1 = min(t0 + CHUNK, L);
   const size_t qkv_row = (size_t)b * (p.Hq + 2 * p.Hkv) * D;
   const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.ctx_cap * D;
+  const size_t part = (size_t)bh * p.splits + split;
 
   if (t0 < t1) {
-    const int c = lane & 15;    // 8 dims 8c .. 8c+7 of a slot
-    const int rg = lane >> 4;   // slot row within the wave
-    // The chunk's K and V rows do not depend on the prologue: issue all of them
-    // first so the whole chunk is in flight while q/k are normalised and rotated.
-    u32x4 kreg[ATT_ROWS], vreg[ATT_ROWS];
+    // ---- 1. prologue inputs, then the chunk's K / V rows ----
+    const int i0 = p.style == 0 ? lane : 2 * lane;        // pair (i0, i1) rotates together
+    const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
+    float px0[NV], px1[NV], pg0[NV], pg1[NV];
 #pragma unroll
-    for (int it = 0; it < ATT_ROWS; ++it) {
-      const int t = t0 + it * 16 + wave * 4 + rg;
+    for (int n = 0; n < NV; ++n) {
+      const int vi = wave + 4 * n;
+      px0[n] = px1[n] = 0.0f;
+      pg0[n] = pg1[n] = 1.0f;
+      if (vi < Q + 2) {
+        const uint16_t* src;
+        const uint16_t* gamma = nullptr;
+        if (vi < Q) { src = p.qkv + qkv_row + (size_t)(h * Q + vi) * D; gamma = p.qn; }
+        else if (vi == Q) { src = p.qkv + qkv_row + (size_t)(p.Hq + h) * D; gamma = p.kn; }
+        else { src = p.qkv + qkv_row + (size_t)(p.Hq + p.Hkv + h) * D; }
+        px0[n] = bf16_to_f32(src[i0]);
+        px1[n] = bf16_to_f32(src[i1]);
+        if (gamma) { pg0[n] = bf16_to_f32(gamma[i0]); pg1[n] = bf16_to_f32(gamma[i1]); }
+      }
+    }
+    const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
+    const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+
+    u32x4 kreg[ROWS], vreg[ROWS];
+#pragma unroll
+    for (int it = 0; it < ROWS; ++it) {
+      const int t = t0 + it * 16 + grp;
       if (t < t1 && t != pos) {
         kreg[it] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)t * D + 8 * c);
         vreg[it] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)t * D + 8 * c);
@@ -153,24 +202,17 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
       }
     }
 
-    // ---- prologue: q heads h*Q .. h*Q+Q-1, current k and v ----
-    const int i0 = p.style == 0 ? lane : 2 * lane;        // pair (i0, i1) rotates together
-    const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
-    for (int vi = wave; vi < Q + 2; vi += 4) {
-      const uint16_t* src;
-      const uint16_t* gamma = nullptr;
-      if (vi < Q) { src = p.qkv + qkv_row + (size_t)(h * Q + vi) * D; gamma = p.qn; }
-      else if (vi == Q) { src = p.qkv + qkv_row + (size_t)(p.Hq + h) * D; gamma = p.kn; }
-      else { src = p.qkv + qkv_row + (size_t)(p.Hq + p.Hkv + h) * D; }
-      float x0 = bf16_to_f32(src[i0]);
-      float x1 = bf16_to_f32(src[i1]);
-      if (gamma) {
+    // ---- q heads and the current k: per-head RMSNorm then RoPE; v as is ----
+#pragma unroll
+    for (int n = 0; n < NV; ++n) {
+      const int vi = wave + 4 * n;
+      if (vi >= Q + 2) continue;
+      float x0 = px0[n], x1 = px1[n];
+      if (vi <= Q) {
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-        x0 = round_bf16(round_bf16(x0 * inv) * bf16_to_f32(gamma[i0]));
-        x1 = round_bf16(round_bf16(x1 * inv) * bf16_to_f32(gamma[i1]));
-        const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
-        const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+        x0 = round_bf16(round_bf16(x0 * inv) * pg0[n]);
+        x1 = round_bf16(round_bf16(x1 * inv) * pg1[n]);
         const float y0 = round_bf16(round_bf16(x0 * cs) + round_bf16(-x1 * sn));
         const float y1 = round_bf16(round_bf16(x1 * cs) + round_bf16(x0 * sn));
         x0 = y0;
@@ -193,7 +235,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     }
     __syncthreads();
 
-    // ---- scores: 16 lanes per slot, 8 dims per lane ----
+    // ---- 2. scores and the softmax state of each 16-lane group ----
     float qf[Q][8];
 #pragma unroll
     for (int j = 0; j < Q; ++j)
@@ -201,9 +243,10 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
       for (int e = 0; e < 8; ++e) qf[j][e] = s_q[j][8 * c + e];
     const u32x4* kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0]);
     const u32x4* vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0]);
+    float sc[ROWS][Q];
 #pragma unroll
-    for (int it = 0; it < ATT_ROWS; ++it) {
-      const int t = t0 + it * 16 + wave * 4 + rg;
+    for (int it = 0; it < ROWS; ++it) {
+      const int t = t0 + it * 16 + grp;
       if (t == pos) { kreg[it] = kcur[c]; vreg[it] = vcur[c]; }
       float kf[8];
       unpack8(kreg[it], kf);
@@ -213,121 +256,132 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(qf[j][e], kf[e], d);
         d = row_sum16(d);
-        if (c == 0 && t < t1) s_p[j][t - t0] = d * p.scale;
+        sc[it][j] = t < t1 ? d * p.scale : -INFINITY;
       }
     }
-    __syncthreads();
-
-    // ---- chunk softmax statistics ----
-    const int n = t1 - t0;
-    for (int j = wave; j < Q; j += 4) {
-      float mx = -INFINITY;
-      for (int i = lane; i < n; i += 64) mx = fmaxf(mx, s_p[j][i]);
-      mx = row_max16(mx);
-      mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      float sum = 0.0f;
-      for (int i = lane; i < n; i += 64) {
-        const float e = expf(s_p[j][i] - mx);
-        s_p[j][i] = e;
-        sum += e;
-      }
-      sum = wave_sum(sum);
-      if (lane == 0) { s_stat[j][0] = mx; s_stat[j][1] = sum; }
-    }
-    __syncthreads();
-
-    // ---- P . V ----
-    float acc[Q][8];
+    float m[Q], l[Q], acc[Q][8];
 #pragma unroll
-    for (int j = 0; j < Q; ++j)
+    for (int j = 0; j < Q; ++j) {
+      m[j] = sc[0][j];
+#pragma unroll
+      for (int it = 1; it < ROWS; ++it) m[j] = fmaxf(m[j], sc[it][j]);
+      l[j] = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+    }
 #pragma unroll
-    for (int it = 0; it < ATT_ROWS; ++it) {
-      const int t = t0 + it * 16 + wave * 4 + rg;
-      if (t < t1) {
-        float vf[8];
-        unpack8(vreg[it], vf);
+    for (int it = 0; it < ROWS; ++it) {
+      float vf[8];
+      unpack8(vreg[it], vf);
 #pragma unroll
-        for (int j = 0; j < Q; ++j) {
-          const float pj = s_p[j][t - t0];
+      for (int j = 0; j < Q; ++j) {
+        const float pe = sc[it][j] > -INFINITY ? expf(sc[it][j] - m[j]) : 0.0f;
+        l[j] += pe;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pj, vf[e], acc[j][e]);
+        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pe, vf[e], acc[j][e]);
+      }
+    }
+    // merge the four groups of the wave (lanes c, c+16, c+32, c+48 hold the same dims)
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+#pragma unroll
+      for (int j = 0; j < Q; ++j) {
+        const float mo = __shfl_xor(m[j], off, 64);
+        const float lo = __shfl_xor(l[j], off, 64);
+        const float mn = fmaxf(m[j], mo);
+        const float fa = state_weight(m[j], mn), fb = state_weight(mo, mn);
+        l[j] = l[j] * fa + lo * fb;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] * fa + __shfl_xor(acc[j][e], off, 64) * fb;
+        m[j] = mn;
+      }
+    }
+    if (rg == 0) {
+#pragma unroll
+      for (int j = 0; j < Q; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_wacc[wave][j][8 * c + e] = acc[j][e];
+        if (c == 0) { s_wm[wave][j] = m[j]; s_wl[wave][j] = l[j]; }
+      }
+    }
+    __syncthreads();
+
+    // ---- merge the four waves; one chunk: write the context, else store the state ----
+    for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
+      const int j = idx / D, d = idx - j * D;
+      float M = s_wm[0][j];
+#pragma unroll
+      for (int w = 1; w < 4; ++w) M = fmaxf(M, s_wm[w][j]);
+      float lsum = 0.0f, o = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float f = state_weight(s_wm[w][j], M);
+        lsum = fmaf(s_wl[w][j], f, lsum);
+        o = fmaf(s_wacc[w][j][d], f, o);
+      }
+      if (p.splits == 1) {
+        p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] = (uint16_t)f32_to_bf16(o / lsum);
+      } else {
+        st_agent(p.part_o + (part * Q + j) * D + d, o);
+        if (d == 0) {
+          st_agent(p.part_ml + (part * Q + j) * 2, M);
+          st_agent(p.part_ml + (part * Q + j) * 2 + 1, lsum);
         }
       }
     }
-#pragma unroll
-    for (int j = 0; j < Q; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float a = acc[j][e];
-        a += __shfl_xor(a, 16, 64);
-        a += __shfl_xor(a, 32, 64);
-        acc[j][e] = a;
-      }
-    if (rg == 0) {
-#pragma unroll
-      for (int j = 0; j < Q; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s_red[wave][j][8 * c + e] = acc[j][e];
-    }
-    __syncthreads();
-    for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
-      const int j = idx / D, d = idx - (idx / D) * D;
-      const float o = s_red[0][j][d] + s_red[1][j][d] + s_red[2][j][d] + s_red[3][j][d];
-      if (p.splits == 1) {
-        p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] = (uint16_t)f32_to_bf16(o / s_stat[j][1]);
-      } else {
-        p.part_o[(((size_t)bh * p.splits + split) * Q + j) * D + d] = o;
-      }
-    }
-    if (p.splits > 1 && tid < Q) {
-      float* ml = p.part_ml + (((size_t)bh * p.splits + split) * Q + tid) * 2;
-      ml[0] = s_stat[tid][0];
-      ml[1] = s_stat[tid][1];
-    }
   } else if (p.splits > 1) {
-    if (tid < Q) {
-      float* ml = p.part_ml + (((size_t)bh * p.splits + split) * Q + tid) * 2;
-      ml[0] = -INFINITY;
-      ml[1] = 0.0f;
+    if (tid < Q) {   // an empty chunk: a state that weighs nothing
+      st_agent(p.part_ml + (part * Q + tid) * 2, -INFINITY);
+      st_agent(p.part_ml + (part * Q + tid) * 2 + 1, 0.0f);
     }
   } else {
     for (int idx = tid; idx < Q * D; idx += ATT_THREADS)
       p.out[(size_t)b * p.Hq * D + (size_t)h * Q * D + idx] = 0;
   }
-}
+  if (p.splits == 1) return;
 
-// Combine the context splits of one (sequence, kv head) in split order:
-// M = max m_s, L = sum l_s e^(m_s - M), O = sum o_s e^(m_s - M) / L.
-// A separate launch: the kernel boundary makes the partials visible, which is
-// far cheaper than a device-scope release fence in every attention workgroup.
-__global__ __launch_bounds__(ATT_THREADS) void attention_combine_kernel(const AttnParams p, int Q) {
-  constexpr int D = ATT_D;
-  const int bh = blockIdx.x;
-  const int b = bh / p.Hkv;
-  const int h = bh - b * p.Hkv;
-  for (int idx = threadIdx.x; idx < Q * D; idx += ATT_THREADS) {
-    const int j = idx / D, d = idx - (idx / D) * D;
-    const float* ml = p.part_ml + ((size_t)bh * p.splits * Q + j) * 2;
-    float mx = -INFINITY;
-    for (int s = 0; s < p.splits; ++s) {
-      const float* e = ml + (size_t)s * Q * 2;
-      if (e[1] > 0.0f) mx = fmaxf(mx, e[0]);
-    }
-    float lsum = 0.0f, o = 0.0f;
-    for (int s = 0; s < p.splits; ++s) {
-      const float* e = ml + (size_t)s * Q * 2;
-      if (e[1] > 0.0f) {
-        const float f = expf(e[0] - mx);
-        lsum = fmaf(e[1], f, lsum);
-        o = fmaf(p.part_o[(((size_t)bh * p.splits + s) * Q + j) * D + d], f, o);
+  // ---- 3. the last chunk of (b, h) to arrive merges every chunk's state, in chunk order ----
+  wait_stores();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned before = __hip_atomic_fetch_add(p.arrivals + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = before == (unsigned)(p.splits - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
+    const int j = idx / D, d = idx - j * D;
+    float M = -INFINITY, lsum = 0.0f, o = 0.0f;
+    // chunk states in groups of 8: the loads of a group are issued back to back
+    for (int s0 = 0; s0 < p.splits; s0 += 8) {
+      float ms[8], ls[8], os[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const size_t st = (size_t)bh * p.splits + s0 + u;
+        ms[u] = -INFINITY;
+        ls[u] = 0.0f;
+        os[u] = 0.0f;
+        if (s0 + u < p.splits) {
+          ms[u] = ld_agent(p.part_ml + (st * Q + j) * 2);
+          ls[u] = ld_agent(p.part_ml + (st * Q + j) * 2 + 1);
+          os[u] = ld_agent(p.part_o + (st * Q + j) * D + d);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (ls[u] > 0.0f) {   // an empty chunk stored no context
+          const float mn = fmaxf(M, ms[u]);
+          const float fa = state_weight(M, mn), fb = expf(ms[u] - mn);
+          lsum = lsum * fa + ls[u] * fb;
+          o = o * fa + os[u] * fb;
+          M = mn;
+        }
       }
     }
     p.out[(size_t)b * p.Hq * D + (size_t)(h * Q + j) * D + d] =
         lsum > 0.0f ? (uint16_t)f32_to_bf16(o / lsum) : (uint16_t)0;
   }
+  if (tid == 0) __hip_atomic_store(p.arrivals + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ============================================================================
@@ -461,22 +515,40 @@ using t2i_host::fail;
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Attention plan: the context is split into chunks of 16 * rows slots, one
+// workgroup each; with more than one chunk, their states meet in a workspace:
+// the arrival counters (zero between launches), each chunk's (max, sum) pairs
+// and each chunk's context.
 struct AttnPlan {
-  int chunk, splits;
-  size_t off_o, bytes;
+  int rows, chunk, splits;
+  size_t off_ml, off_o, bytes;
 };
 
 AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
   AttnPlan pl{};
-  pl.chunk = ATT_CHUNK;
-  pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
   const int Q = Hq / Hkv;
+  pl.rows = att_rows(Q);
+#ifdef T2I_TUNING
+  if (const char* env = getenv("T2I_ATTN_ROWS")) {
+    const int r = atoi(env);
+    if ((r == 4 || r == 8 || r == 16) && Q <= 2) pl.rows = r;
+  }
+#endif
+  pl.chunk = 16 * pl.rows;
+  pl.splits = (ctx_cap + pl.chunk - 1) / pl.chunk;
   const size_t units = (size_t)B * Hkv;
   if (pl.splits > 1) {
-    pl.off_o = align256(units * pl.splits * Q * 2 * 4);
-    pl.bytes = pl.off_o + units * pl.splits * Q * ATT_D * 4;
+    pl.off_ml = align256(units * sizeof(unsigned));
+    pl.off_o = pl.off_ml + align256(units * pl.splits * Q * 2 * sizeof(float));
+    pl.bytes = pl.off_o + units * pl.splits * Q * ATT_D * sizeof(float);
   }
   return pl;
+}
+
+template <int Q, int ROWS>
+hipError_t launch_attention(const AttnParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((decode_attention_kernel<Q, ROWS>), grid, dim3(ATT_THREADS), 0, s, p);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -528,24 +600,27 @@ extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* position
   AttnParams p{};
   p.qkv = qkv; p.pos = positions; p.qn = q_norm; p.kn = k_norm; p.rope = rope;
   p.kc = k_cache; p.vc = v_cache; p.out = ctx;
-  char* ws = reinterpret_cast<char*>(workspace);
-  p.part_ml = ws ? reinterpret_cast<float*>(ws) : nullptr;
+  char* ws = pl.bytes ? reinterpret_cast<char*>(workspace) : nullptr;
+  p.arrivals = ws ? reinterpret_cast<unsigned*>(ws) : nullptr;
+  p.part_ml = ws ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr;
   p.part_o = ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr;
-  p.Hq = Hq; p.Hkv = Hkv; p.ctx_cap = ctx_cap; p.chunk = pl.chunk; p.splits = pl.splits; p.style = rope_style;
+  p.Hq = Hq; p.Hkv = Hkv; p.ctx_cap = ctx_cap; p.splits = pl.splits; p.style = rope_style;
   p.eps = eps;
   p.scale = (float)(1.0 / sqrt((double)D));
-  dim3 grid(B * Hkv, pl.splits);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (Q) {
-    case 1: hipLaunchKernelGGL((decode_attention_kernel<1>), grid, dim3(ATT_THREADS), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((decode_attention_kernel<2>), grid, dim3(ATT_THREADS), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((decode_attention_kernel<4>), grid, dim3(ATT_THREADS), 0, s, p); break;
-    default: hipLaunchKernelGGL((decode_attention_kernel<8>), grid, dim3(ATT_THREADS), 0, s, p); break;
+  const dim3 grid(B * Hkv, pl.splits);
+  hipError_t e;
+  switch (Q * 100 + pl.rows) {
+    case 104: e = launch_attention<1, 4>(p, grid, s); break;
+    case 108: e = launch_attention<1, 8>(p, grid, s); break;
+    case 116: e = launch_attention<1, 16>(p, grid, s); break;
+    case 204: e = launch_attention<2, 4>(p, grid, s); break;
+    case 208: e = launch_attention<2, 8>(p, grid, s); break;
+    case 216: e = launch_attention<2, 16>(p, grid, s); break;
+    case 404: e = launch_attention<4, 4>(p, grid, s); break;
+    default: e = launch_attention<8, 2>(p, grid, s); break;
   }
-  int rc = t2i_host::hip_status(hipGetLastError(), "attention launch");
-  if (rc || pl.splits == 1) return rc;
-  hipLaunchKernelGGL(t2i::attention_combine_kernel, dim3(B * Hkv), dim3(ATT_THREADS), 0, s, p, Q);
-  return t2i_host::hip_status(hipGetLastError(), "attention combine launch");
+  return t2i_host::hip_status(e, "attention launch");
 }
 
 extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,

@@ -58,6 +58,22 @@ __device__ __forceinline__ float row_max16(float v) {
   return v;
 }
 
+// ---- agent-coherent exchange between workgroups of one launch ----
+// The L2 of each XCD is not coherent with the others.  A relaxed agent-scope
+// store is written through to the device-coherent level (sc1) and a relaxed
+// agent-scope load bypasses stale cached copies (sc1), so workgroups on
+// different XCDs can hand data over without an L2 write-back fence: the
+// producer stores with st_agent, waits for its stores (wait_stores) and then
+// bumps an agent-scope counter; a consumer that observes the counter reads
+// the data with ld_agent.
+__device__ __forceinline__ void st_agent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
   v = row_sum16(v);
   // combine the four rows: lanes l, l^16, l^32, l^48 hold row sums
