@@ -91,14 +91,15 @@ def test_python_layer_rejects_cpu_tensors_and_bad_shapes():
 
 def test_workspace_sizes_are_consistent():
     lib = _lib.load()
-    # one workgroup per (sequence, kv head) streams the context: no workspace
-    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 1088) == 0
-    assert lib.t2i_decode_attention_workspace_bytes(16, 16, 8, 640) == 0
+    # a context of at most one 128-slot chunk needs no workspace
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0
-    # few (sequence, kv head) pairs over a long context, or 4+ q heads per kv head: split chunks
-    n = lib.t2i_decode_attention_workspace_bytes(2, 16, 8, 4096)
-    assert n >= 2 * 8 * 4 + 2 * 8 * (4096 // 128) * 2 * (2 * 4 + 128 * 4)
-    assert lib.t2i_decode_attention_workspace_bytes(4, 16, 4, 640) > 0
+    assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 128) == 0
+    # counters + (max, sum) pairs + contexts of every chunk
+    for b, hq, hkv, cap, chunk in ((8, 16, 8, 1088, 128), (2, 16, 8, 4096, 128), (4, 16, 4, 640, 64)):
+        units, q, splits = b * hkv, hq // hkv, -(-cap // chunk)
+        need = units * 4 + units * splits * q * 2 * 4 + units * splits * q * 128 * 4
+        n = lib.t2i_decode_attention_workspace_bytes(b, hq, hkv, cap)
+        assert need <= n <= need + 512, (b, hq, hkv, cap, n, need)
     assert lib.t2i_decode_attention_workspace_bytes(0, 16, 8, 640) == 0
 
 
