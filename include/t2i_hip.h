@@ -86,6 +86,25 @@ int t2i_w4a16_gate_up(const uint16_t* x, int32_t M,
                       int32_t swiglu, uint16_t* y0, uint16_t* y1, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * RMSNorm prologue fused into the linear: each workgroup normalises the rows it
+ * multiplies, y = W4A16(xn), xn = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * norm_weight)
+ * (rounded as t2i_rmsnorm).  K <= 4096; other limits as t2i_w4a16_linear /
+ * t2i_w4a16_gate_up.  x is the un-normalised residual stream [M, K].
+ * Replaces: fast_qwen3/operators/q4nx_fused_qkv_projection/op.py:30-136
+ *           (Q4NXFusedQKVProjection: hidden, norm_weight, W, out) and
+ *           fast_qwen3/operators/q4nx_fused_up_gate_projection/op.py:30-126
+ *           (Q4NXFusedUpGateProjection), with the RMSNorm + projection of
+ *           quantized_qwen3/batch_decode_fused.py:426-530.
+ */
+int t2i_w4a16_rmsnorm_linear(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                             const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                             int32_t K, int32_t N, int32_t group_size, uint16_t* y, void* stream);
+int t2i_w4a16_rmsnorm_gate_up(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                              const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                              int32_t K, int32_t N, int32_t group_size, int32_t swiglu,
+                              uint16_t* y0, uint16_t* y1, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Weighted RMSNorm over rows of H: y = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * w).
  * tokens != NULL: x rows are gathered from the bf16 table `x` ([V, H]) by token id
  * and the gathered rows are also written to x_out (the residual stream); an id

@@ -58,6 +58,19 @@ def test_linear_residual_and_pair_validation():
         == _lib.T2I_ERR_GROUP
 
 
+def test_fused_norm_entry_points_validate():
+    lib = _lib.load()
+    f = lib.t2i_w4a16_rmsnorm_linear
+    assert f(FAKE, 16, None, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_NULL
+    assert f(FAKE, 16, FAKE, 0.0, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_VALUE
+    assert f(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 8192, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert f(FAKE, 65, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert f(FAKE + 2, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_ALIGN
+    g = lib.t2i_w4a16_rmsnorm_gate_up
+    assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None) == _lib.T2I_ERR_NULL
+    assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 64, 1, FAKE, None, None) == _lib.T2I_ERR_GROUP
+
+
 def test_other_entry_points_validate():
     lib = _lib.load()
     assert lib.t2i_rmsnorm(FAKE, None, 0, 4, 1020, FAKE, 1e-6, None, FAKE, None, None) == _lib.T2I_ERR_SHAPE

@@ -132,3 +132,39 @@ def test_golden_fixture_on_gpu(gpu):
     x = torch.from_numpy(g["x"]).to(torch.bfloat16)
     assert torch.equal(x.float(), torch.from_numpy(g["x"])), "fixture activations are bf16 values"
     check_linear(ops.linear(x.to(gpu), w), g["y"])
+
+
+NORM_CASES = [(1, 1024, 4096), (8, 1024, 4096), (16, 1024, 6144), (33, 2048, 4096), (64, 1024, 1024),
+              (5, 4096, 512), (16, 2048, 12288)]
+
+
+@pytest.mark.parametrize("m,k,n", NORM_CASES, ids=[f"M{m}-K{k}-N{n}" for m, k, n in NORM_CASES])
+def test_rmsnorm_linear_fused_equals_unfused(gpu, m, k, n):
+    """The RMSNorm done inside the linear kernel rounds exactly as t2i_rmsnorm, so the
+    fused call is bit-identical to rmsnorm-then-linear, and within the linear bar of
+    the oracle (bf16 RMSNorm chain, fp64 product)."""
+    from oracle import qwen3 as oq
+    qw, qz, sc, x = _inputs(m, k, n, seed=77 + m + k)
+    x = (x.float() * 3.0).to(torch.bfloat16)           # residual-stream-like magnitude
+    gam = (torch.rand(k, generator=torch.Generator().manual_seed(m)) * 0.2 + 0.9).to(torch.bfloat16)
+    w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
+    xd, gd = x.to(gpu), gam.to(gpu)
+    fused = ops.rmsnorm_linear(xd, gd, 1e-6, w)
+    unfused = ops.linear(ops.rmsnorm(xd, gd, 1e-6), w)
+    assert torch.equal(fused, unfused)
+    xn = oq.rmsnorm(x.float(), gam.float(), 1e-6, oq._Round("bf16"))
+    check_linear(fused, ow.linear(xn.numpy(), qw, qz, sc, accumulate="fp64"))
+
+
+@pytest.mark.parametrize("m,k,inter", [(1, 1024, 3072), (16, 1024, 3072), (40, 2048, 6144)])
+def test_rmsnorm_gate_up_fused_equals_unfused(gpu, m, k, inter):
+    gate = ow.synthetic_tensors(k, inter, seed=21)
+    up = ow.synthetic_tensors(k, inter, seed=22)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(23)) * 3.0).to(torch.bfloat16).to(gpu)
+    gam = (torch.rand(k, generator=torch.Generator().manual_seed(24)) * 0.2 + 0.9).to(torch.bfloat16).to(gpu)
+    w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
+    xn = ops.rmsnorm(x, gam, 1e-6)
+    assert torch.equal(ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=True), ops.gate_up(xn, w, swiglu=True))
+    g1, u1 = ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=False)
+    g2, u2 = ops.gate_up(xn, w, swiglu=False)
+    assert torch.equal(g1, g2) and torch.equal(u1, u2)

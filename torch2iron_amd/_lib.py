@@ -33,6 +33,10 @@ SIGNATURES = {
                                    c_void_p, c_void_p, c_void_p]),
     "t2i_w4a16_gate_up": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
                                     c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_w4a16_rmsnorm_linear": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
+                                           c_int32, c_int32, c_int32, c_void_p, c_void_p]),
+    "t2i_w4a16_rmsnorm_gate_up": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
+                                            c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_float, c_void_p,
                               c_void_p, c_void_p, c_void_p]),
     "t2i_decode_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),

@@ -43,6 +43,8 @@ struct LinearParams {
   const uint16_t* residual;
   uint16_t* y0;
   uint16_t* y1;
+  const uint16_t* gamma;   // RMSNorm weight [K] of the fused-norm variant
+  float eps;
   int M, K, N;
   int ldx, ldy;
   int chunks;           // K / (32 * CK)
@@ -93,35 +95,38 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&w)[LW
   }
 }
 
+// Raw fp16 scales of LW consecutive columns, two per word (converted only when
+// the chunk is computed, so issuing a chunk's loads never waits for them).
 template <int LW>
-__device__ __forceinline__ void load_scales(const uint16_t* src, float (&s)[LW]) {
+__device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[(LW + 1) / 2]) {
   if constexpr (LW == 8) {
     const u32x4 a = *reinterpret_cast<const u32x4*>(src);
-    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { s[2 * i] = f16_to_f32(v[i] & 0xFFFFu); s[2 * i + 1] = f16_to_f32(v[i] >> 16); }
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w;
   } else if constexpr (LW == 4) {
     const u32x2 a = *reinterpret_cast<const u32x2*>(src);
-    s[0] = f16_to_f32(a.x & 0xFFFFu); s[1] = f16_to_f32(a.x >> 16);
-    s[2] = f16_to_f32(a.y & 0xFFFFu); s[3] = f16_to_f32(a.y >> 16);
+    s[0] = a.x; s[1] = a.y;
   } else if constexpr (LW == 2) {
-    const uint32_t a = *reinterpret_cast<const uint32_t*>(src);
-    s[0] = f16_to_f32(a & 0xFFFFu); s[1] = f16_to_f32(a >> 16);
+    s[0] = *reinterpret_cast<const uint32_t*>(src);
   } else {
-    s[0] = f16_to_f32(*src);
+    s[0] = *src;
   }
 }
 
-// Operands of one chunk (CK k-steps, all inside one quantisation group).
+template <int LW>
+__device__ __forceinline__ float scale_of(const uint32_t (&s)[(LW + 1) / 2], int t) {
+  return f16_to_f32((t & 1) ? (s[t >> 1] >> 16) : (s[t >> 1] & 0xFFFFu));
+}
+
+// Operands of one chunk (CK k-steps, all inside one quantisation group), as loaded.
 template <int MT, int LW, int CK>
 struct Chunk {
   uint32_t w[CK][LW];
   u32x4 x[MT][CK];
-  float s[LW];
-  uint32_t z;   // zero nibbles of this lane's columns, column ncol + t at bits 4t
+  uint32_t s[(LW + 1) / 2];   // fp16 scales of this lane's LW columns
+  uint32_t zw;                // qzeros word holding this lane's columns
 };
 
-template <int MT, int LW, int CK>
+template <int MT, int LW, int CK, bool NORM>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
   const int ks0 = ch * CK;
@@ -129,7 +134,7 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
   for (int j = 0; j < CK; ++j)
     load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
+  for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) {
     const int m = mbase + mi * 16 + c;
 #pragma unroll
     for (int j = 0; j < CK; ++j) {
@@ -141,11 +146,15 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
   }
   const int g = ks0 / KSG;
   load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s);
-  b.z = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)] >> ((ncol & 7) * 4);
+  b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
 }
 
-template <int MT, int LW, int CK>
-__device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4]) {
+// a_lds (fused-norm variant): the normalised activations of the row tile in
+// A-operand order, 64 lanes x 16 bytes per k-step; k-step ks0 is this chunk's first.
+template <int MT, int LW, int CK, bool NORM>
+__device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4],
+                                              const u32x4* a_lds, int ks0, int lane, int zshift) {
+  const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
   const bf16x8 ones = ones_operand();
   f32x4 acc[MT][LW];
   f32x4 xs[MT];
@@ -162,7 +171,9 @@ __device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float 
     for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t]);
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) {
-      const bf16x8 a = a_operand(b.x[mi][j]);
+      bf16x8 a;
+      if constexpr (NORM) a = __builtin_bit_cast(bf16x8, a_lds[(ks0 + j) * 64 + lane]);
+      else a = a_operand(b.x[mi][j]);
       xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < LW; ++t)
@@ -171,12 +182,13 @@ __device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float 
   }
 #pragma unroll
   for (int t = 0; t < LW; ++t) {
-    const float zb = -(float)(128 + 1 + ((b.z >> (4 * t)) & 0xFu));
+    const float zb = -(float)(128 + 1 + ((zw >> (4 * t)) & 0xFu));
+    const float sc = scale_of<LW>(b.s, t);
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        total[mi][t][i] = fmaf(b.s[t], fmaf(zb, xs[mi][i], acc[mi][t][i]), total[mi][t][i]);
+        total[mi][t][i] = fmaf(sc, fmaf(zb, xs[mi][i], acc[mi][t][i]), total[mi][t][i]);
   }
 }
 
@@ -240,20 +252,100 @@ __device__ __forceinline__ void epilogue(const LinearParams& p, int ncol, int r,
     }
 }
 
-template <int MT, int LW, int W, int CK>
+// Fused RMSNorm prologue.  Wave w takes k-steps w, w + W, ...; for k-step ks
+// lane l = 16 r + row loads x[row][32 ks + 8 r .. + 7] and the matching norm
+// weight (all loads of the tile issued together, overlapping the first weight
+// chunk already in flight) and parks them in LDS at A-operand slot 64 ks + l,
+// so every LDS access of a wave is one contiguous 1 KB (no bank conflicts).
+// The per-row sums of squares meet through lane shuffles and a small table
+// (fixed order), then each lane normalises the slots it parked, rounding as the
+// standalone RMSNorm: bf16(bf16(x * inv) * w), inv = bf16(1 / sqrt(mean(x^2) + eps)).
+// Rows beyond M are zero.
+constexpr int NORM_MAX_K = 4096;
+
+template <int W>
+__device__ __forceinline__ void norm_prologue(const LinearParams& p, int mbase, int wave, int lane, u32x4* a_lds) {
+  __shared__ float s_ss[W][16];
+  __shared__ float s_inv[16];
+  const int ksteps = p.K / 32;
+  const int row = lane & 15, r = lane >> 4;
+  const bool row_ok = mbase + row < p.M;
+  const uint16_t* xrow = p.x + (size_t)(mbase + row) * p.ldx + r * 8;
+  u32x4* g_lds = a_lds + ksteps * 64;            // norm weight, 16 bytes per (k-step, sub-block)
+  float ss = 0.0f;
+  for (int ks0 = wave; ks0 < ksteps; ks0 += 4 * W) {
+    u32x4 v[4], g[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ks = ks0 + i * W;
+      v[i] = g[i] = u32x4{0u, 0u, 0u, 0u};
+      if (ks < ksteps) {
+        if (row_ok) v[i] = *reinterpret_cast<const u32x4*>(xrow + ks * 32);
+        if (row == 0) g[i] = *reinterpret_cast<const u32x4*>(p.gamma + ks * 32 + r * 8);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ks = ks0 + i * W;
+      if (ks >= ksteps) continue;
+      const uint32_t a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
+        ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
+      }
+      a_lds[ks * 64 + lane] = v[i];
+      if (row == 0) g_lds[ks * 4 + r] = g[i];
+    }
+  }
+  ss += __shfl_xor(ss, 16, 64);                  // the four sub-blocks of a row
+  ss += __shfl_xor(ss, 32, 64);
+  if (lane < 16) s_ss[wave][lane] = ss;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t += s_ss[w][threadIdx.x];
+    s_inv[threadIdx.x] = round_bf16(1.0f / sqrtf(t / (float)p.K + p.eps));
+  }
+  __syncthreads();
+  const float inv = s_inv[row];
+  for (int ks = wave; ks < ksteps; ks += W) {
+    const u32x4 v = a_lds[ks * 64 + lane];
+    const u32x4 g = g_lds[ks * 4 + r];
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+    const uint32_t w[4] = {g.x, g.y, g.z, g.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = round_bf16(round_bf16(bf16_lo(a[e]) * inv) * bf16_lo(w[e]));
+      const float hi = round_bf16(round_bf16(bf16_hi(a[e]) * inv) * bf16_hi(w[e]));
+      o[e] = pack_bf16x2(lo, hi);
+    }
+    a_lds[ks * 64 + lane] = __builtin_bit_cast(u32x4, a_operand(u32x4{o[0], o[1], o[2], o[3]}));
+  }
+}
+
+template <int MT, int LW, int W, int CK, bool NORM>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p) {
+  static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
   constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int r = lane >> 4;
   const int ncol = blockIdx.x * (16 * LW) + LW * c;
+  const int zshift = (ncol & 7) * 4;
   const int mbase = blockIdx.z * (16 * MT);   // row tile of this workgroup
 
   // this wave's chunks: a contiguous slice of K
   const int per_wave = (p.chunks + W - 1) / W;
   const int c_begin = wave * per_wave;
   const int c_end = min(c_begin + per_wave, p.chunks);
+
+  // fused-norm variant: the normalised row tile (K / 32 KB), later reused for the wave reduction
+  extern __shared__ __align__(16) char dyn_lds[];
+  u32x4* a_lds = reinterpret_cast<u32x4*>(dyn_lds);
 
   float total[MT][LW][4];
 #pragma unroll
@@ -263,21 +355,28 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
 #pragma unroll
       for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
 
+  Chunk<MT, LW, CK> A, B;
+  if (c_begin < c_end) load_chunk<MT, LW, CK, NORM>(p, c_begin, ncol, c, r, mbase, A);
+  if constexpr (NORM) {
+    // the first chunk's weights are in flight while the rows are normalised
+    norm_prologue<W>(p, mbase, wave, lane, a_lds);
+    __syncthreads();
+  }
   if (c_begin < c_end) {
-    Chunk<MT, LW, CK> A, B;
-    load_chunk(p, c_begin, ncol, c, r, mbase, A);
     for (int ch = c_begin; ch < c_end; ch += 2) {
-      if (ch + 1 < c_end) load_chunk(p, ch + 1, ncol, c, r, mbase, B);
-      compute_chunk(A, total);
+      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
+      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, ch * CK, lane, zshift);
       if (ch + 1 >= c_end) break;
-      if (ch + 2 < c_end) load_chunk(p, ch + 2, ncol, c, r, mbase, A);
-      compute_chunk(B, total);
+      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 2, ncol, c, r, mbase, A);
+      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (ch + 1) * CK, lane, zshift);
     }
   }
 
   // ---- reduce the waves of this workgroup in LDS (fixed tree) ----
   if constexpr (W > 1) {
-    __shared__ float red[(W / 2) * E * 64];
+    __shared__ float red_static[NORM ? 1 : (W / 2) * E * 64];
+    float* red = NORM ? reinterpret_cast<float*>(dyn_lds) : red_static;
+    if constexpr (NORM) __syncthreads();   // every wave is done with the normalised rows
 #pragma unroll
     for (int half = W / 2; half >= 1; half >>= 1) {
       if (wave >= half && wave < 2 * half) {
@@ -400,16 +499,36 @@ Plan plan_linear(int M, int K, int N, bool paired) {
   return pl;
 }
 
-template <int MT, int LW, int W, int CK>
-hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK>), grid, dim3(64 * W), 0, s, p);
+// LDS of the fused-norm variant: the normalised row tile, later reused by the
+// wave reduction.
+size_t norm_lds_bytes(const Plan& pl, int K) {
+  const size_t rows = (size_t)K * 32 + (size_t)K * 2;                  // K / 32 k-steps x 1 KB + norm weight
+  const size_t red = (size_t)(pl.W / 2) * pl.MT * pl.LW * 4 * 64 * sizeof(float);
+  return rows > red ? rows : red;
+}
+
+template <int MT, int LW, int W, int CK, bool NORM>
+hipError_t launch_t(const LinearParams& p, dim3 grid, size_t lds, hipStream_t s) {
+  if constexpr (NORM) {
+    // raise the dynamic LDS limit once per kernel for tiles above 64 KB
+    static thread_local size_t raised = 65536;
+    if (lds > raised) {
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_mfma_kernel<MT, LW, W, CK, true>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      raised = lds;
+    }
+  }
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM>), grid, dim3(64 * W), lds, s, p);
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const Plan& pl, const LinearParams& p, hipStream_t s) {
+hipError_t launch_plan(const Plan& pl, const LinearParams& p, bool norm, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
-#define T2I_LAUNCH(a, b, c, d) \
-  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_t<a, b, c, d>(p, grid, s);
+  const size_t lds = norm ? norm_lds_bytes(pl, p.K) : 0;
+#define T2I_LAUNCH(a, b, c, d)                                                          \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)                              \
+    return norm ? launch_t<a, b, c, d, true>(p, grid, lds, s) : launch_t<a, b, c, d, false>(p, grid, lds, s);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;
@@ -426,9 +545,10 @@ int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
   return T2I_OK;
 }
 
-int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const int32_t* qzeros,
-               const uint16_t* scales, int K, int N, int group_size, const uint16_t* residual,
-               uint16_t* y0, uint16_t* y1, void* stream) {
+// gamma != NULL: the fused-norm variant (x is normalised with gamma, eps first).
+int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float eps, const int32_t* qweight,
+               const int32_t* qzeros, const uint16_t* scales, int K, int N, int group_size,
+               const uint16_t* residual, uint16_t* y0, uint16_t* y1, void* stream) {
   int rc = check_weights(qweight, qzeros, scales, K, N, group_size);
   if (rc) return rc;
   if (!x || !y0) return fail(T2I_ERR_NULL, "x and y must not be NULL");
@@ -437,6 +557,11 @@ int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const 
   if (M < 1 || M > 64) return fail(T2I_ERR_SHAPE, "M=%d must be in [1, 64]", M);
   if (!aligned16(x) || !aligned16(y0) || (y1 && !aligned16(y1)) || (residual && !aligned16(residual)))
     return fail(T2I_ERR_ALIGN, "activation pointers must be 16-byte aligned");
+  if (gamma) {
+    if (K > NORM_MAX_K) return fail(T2I_ERR_SHAPE, "K=%d exceeds %d for the fused RMSNorm", K, NORM_MAX_K);
+    if (!aligned16(gamma)) return fail(T2I_ERR_ALIGN, "norm_weight must be 16-byte aligned");
+    if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  }
   const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
   const Plan pl = plan_linear(M, K, N, paired);
   LinearParams p{};
@@ -447,12 +572,15 @@ int run_linear(int epi, const uint16_t* x, int M, const int32_t* qweight, const 
   p.residual = residual;
   p.y0 = y0;
   p.y1 = y1;
+  p.gamma = gamma;
+  p.eps = eps;
   p.M = M; p.K = K; p.N = N;
   p.ldx = K;
   p.ldy = paired ? N / 2 : N;
   p.chunks = pl.chunks;
   p.epi = epi;
-  return t2i_host::hip_status(launch_plan(pl, p, reinterpret_cast<hipStream_t>(stream)), "w4a16 linear launch");
+  return t2i_host::hip_status(launch_plan(pl, p, gamma != nullptr, reinterpret_cast<hipStream_t>(stream)),
+                              "w4a16 linear launch");
 }
 
 }  // namespace
@@ -461,7 +589,7 @@ extern "C" int t2i_w4a16_linear(const uint16_t* x, int32_t M, const int32_t* qwe
                                 const int32_t* qzeros, const uint16_t* scales, int32_t K,
                                 int32_t N, int32_t group_size, const uint16_t* residual,
                                 uint16_t* y, void* stream) {
-  return run_linear(residual ? EPI_RESIDUAL : EPI_STORE, x, M, qweight, qzeros, scales, K, N,
+  return run_linear(residual ? EPI_RESIDUAL : EPI_STORE, x, M, nullptr, 0.0f, qweight, qzeros, scales, K, N,
                     group_size, residual, y, nullptr, stream);
 }
 
@@ -469,7 +597,24 @@ extern "C" int t2i_w4a16_gate_up(const uint16_t* x, int32_t M, const int32_t* qw
                                  const int32_t* qzeros, const uint16_t* scales, int32_t K,
                                  int32_t N, int32_t group_size, int32_t swiglu, uint16_t* y0,
                                  uint16_t* y1, void* stream) {
-  return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, qweight, qzeros, scales, K, N,
+  return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, nullptr, 0.0f, qweight, qzeros, scales, K, N,
+                    group_size, nullptr, y0, y1, stream);
+}
+
+extern "C" int t2i_w4a16_rmsnorm_linear(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                                        const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                        int32_t K, int32_t N, int32_t group_size, uint16_t* y, void* stream) {
+  if (!norm_weight) return fail(T2I_ERR_NULL, "norm_weight must not be NULL");
+  return run_linear(EPI_STORE, x, M, norm_weight, eps, qweight, qzeros, scales, K, N, group_size, nullptr, y,
+                    nullptr, stream);
+}
+
+extern "C" int t2i_w4a16_rmsnorm_gate_up(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                                         const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                         int32_t K, int32_t N, int32_t group_size, int32_t swiglu, uint16_t* y0,
+                                         uint16_t* y1, void* stream) {
+  if (!norm_weight) return fail(T2I_ERR_NULL, "norm_weight must not be NULL");
+  return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, norm_weight, eps, qweight, qzeros, scales, K, N,
                     group_size, nullptr, y0, y1, stream);
 }
 

@@ -1,20 +1,21 @@
 """W4A16 Qwen3 decoder on one MI355X: the fused decode layer and batched greedy decode.
 
-Per layer and decode step (batch B, one token per sequence), seven launches:
+Per layer and decode step (batch B, one token per sequence), five launches:
 
-1. ``t2i_rmsnorm``           input RMSNorm (layer 0: gathers the embedding rows)
-2. ``t2i_w4a16_linear``      fused q|k|v projection (N = (Hq + 2 Hkv) * D)
-3. ``t2i_decode_attention``  q/k RMSNorm + RoPE + KV-cache write + GQA attention
-4. ``t2i_w4a16_linear``      o_proj with the residual add folded in (in place)
-5. ``t2i_rmsnorm``           post-attention RMSNorm
-6. ``t2i_w4a16_gate_up``     fused gate|up projection with the SwiGLU epilogue
-7. ``t2i_w4a16_linear``      down projection with the residual add (in place)
+1. ``t2i_w4a16_rmsnorm_linear``   input RMSNorm + fused q|k|v projection (N = (Hq + 2 Hkv) * D);
+                                  layer 0 instead takes the rows that ``t2i_rmsnorm`` gathered
+                                  from the embedding and normalised
+2. ``t2i_decode_attention``       q/k RMSNorm + RoPE + KV-cache write + GQA attention
+3. ``t2i_w4a16_linear``           o_proj with the residual add folded in (in place)
+4. ``t2i_w4a16_rmsnorm_gate_up``  post-attention RMSNorm + fused gate|up projection + SwiGLU
+5. ``t2i_w4a16_linear``           down projection with the residual add (in place)
 
 then the final RMSNorm, the tied bf16 lm_head with the fused argmax, and the
 device-side token bookkeeping.  This is the per-layer runlist of the
 reference's NPU batch decoder (``quantized_qwen3/batch_decode_fused.py:426-539``)
-re-cut for the GPU: q/k/v are one linear, gate/up one linear with SwiGLU, and
-the RoPE, q/k-norm and KV write live in the attention prologue.
+re-cut for the GPU: q/k/v are one linear, gate/up one linear with SwiGLU, the
+RMSNorms run inside the linears that consume them, and the RoPE, q/k-norm and
+KV write live in the attention prologue.
 
 A whole decode step is captured once into a HIP graph and replayed; token ids,
 positions and the output history stay on the device between steps.
@@ -201,18 +202,21 @@ class Qwen3DecodeLayer:
         self.rope_style = ops.ROPE_HALVES if cfg.rope_style == "halves" else ops.ROPE_INTERLEAVED
 
     def attention_half(self, buf: DecodeBuffers, positions, k_cache, v_cache, normed: bool = False):
+        """``normed``: ``buf.xn`` already holds the normalised input (layer 0, whose
+        RMSNorm is fused with the embedding gather); otherwise the RMSNorm runs
+        inside the qkv linear."""
         c, w = self.cfg, self.w
-        if not normed:
-            ops.rmsnorm(buf.x, w.ln1, c.eps, out=buf.xn)
-        ops.linear(buf.xn, w.qkv, out=buf.qkv)
+        if normed:
+            ops.linear(buf.xn, w.qkv, out=buf.qkv)
+        else:
+            ops.rmsnorm_linear(buf.x, w.ln1, c.eps, w.qkv, out=buf.qkv)
         ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, self.rope,
                              k_cache, v_cache, rope_style=self.rope_style, out=buf.ctx, workspace=buf.workspace)
         ops.linear(buf.ctx, w.o, residual=buf.x, out=buf.x)
 
     def mlp_half(self, buf: DecodeBuffers):
         c, w = self.cfg, self.w
-        ops.rmsnorm(buf.x, w.ln2, c.eps, out=buf.xn)
-        ops.gate_up(buf.xn, w.gate_up, swiglu=True, out=buf.hmlp)
+        ops.rmsnorm_gate_up(buf.x, w.ln2, c.eps, w.gate_up, swiglu=True, out=buf.hmlp)
         ops.linear(buf.hmlp, w.down, residual=buf.x, out=buf.x)
 
     def __call__(self, buf: DecodeBuffers, positions, k_cache, v_cache, normed: bool = False):

@@ -157,11 +157,12 @@ class _NormedProjection:
     out_features: int
     rows: int = 1
     rms_norm_epsilon: float = 1e-6
-    _xn: torch.Tensor | None = field(default=None, repr=False)
 
     def __post_init__(self):
         if self.in_features % 128 != 0:
             raise ValueError("in_features must be divisible by 128")
+        if self.in_features > 4096:
+            raise ValueError("in_features must be at most 4096 for the fused RMSNorm")
         if self.out_features % 64 != 0:
             raise ValueError("out_features must be divisible by 64")
         if not 1 <= self.rows <= 64:
@@ -169,16 +170,10 @@ class _NormedProjection:
         if self.rms_norm_epsilon <= 0:
             raise ValueError("rms_norm_epsilon must be positive")
 
-    def _normed(self, hidden, norm_weight):
-        if self._xn is None or self._xn.device != hidden.device:
-            self._xn = torch.empty(self.rows, self.in_features, dtype=BF16, device=hidden.device)
-        return ops.rmsnorm(hidden.view(self.rows, self.in_features), norm_weight, self.rms_norm_epsilon,
-                           out=self._xn)
-
 
 @dataclass
 class Qwen3FusedQKVProjection(_NormedProjection):
-    """RMSNorm + fused q|k|v projection: out [rows, (Hq + 2 Hkv) * D]."""
+    """RMSNorm + fused q|k|v projection in one kernel: out [rows, (Hq + 2 Hkv) * D]."""
 
     def get_arg_spec(self):
         return [ArgSpec("in", (self.rows, self.in_features), BF16), ArgSpec("in", (self.in_features,), BF16),
@@ -187,12 +182,13 @@ class Qwen3FusedQKVProjection(_NormedProjection):
 
     def __call__(self, hidden, norm_weight, W_qkv: W4A16Weight, out):
         _check_weight(W_qkv, self.in_features, self.out_features)
-        return ops.linear(self._normed(hidden, norm_weight), W_qkv, out=out)
+        return ops.rmsnorm_linear(hidden.view(self.rows, self.in_features), norm_weight, self.rms_norm_epsilon,
+                                  W_qkv, out=out)
 
 
 @dataclass
 class Qwen3FusedUpGateProjection(_NormedProjection):
-    """RMSNorm + fused gate|up projection with the SwiGLU epilogue:
+    """RMSNorm + fused gate|up projection with the SwiGLU epilogue, in one kernel:
     out [rows, out_features] = silu(gate) * up, out_features = intermediate size."""
 
     def get_arg_spec(self):
@@ -202,7 +198,8 @@ class Qwen3FusedUpGateProjection(_NormedProjection):
 
     def __call__(self, hidden, norm_weight, W_up_gate: W4A16Weight, out):
         _check_weight(W_up_gate, self.in_features, 2 * self.out_features)
-        return ops.gate_up(self._normed(hidden, norm_weight), W_up_gate, swiglu=True, out=out)
+        return ops.rmsnorm_gate_up(hidden.view(self.rows, self.in_features), norm_weight, self.rms_norm_epsilon,
+                                   W_up_gate, swiglu=True, out=out)
 
 
 @dataclass

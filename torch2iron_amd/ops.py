@@ -128,6 +128,58 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
     return out if swiglu else (out, out_up)
 
 
+def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: W4A16Weight,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y = rmsnorm(x) @ W^T`` with the RMSNorm done inside the linear kernel
+    (``x`` bf16 ``[M, K]`` is the un-normalised residual stream, 1 <= M <= 64, K <= 4096)."""
+    _check_weight(w)
+    _check_dev("x", x, BF16)
+    _check_dev("norm_weight", norm_weight, BF16)
+    x2 = x.view(1, -1) if x.dim() == 1 else x
+    if x2.dim() != 2 or x2.shape[1] != w.K or norm_weight.numel() != w.K:
+        raise ValueError(f"x shape {tuple(x.shape)} / norm_weight do not match K={w.K}")
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty(m, w.N, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != m * w.N:
+        raise ValueError(f"out must hold {m}x{w.N} elements")
+    lib = _lib.load()
+    rc = lib.t2i_w4a16_rmsnorm_linear(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps), w.qweight.data_ptr(),
+                                      w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N, w.group_size,
+                                      out.data_ptr(), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_w4a16_rmsnorm_linear")
+    return out.view(m, w.N) if x.dim() != 1 else out.view(-1)
+
+
+def rmsnorm_gate_up(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_pair: W4A16Weight,
+                    swiglu: bool = True, out: torch.Tensor | None = None, out_up: torch.Tensor | None = None):
+    """RMSNorm fused into the paired gate/up projection (see ``gate_up``)."""
+    _check_weight(w_pair)
+    _check_dev("x", x, BF16)
+    _check_dev("norm_weight", norm_weight, BF16)
+    x2 = x.view(1, -1) if x.dim() == 1 else x
+    if x2.dim() != 2 or x2.shape[1] != w_pair.K or norm_weight.numel() != w_pair.K:
+        raise ValueError(f"x shape {tuple(x.shape)} / norm_weight do not match K={w_pair.K}")
+    m, inter = x2.shape[0], w_pair.N // 2
+    if out is None:
+        out = torch.empty(m, inter, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != m * inter:
+        raise ValueError(f"out must hold {m}x{inter} elements")
+    if not swiglu:
+        if out_up is None:
+            out_up = torch.empty(m, inter, dtype=BF16, device=x.device)
+        _check_dev("out_up", out_up, BF16)
+    lib = _lib.load()
+    rc = lib.t2i_w4a16_rmsnorm_gate_up(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps),
+                                       w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(), w_pair.scales.data_ptr(),
+                                       w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)), out.data_ptr(),
+                                       _lib.ptr(out_up), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_w4a16_rmsnorm_gate_up")
+    return out if swiglu else (out, out_up)
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
             tokens: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
             argmax_keys: torch.Tensor | None = None) -> torch.Tensor:
