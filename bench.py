@@ -35,6 +35,17 @@ PEAK_GBPS = 8000.0
 QWEN3_06B = [("qkv", 1024, 4096), ("o_proj", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)]
 QWEN3_17B = [("qkv", 2048, 4096), ("o_proj", 2048, 2048), ("gate_up", 2048, 12288), ("down", 6144, 2048)]
 MALL_BYTES = 256 << 20
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = ROOT / "profiles" / "w4a16_linear_qwen3_0.6b_sweep_traffic.json"
+
+
+def measured_traffic():
+    """HBM bytes per launch of the sweep's linear kernel, from the FETCH_SIZE /
+    WRITE_SIZE counter runs summarised in ``TRAFFIC_FILE`` (None if absent)."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
 
 
 def log(msg: str) -> None:
@@ -55,13 +66,16 @@ def parse():
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--streams", default="1,2", help="micro-batch stream counts to measure for batch decode")
+    ap.add_argument("--eager", action="store_true", help="sweep launches without graphs (for counter collection)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="also run a 256 MiB device copy (the reference kernel for HBM byte counters)")
     return ap.parse_args()
 
 
 class Sweep:
     """Graph-captured launches of one (M, shape) grid over a weight pool."""
 
-    def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None):
+    def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None, eager=False):
         import torch
         from torch2iron_amd import ops
         from torch2iron_amd.formats import algorithmic_bytes, random_weight_on_device
@@ -75,18 +89,28 @@ class Sweep:
                         for name, k, n in shapes}
         # launches per graph: one per weight copy (HBM-cold), or ``reps`` of the one copy (MALL-warm)
         self.reps = reps or self.copies
+        self.eager = eager
         self.groups = []   # (label, M, K, N, graph, bytes, launches)
         for m in ms:
             for name, k, n in shapes:
                 x = torch.randn(m, k, generator=gen, device=dev).to(torch.bfloat16)
                 y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-                ops.linear(x, self.weights[name][0], out=y)
+                ws = [self.weights[name][i % self.copies] for i in range(self.reps)]
+                ops.linear(x, ws[0], out=y)
                 torch.cuda.synchronize()
-                g = torch.cuda.CUDAGraph()
-                with torch.cuda.graph(g):
-                    for i in range(self.reps):
-                        ops.linear(x, self.weights[name][i % self.copies], out=y)
-                self.groups.append(dict(label=f"{name}/M{m}", M=m, K=k, N=n, graph=g, x=x, y=y,
+
+                def launch_all(x=x, y=y, ws=ws):
+                    for w in ws:
+                        ops.linear(x, w, out=y)
+
+                if eager:
+                    replay = launch_all
+                else:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g):
+                        launch_all()
+                    replay = g.replay
+                self.groups.append(dict(label=f"{name}/M{m}", M=m, K=k, N=n, replay=replay, x=x, y=y,
                                         bytes=algorithmic_bytes(m, k, n) * self.reps, launches=self.reps))
         self.bytes_per_step = sum(gr["bytes"] for gr in self.groups)
         self.launches_per_step = sum(gr["launches"] for gr in self.groups)
@@ -95,14 +119,14 @@ class Sweep:
         torch = self.torch
         for _ in range(warmup):
             for gr in self.groups:
-                gr["graph"].replay()
+                gr["replay"]()
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         marks = [[torch.cuda.Event(enable_timing=True) for _ in self.groups] for _ in range(steps)]
         start.record()
         for s in range(steps):
             for i, gr in enumerate(self.groups):
-                gr["graph"].replay()
+                gr["replay"]()
                 marks[s][i].record()
         torch.cuda.synchronize()
         total_ms = start.elapsed_time(marks[-1][-1])
@@ -294,7 +318,7 @@ def main():
 
     ms = [1, 8, 16, 32, 64]
     log(f"building HBM-cold sweep (pool {args.pool_mb} MB)")
-    cold = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1)
+    cold = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1, eager=args.eager)
     log(f"{cold.copies} weight copies, {cold.launches_per_step} launches/step, "
         f"{cold.bytes_per_step / 1e6:.1f} MB/step")
     total_ms, per_group = cold.run(args.steps, args.warmup)
@@ -308,6 +332,14 @@ def main():
     for gr, t in zip(cold.groups, per_group):
         breakdown[gr["label"]] = {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
                                   "us_per_launch": round(t * 1e3 / gr["launches"], 3)}
+
+    if args.calibrate_copy:
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     extra = {}
     if not args.skip_extra:
@@ -341,6 +373,7 @@ def main():
             cpu["decode"] = cpu_decode_baseline(tensors, args.cpu_seconds, args.batch)
 
     achieved_gbps = value * 1e3
+    traffic = measured_traffic()
     line = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -368,7 +401,8 @@ def main():
             "peak": PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved_gbps / PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": (traffic or {}).get("hbm_bytes_per_launch"),
+            "traffic_source": (traffic or {}).get("source"),
             "kernel": "w4a16_mfma_kernel",
             "avg_launch_us": round(avg_launch_us, 3),
         },

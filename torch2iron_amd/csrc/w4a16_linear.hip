@@ -326,6 +326,16 @@ __device__ __forceinline__ void norm_prologue(const LinearParams& p, int mbase, 
   }
 }
 
+// Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
+// its own L2.  Neighbouring column blocks share 128-byte lines of qweight,
+// scales and qzeros, so the blocks are renumbered to give each XCD one
+// contiguous range of them: a shared line is then fetched from HBM once, not
+// once per XCD.  (With G a multiple of 8 the row-tile index in grid.z keeps
+// the XCD, so the row tiles of a column block share its weights in one L2.)
+__device__ __forceinline__ int xcd_block(int b, int G) {
+  return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
+}
+
 template <int MT, int LW, int W, int CK, bool NORM>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p) {
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
@@ -334,7 +344,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
   const int wave = threadIdx.x >> 6;
   const int c = lane & 15;
   const int r = lane >> 4;
-  const int ncol = blockIdx.x * (16 * LW) + LW * c;
+  const int ncol = xcd_block(blockIdx.x, gridDim.x) * (16 * LW) + LW * c;
   const int zshift = (ncol & 7) * 4;
   const int mbase = blockIdx.z * (16 * MT);   // row tile of this workgroup
 
