@@ -192,64 +192,58 @@ __device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float 
   }
 }
 
-template <int MT, int LW>
-__device__ __forceinline__ void epilogue(const LinearParams& p, int ncol, int r, int mbase,
-                                         const float (&total)[MT][LW][4]) {
+// Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32 sums v.
+template <int LW>
+__device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW]) {
+  if (m >= p.M) return;
+  if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
+    float v[LW];
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi)
+    for (int t = 0; t < LW; ++t) v[t] = v_in[t];
+    if (p.epi == EPI_RESIDUAL) {
+      const uint16_t* res = p.residual + (size_t)m * p.ldy + ncol;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = mbase + mi * 16 + r * 4 + i;
-      if (m >= p.M) continue;
-      if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
-        float v[LW];
+      for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32(res[t]);
+    }
+    uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
+    if constexpr (LW == 1) {
+      dst[0] = (uint16_t)f32_to_bf16(v[0]);
+    } else {
+      uint32_t packed[LW / 2];
 #pragma unroll
-        for (int t = 0; t < LW; ++t) v[t] = total[mi][t][i];
-        if (p.epi == EPI_RESIDUAL) {
-          const uint16_t* res = p.residual + (size_t)m * p.ldy + ncol;
+      for (int j = 0; j < LW / 2; ++j) packed[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+      if constexpr (LW == 8) *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+      else if constexpr (LW == 4) *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
+      else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+    }
+  } else if constexpr (LW >= 2) {
+    // fused column 2q = gate q, 2q + 1 = up q
+    float o0[LW / 2], o1[LW / 2];
 #pragma unroll
-          for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32(res[t]);
-        }
-        uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
-        if constexpr (LW == 1) {
-          dst[0] = (uint16_t)f32_to_bf16(v[0]);
-        } else {
-          uint32_t packed[LW / 2];
-#pragma unroll
-          for (int j = 0; j < LW / 2; ++j) packed[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
-          if constexpr (LW == 8) *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
-          else if constexpr (LW == 4) *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
-          else *reinterpret_cast<uint32_t*>(dst) = packed[0];
-        }
-      } else if constexpr (LW >= 2) {
-        // fused column 2q = gate q, 2q + 1 = up q
-        float o0[LW / 2], o1[LW / 2];
-#pragma unroll
-        for (int q = 0; q < LW / 2; ++q) {
-          const float g = round_bf16(total[mi][2 * q][i]);
-          const float u = round_bf16(total[mi][2 * q + 1][i]);
-          if (p.epi == EPI_SWIGLU) {
-            o0[q] = round_bf16(silu_f32(g)) * u;
-            o1[q] = 0.0f;
-          } else {
-            o0[q] = g;
-            o1[q] = u;
-          }
-        }
-        const size_t off = (size_t)m * p.ldy + (ncol >> 1);
-        if constexpr (LW == 8) {
-          *reinterpret_cast<u32x2*>(p.y0 + off) = u32x2{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3])};
-          if (p.epi == EPI_PAIRED)
-            *reinterpret_cast<u32x2*>(p.y1 + off) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
-        } else if constexpr (LW == 4) {
-          *reinterpret_cast<uint32_t*>(p.y0 + off) = pack_bf16x2(o0[0], o0[1]);
-          if (p.epi == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = pack_bf16x2(o1[0], o1[1]);
-        } else {
-          p.y0[off] = (uint16_t)f32_to_bf16(o0[0]);
-          if (p.epi == EPI_PAIRED) p.y1[off] = (uint16_t)f32_to_bf16(o1[0]);
-        }
+    for (int q = 0; q < LW / 2; ++q) {
+      const float g = round_bf16(v_in[2 * q]);
+      const float u = round_bf16(v_in[2 * q + 1]);
+      if (p.epi == EPI_SWIGLU) {
+        o0[q] = round_bf16(silu_f32(g)) * u;
+        o1[q] = 0.0f;
+      } else {
+        o0[q] = g;
+        o1[q] = u;
       }
     }
+    const size_t off = (size_t)m * p.ldy + (ncol >> 1);
+    if constexpr (LW == 8) {
+      *reinterpret_cast<u32x2*>(p.y0 + off) = u32x2{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3])};
+      if (p.epi == EPI_PAIRED)
+        *reinterpret_cast<u32x2*>(p.y1 + off) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+    } else if constexpr (LW == 4) {
+      *reinterpret_cast<uint32_t*>(p.y0 + off) = pack_bf16x2(o0[0], o0[1]);
+      if (p.epi == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = pack_bf16x2(o1[0], o1[1]);
+    } else {
+      p.y0[off] = (uint16_t)f32_to_bf16(o0[0]);
+      if (p.epi == EPI_PAIRED) p.y1[off] = (uint16_t)f32_to_bf16(o1[0]);
+    }
+  }
 }
 
 // Fused RMSNorm prologue.  Wave w takes k-steps w, w + W, ...; for k-step ks
@@ -382,38 +376,47 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
     }
   }
 
-  // ---- reduce the waves of this workgroup in LDS (fixed tree) ----
+  // ---- reduce the waves of this workgroup in LDS: one barrier, fixed order ----
+  // Every wave that had chunks parks its sums; then wave 4 mi + i adds row i of
+  // m-tile mi over the waves in wave order and stores it.
+  const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
   if constexpr (W > 1) {
-    __shared__ float red_static[NORM ? 1 : (W / 2) * E * 64];
+    static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
+    __shared__ float red_static[NORM ? 1 : W * E * 64];
     float* red = NORM ? reinterpret_cast<float*>(dyn_lds) : red_static;
     if constexpr (NORM) __syncthreads();   // every wave is done with the normalised rows
+    if (wave < nw) {
+      float* dst = red + wave * E * 64 + lane;
 #pragma unroll
-    for (int half = W / 2; half >= 1; half >>= 1) {
-      if (wave >= half && wave < 2 * half) {
-        float* dst = red + (wave - half) * E * 64 + lane;
+      for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-        for (int mi = 0; mi < MT; ++mi)
+        for (int t = 0; t < LW; ++t)
 #pragma unroll
-          for (int t = 0; t < LW; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
-      }
-      __syncthreads();
-      if (wave < half) {
-        const float* src = red + wave * E * 64 + lane;
-#pragma unroll
-        for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-          for (int t = 0; t < LW; ++t)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) total[mi][t][i] += src[((mi * LW + t) * 4 + i) * 64];
-      }
-      __syncthreads();
+          for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
     }
+    __syncthreads();
+    if (wave >= 4 * MT) return;
+    const int mi = wave >> 2, i = wave & 3;
+    float v[LW];
+#pragma unroll
+    for (int t = 0; t < LW; ++t) v[t] = 0.0f;
+    for (int w = 0; w < nw; ++w) {
+      const float* src = red + w * E * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < LW; ++t) v[t] += src[((mi * LW + t) * 4 + i) * 64];
+    }
+    store_row<LW>(p, ncol, mbase + mi * 16 + r * 4 + i, v);
+  } else {
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v[LW];
+#pragma unroll
+        for (int t = 0; t < LW; ++t) v[t] = total[mi][t][i];
+        store_row<LW>(p, ncol, mbase + mi * 16 + r * 4 + i, v);
+      }
   }
-  if (wave != 0) return;
-
-  epilogue<MT, LW>(p, ncol, r, mbase, total);
 }
 
 __global__ void dequant_f32_kernel(const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
@@ -449,9 +452,9 @@ using t2i_host::fail;
 // on every Qwen3 shape at M = 32 and 64).
 #define T2I_LINEAR_CONFIGS(X) \
   X(1, 1, 16, 4)              \
+  X(1, 1, 16, 2)              \
   X(1, 2, 16, 4)              \
   X(1, 2, 8, 4)               \
-  X(1, 4, 16, 2)              \
   X(1, 4, 8, 4)               \
   X(1, 4, 4, 4)               \
   X(1, 8, 4, 4)
@@ -476,22 +479,25 @@ void finish_plan(Plan& pl, int M, int K, int N) {
   pl.chunks = K / (32 * pl.CK);
 }
 
-// Tile choice, from an HBM-cold sweep over the Qwen3-0.6B/1.7B linear shapes
-// at M in {1, 8, 16, 32, 64}: one 16-row tile per workgroup (more rows go to
-// grid.z and share the weights through L2), and column blocks sized so that
-// the column-tile x row-tile count gives a few hundred workgroups.  Splitting
-// K across workgroups (fp32 partials + an arrival counter) was measured
-// slower at every one of these shapes: its extra memory round trips cost more
-// than the parallelism it adds, so K is only split between the waves of a
-// workgroup.
+// Tile choice, from an HBM-cold sweep (graph-launched, 42-300 weight copies)
+// of every Qwen3-0.6B / 1.7B linear shape at M in {1, 8, 16, 32, 64} over all
+// compiled plans: one 16-row tile per workgroup (more rows go to grid.z and
+// share the weights in their XCD's L2), and the narrowest column block that
+// keeps the column-block x row-tile count at 256 or less: 16 columns (1 word
+// per lane, 16 waves, chunks of 2 k-steps), else 32 (2 words, 8 waves), else
+// 64 (4 words, 8 waves).  The rule picks the measured optimum, or a plan
+// within 4 % of it, at 38 of the 40 shape/M points, and is within 9 % at all.  Splitting K across workgroups was measured slower:
+// the fp32 partials and an arrival counter add memory round trips that cost
+// more than the parallelism they add at these sizes, so K is only split
+// between the waves of a workgroup.
 Plan plan_linear(int M, int K, int N, bool paired) {
   Plan pl{};
   pl.MT = 1;
   pl.CK = 4;
   const int mz = (M + 15) / 16;
-  if (((N / 16) * mz <= 256 || N % 32) && !paired) {
-    pl.LW = 1; pl.W = 16;
-  } else if ((N / 32) * mz <= (mz >= 4 ? 384 : 768) || N % 64) {
+  if ((N / 16) * mz <= 256 && !paired) {
+    pl.LW = 1; pl.W = 16; pl.CK = 2;
+  } else if ((N / 32) * mz <= 256 || N % 64) {
     pl.LW = 2; pl.W = 8;
   } else {
     pl.LW = 4; pl.W = 8;
@@ -513,7 +519,7 @@ Plan plan_linear(int M, int K, int N, bool paired) {
 // wave reduction.
 size_t norm_lds_bytes(const Plan& pl, int K) {
   const size_t rows = (size_t)K * 32 + (size_t)K * 2;                  // K / 32 k-steps x 1 KB + norm weight
-  const size_t red = (size_t)(pl.W / 2) * pl.MT * pl.LW * 4 * 64 * sizeof(float);
+  const size_t red = (size_t)pl.W * pl.MT * pl.LW * 4 * 64 * sizeof(float);
   return rows > red ? rows : red;
 }
 
