@@ -34,7 +34,8 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 2
+#define T2I_ABI_VERSION 3
+#define T2I_MAX_ROWS (65535 * 16)   /* rows of one linear call: 16-row tiles in grid.z */
 
 #define T2I_OK 0
 #define T2I_ERR_NULL (-1)      /* a required pointer is NULL */
@@ -60,7 +61,8 @@ int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,
 
 /* ---------------------------------------------------------------------------
  * W4A16 linear: y[M, N] = x[M, K] . W^T, fp32 accumulation, bf16 output.
- * 1 <= M <= 64; K % 128 == 0; N % 64 == 0.  M = 1 is the GEMV case.
+ * 1 <= M <= T2I_MAX_ROWS; K % 128 == 0; N % 64 == 0.  M = 1 is the GEMV case,
+ * M up to 64 the batched decode, larger M a prompt (prefill) batch.
  * residual (nullable, may alias y): y = bf16(bf16(x.W^T) + residual).
  * Replaces: quantized_qwen3/operators/w4a16_gemv/op.py:22-126 (W4A16GEMV, M = 1)
  *           quantized_qwen3/operators/w4a16_gemm/op.py:23-174, 267-333
@@ -141,6 +143,31 @@ int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t 
                          uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
                          uint16_t* ctx, void* workspace, size_t workspace_bytes,
                          void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Prompt (prefill) attention, every prompt row of B sequences at once.  Rows of
+ * qkv are b * T + t for prompt token t of sequence b at position p0 + t.
+ *
+ * t2i_prefill_qk_rope_kv: per-head q/k RMSNorm + RoPE (as t2i_decode_attention's
+ * prologue) of every row; q_out bf16 [B, Hq, T, D]; k and v written to
+ * k_cache / v_cache [B, Hkv, ctx_cap, D] at positions p0 .. p0 + T - 1.
+ *
+ * t2i_prefill_attention: causal GQA attention of those rows over cache slots
+ * 0 .. p0 + t (slots before p0 hold an earlier prompt chunk); fp32 scores and
+ * online softmax, softmax weights rounded to bf16 for the product with V (as
+ * quantized_qwen3/model.py:277 in bf16 compute); out bf16 [B * T, Hq * D].
+ * D = 128; Hq / Hkv in {1, 2, 4, 8}; p0 + T <= ctx_cap.
+ * Replaces: the prompt pass of quantized_qwen3/model.py:453-478 (causal mask
+ *           271-275) and the NPU prefill runtime quantized_qwen3/prefill_runtime.py:95-164
+ *           with torch2iron/operators/llama_chunked_prefill_attention.
+ */
+int t2i_prefill_qk_rope_kv(const uint16_t* qkv, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
+                           int32_t D, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                           const uint16_t* rope, int32_t rope_style, uint16_t* q_out,
+                           uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, void* stream);
+int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
+                          int32_t D, const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap,
+                          uint16_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Tied bf16 lm_head with a fused greedy argmax.

@@ -28,13 +28,13 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.t2i_abi_version() == 2
+    assert lib.t2i_abi_version() == 3
     assert lib.t2i_strerror(-2) == b"unsupported shape"
 
 
 @pytest.mark.parametrize("M,K,N,group,x,code", [
     (0, 1024, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
-    (65, 1024, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
+    (65535 * 16 + 1, 1024, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
     (1, 1000, 3072, 128, FAKE, _lib.T2I_ERR_SHAPE),
     (1, 1024, 3000, 128, FAKE, _lib.T2I_ERR_SHAPE),
     (1, 1024, 3072, 64, FAKE, _lib.T2I_ERR_GROUP),
@@ -64,11 +64,35 @@ def test_fused_norm_entry_points_validate():
     assert f(FAKE, 16, None, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_NULL
     assert f(FAKE, 16, FAKE, 0.0, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_VALUE
     assert f(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 8192, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
-    assert f(FAKE, 65, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert f(FAKE, 0, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert f(FAKE + 2, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_ALIGN
     g = lib.t2i_w4a16_rmsnorm_gate_up
     assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None) == _lib.T2I_ERR_NULL
     assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 64, 1, FAKE, None, None) == _lib.T2I_ERR_GROUP
+
+
+def test_prefill_entry_points_validate():
+    lib = _lib.load()
+    prep = lib.t2i_prefill_qk_rope_kv
+    args = [FAKE, 2, 100, 0, 16, 8, 128, FAKE, FAKE, 1e-6, FAKE, 0, FAKE, FAKE, FAKE, 640, None]
+    a = list(args); a[6] = 64
+    assert prep(*a) == _lib.T2I_ERR_SHAPE                       # head_dim 64
+    a = list(args); a[3] = 600
+    assert prep(*a) == _lib.T2I_ERR_SHAPE                       # positions 600..699 beyond the 640-slot cache
+    a = list(args); a[11] = 2
+    assert prep(*a) == _lib.T2I_ERR_VALUE                       # rope style
+    a = list(args); a[12] = None
+    assert prep(*a) == _lib.T2I_ERR_NULL
+    att = lib.t2i_prefill_attention
+    args = [FAKE, 2, 100, 0, 16, 8, 128, FAKE, FAKE, 640, FAKE, None]
+    a = list(args); a[4] = 12
+    assert att(*a) == _lib.T2I_ERR_SHAPE                        # 12 q heads over 8 kv heads
+    a = list(args); a[4], a[5] = 32, 2
+    assert att(*a) == _lib.T2I_ERR_SHAPE                        # 16 q heads per kv head
+    a = list(args); a[10] = FAKE + 2
+    assert att(*a) == _lib.T2I_ERR_ALIGN
+    a = list(args); a[2], a[3] = 700, 0
+    assert att(*a) == _lib.T2I_ERR_SHAPE
 
 
 def test_other_entry_points_validate():

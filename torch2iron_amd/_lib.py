@@ -43,6 +43,11 @@ SIGNATURES = {
     "t2i_decode_attention": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                        c_float, c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
                                        c_size_t, c_void_p]),
+    "t2i_prefill_qk_rope_kv": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                         c_void_p, c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p,
+                                         c_void_p, c_int32, c_void_p]),
+    "t2i_prefill_attention": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                        c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "t2i_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_greedy_advance": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "t2i_prompt_advance": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),

@@ -1,0 +1,314 @@
+// Prompt (prefill) kernels for gfx950: every prompt row of a batch at once.
+//
+//   * t2i_prefill_qk_rope_kv: per-head q/k RMSNorm + RoPE of every prompt row,
+//     q stored per (sequence, head) for the attention, k and v written into the
+//     contiguous KV cache at their positions;
+//   * t2i_prefill_attention: causal GQA attention of the prompt rows over the
+//     cache on MFMA (flash-attention style: 64-key blocks through LDS, an online
+//     softmax per query row, P . V on MFMA), bf16 context out.
+//
+// Rounding follows the decode path (and the reference runtime in bf16
+// compute, quantized_qwen3/model.py:246-253, 268-280): q/k norm and RoPE round
+// at the same points; scores and softmax are fp32; the softmax weights enter
+// the P . V product as bf16 (model.py:277 casts them to the compute dtype
+// before that product), and each row's normaliser sums those bf16 weights.
+#include <math.h>
+
+#include "t2i_common.h"
+
+namespace t2i {
+
+constexpr int PF_D = 128;
+
+// ============================================================================
+// q/k RMSNorm + RoPE + KV-cache write for every prompt row
+// ============================================================================
+struct PrefillPrepParams {
+  const uint16_t* qkv;    // [B*T, (Hq + 2 Hkv) * D] raw projection, row b*T + t
+  const uint16_t* qn;
+  const uint16_t* kn;
+  const uint16_t* rope;   // [>= p0 + T, D] cos even / sin odd
+  uint16_t* q;            // [B, Hq, T, D]
+  uint16_t* kc;           // [B, Hkv, cap, D]
+  uint16_t* vc;
+  int B, T, Hq, Hkv, cap, p0, style;
+  float eps;
+};
+
+// One workgroup (4 waves) per prompt row; wave w takes vectors w, w + 4, ...
+// of the row's Hq + 2 Hkv heads; a lane holds the rotation pair (i0, i1).
+__global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepParams p) {
+  constexpr int D = PF_D;
+  const int row = blockIdx.x;
+  const int b = row / p.T;
+  const int t = row - b * p.T;
+  const int pos = p.p0 + t;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nvec = p.Hq + 2 * p.Hkv;
+  const int i0 = p.style == 0 ? lane : 2 * lane;
+  const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
+  const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
+  const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+  const uint16_t* src_row = p.qkv + (size_t)row * nvec * D;
+  for (int vi = wave; vi < nvec; vi += 4) {
+    const uint16_t* src = src_row + (size_t)vi * D;
+    float x0 = bf16_to_f32(src[i0]);
+    float x1 = bf16_to_f32(src[i1]);
+    uint16_t* dst;
+    if (vi < p.Hq + p.Hkv) {
+      const uint16_t* gamma = vi < p.Hq ? p.qn : p.kn;
+      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+      x0 = round_bf16(round_bf16(x0 * inv) * bf16_to_f32(gamma[i0]));
+      x1 = round_bf16(round_bf16(x1 * inv) * bf16_to_f32(gamma[i1]));
+      const float y0 = round_bf16(round_bf16(x0 * cs) + round_bf16(-x1 * sn));
+      const float y1 = round_bf16(round_bf16(x1 * cs) + round_bf16(x0 * sn));
+      x0 = y0;
+      x1 = y1;
+      if (vi < p.Hq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
+      else dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
+    } else {
+      dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
+    }
+    dst[i0] = (uint16_t)f32_to_bf16(x0);
+    dst[i1] = (uint16_t)f32_to_bf16(x1);
+  }
+}
+
+// ============================================================================
+// causal GQA flash attention over the cache
+// ============================================================================
+constexpr int PF_ROWS = 64;                 // query rows per workgroup (over the kv head's q heads)
+constexpr int PF_KEYS = 64;                 // keys per block
+constexpr int PF_KLD = PF_D + 8;            // K tile row stride (bf16): 272 bytes
+constexpr int PF_VLD = PF_KEYS + 8;         // transposed V tile row stride: 144 bytes
+constexpr int PF_PLD = PF_KEYS + 8;         // P tile row stride
+
+struct PrefillAttnParams {
+  const uint16_t* q;      // [B, Hq, T, D]
+  const uint16_t* kc;     // [B, Hkv, cap, D]
+  const uint16_t* vc;
+  uint16_t* out;          // [B*T, Hq * D]
+  int B, T, Hq, Hkv, cap, p0;
+  float scale_log2;       // D^-1/2 * log2(e)
+};
+
+// One workgroup per (query block, kv head h, sequence b); 4 waves of 16 query
+// rows.  Row j of the 64 is q head h * Q + j / BQ at prompt row t0 + j % BQ
+// (BQ = 64 / Q), so the q heads sharing kv head h share every K / V block.
+//   S = Q K^T: A = q rows (registers, 4 k-steps of 32 dims), B = K from LDS;
+//   online softmax per row in fp32 (rows 4r + i of the lane's MFMA output);
+//   O += P V: P goes to A layout through a per-wave LDS tile, B = V^T from LDS.
+template <int Q>
+__global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAttnParams p) {
+  constexpr int D = PF_D;
+  constexpr int BQ = PF_ROWS / Q;           // prompt rows per q head in the tile
+  const int t0 = blockIdx.x * BQ;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int c = lane & 15;
+  const int r = lane >> 4;
+
+  __shared__ __align__(16) uint16_t s_k[PF_KEYS * PF_KLD];     // [key][dim]
+  __shared__ __align__(16) uint16_t s_vt[D * PF_VLD];          // [dim][key]
+  __shared__ __align__(16) uint16_t s_p[4][16 * PF_PLD];       // per wave [row][key]
+
+  // ---- the wave's 16 query rows as A operands (row c of the wave) ----
+  const int jrow_a = wave * 16 + c;
+  const int t_a = t0 + jrow_a % BQ;
+  const int head_a = h * Q + jrow_a / BQ;
+  u32x4 qa[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    qa[ks] = u32x4{0u, 0u, 0u, 0u};
+    if (t_a < p.T)
+      qa[ks] = *reinterpret_cast<const u32x4*>(p.q + (((size_t)b * p.Hq + head_a) * p.T + t_a) * D + ks * 32 + 8 * r);
+  }
+  // the rows this lane holds in MFMA outputs: 4r + i of the wave
+  int qpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = wave * 16 + 4 * r + i;
+    qpos[i] = p.p0 + t0 + j % BQ;            // absolute query position (masks keys beyond it)
+  }
+  const int last_t = min(t0 + BQ, p.T) - 1;
+  const int kend = p.p0 + last_t + 1;        // keys [0, kend) can be attended
+  const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.cap * D;
+
+  float m[4], l[4];
+  f32x4 o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.0f; }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per thread
+  auto load_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q16 = tid + 256 * u;        // chunk: key q16 / 16, dims 8 * (q16 % 16)
+      const int key = kb * PF_KEYS + (q16 >> 4);
+      kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
+      if (key < kend) {
+        kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)key * D + 8 * (q16 & 15));
+        vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)key * D + 8 * (q16 & 15));
+      }
+    }
+  };
+  auto store_block = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q16 = tid + 256 * u;
+      const int key = q16 >> 4, d0 = 8 * (q16 & 15);
+      *reinterpret_cast<u32x4*>(s_k + key * PF_KLD + d0) = kr[u];
+      const uint32_t w[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s_vt[(d0 + 2 * e) * PF_VLD + key] = (uint16_t)(w[e] & 0xFFFFu);
+        s_vt[(d0 + 2 * e + 1) * PF_VLD + key] = (uint16_t)(w[e] >> 16);
+      }
+    }
+  };
+
+  const int nblocks = (kend + PF_KEYS - 1) / PF_KEYS;
+  u32x4 kr[4], vr[4];
+  load_block(0, kr, vr);
+  for (int kb = 0; kb < nblocks; ++kb) {
+    __syncthreads();                          // the previous block's tiles are consumed
+    store_block(kr, vr);
+    __syncthreads();
+    if (kb + 1 < nblocks) load_block(kb + 1, kr, vr);   // next block in flight during this one
+
+    // ---- S = Q K^T for 4 key tiles of 16 ----
+    f32x4 s[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 kb16 = *reinterpret_cast<const u32x4*>(s_k + (n * 16 + c) * PF_KLD + ks * 32 + 8 * r);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[ks]),
+                                                       __builtin_bit_cast(bf16x8, kb16), s[n], 0, 0, 0);
+      }
+    }
+    // ---- online softmax (log2 domain), causal mask ----
+    float pv[4][4];   // [i][n]
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int key = kb * PF_KEYS + n * 16 + c;
+        const float v = key <= qpos[i] ? s[n][i] * p.scale_log2 : -INFINITY;
+        pv[i][n] = v;
+        mx = fmaxf(mx, v);
+      }
+      mx = row_max16(mx);
+      const float mn = fmaxf(m[i], mx);
+      const float f = m[i] > -INFINITY ? exp2f(m[i] - mn) : 0.0f;
+      float sum = 0.0f;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const float e = pv[i][n] > -INFINITY ? round_bf16(exp2f(pv[i][n] - mn)) : 0.0f;
+        pv[i][n] = e;
+        sum += e;
+      }
+      sum = row_sum16(sum);
+      l[i] = l[i] * f + sum;
+      m[i] = mn;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) o[n][i] *= f;
+    }
+    // ---- P to A layout through the wave's LDS tile ----
+    uint16_t* pt = s_p[wave];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) pt[(4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): the wave's P writes are done
+    __builtin_amdgcn_wave_barrier();
+    // ---- O += P V: 2 k-steps of 32 keys, 8 dim tiles ----
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 pa = *reinterpret_cast<const u32x4*>(pt + c * PF_PLD + ks * 32 + 8 * r);
+#pragma unroll
+      for (int n = 0; n < 8; ++n) {
+        const u32x4 vb = *reinterpret_cast<const u32x4*>(s_vt + (n * 16 + c) * PF_VLD + ks * 32 + 8 * r);
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa),
+                                                       __builtin_bit_cast(bf16x8, vb), o[n], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds rows 4r + i, dims n * 16 + c ----
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = wave * 16 + 4 * r + i;
+    const int t = t0 + j % BQ;
+    if (t >= p.T) continue;
+    const int head = h * Q + j / BQ;
+    uint16_t* dst = p.out + ((size_t)b * p.T + t) * p.Hq * D + (size_t)head * D;
+    const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) dst[n * 16 + c] = (uint16_t)f32_to_bf16(o[n][i] * inv);
+  }
+}
+
+}  // namespace t2i
+
+// ============================================================================
+// host side
+// ============================================================================
+using t2i_host::aligned16;
+using t2i_host::fail;
+
+extern "C" int t2i_prefill_qk_rope_kv(const uint16_t* qkv, int32_t B, int32_t T, int32_t p0, int32_t Hq,
+                                      int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
+                                      float eps, const uint16_t* rope, int32_t rope_style, uint16_t* q_out,
+                                      uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, void* stream) {
+  if (!qkv || !q_norm || !k_norm || !rope || !q_out || !k_cache || !v_cache)
+    return fail(T2I_ERR_NULL, "prefill prep pointers must not be NULL");
+  if (D != t2i::PF_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
+  if (B < 1 || T < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(T2I_ERR_SHAPE, "B=%d T=%d Hq=%d Hkv=%d invalid", B, T, Hq, Hkv);
+  if (p0 < 0 || ctx_cap < 1 || p0 + T > ctx_cap) return fail(T2I_ERR_SHAPE, "positions %d..%d exceed the cache (%d)", p0, p0 + T - 1, ctx_cap);
+  if ((long long)B * T > 0x7FFFFFFF / 2) return fail(T2I_ERR_SHAPE, "B*T too large");
+  if (rope_style != 0 && rope_style != 1) return fail(T2I_ERR_VALUE, "rope_style must be 0 or 1");
+  if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  t2i::PrefillPrepParams p{};
+  p.qkv = qkv; p.qn = q_norm; p.kn = k_norm; p.rope = rope; p.q = q_out; p.kc = k_cache; p.vc = v_cache;
+  p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.cap = ctx_cap; p.p0 = p0; p.style = rope_style; p.eps = eps;
+  hipLaunchKernelGGL(t2i::prefill_prep_kernel, dim3(B * T), dim3(256), 0, reinterpret_cast<hipStream_t>(stream), p);
+  return t2i_host::hip_status(hipGetLastError(), "prefill prep launch");
+}
+
+extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
+                                     int32_t D, const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap,
+                                     uint16_t* out, void* stream) {
+  if (!q || !k_cache || !v_cache || !out) return fail(T2I_ERR_NULL, "prefill attention pointers must not be NULL");
+  if (D != t2i::PF_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
+  if (B < 1 || T < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(T2I_ERR_SHAPE, "B=%d T=%d Hq=%d Hkv=%d invalid", B, T, Hq, Hkv);
+  const int Q = Hq / Hkv;
+  if (Q != 1 && Q != 2 && Q != 4 && Q != 8) return fail(T2I_ERR_SHAPE, "Hq/Hkv=%d must be 1, 2, 4 or 8", Q);
+  if (p0 < 0 || ctx_cap < 1 || p0 + T > ctx_cap) return fail(T2I_ERR_SHAPE, "positions %d..%d exceed the cache (%d)", p0, p0 + T - 1, ctx_cap);
+  if (B > 65535 || Hkv > 65535) return fail(T2I_ERR_SHAPE, "B=%d or Hkv=%d exceeds the grid", B, Hkv);
+  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+    return fail(T2I_ERR_ALIGN, "prefill attention tensors must be 16-byte aligned");
+  t2i::PrefillAttnParams p{};
+  p.q = q; p.kc = k_cache; p.vc = v_cache; p.out = out;
+  p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.cap = ctx_cap; p.p0 = p0;
+  p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)D));
+  const int bq = t2i::PF_ROWS / Q;
+  const dim3 grid((T + bq - 1) / bq, Hkv, B);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (Q) {
+    case 1: hipLaunchKernelGGL((t2i::prefill_attention_kernel<1>), grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((t2i::prefill_attention_kernel<2>), grid, dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((t2i::prefill_attention_kernel<4>), grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL((t2i::prefill_attention_kernel<8>), grid, dim3(256), 0, s, p); break;
+  }
+  return t2i_host::hip_status(hipGetLastError(), "prefill attention launch");
+}

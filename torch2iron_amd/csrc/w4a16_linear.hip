@@ -1,4 +1,5 @@
-// W4A16 group-128 linear for gfx950: y[M, N] = x[M, K] . W^T, 1 <= M <= 64.
+// W4A16 group-128 linear for gfx950: y[M, N] = x[M, K] . W^T (M = 1: GEMV;
+// M <= 64: batched decode; more rows: a prompt batch, 16-row tiles in grid.z).
 //
 // Weights stay in the AutoGPTQ layout.  One int32 word of qweight holds the
 // 8 consecutive k of one column, which is exactly the 8 bf16 values one lane
@@ -570,7 +571,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   if (!x || !y0) return fail(T2I_ERR_NULL, "x and y must not be NULL");
   if (epi == EPI_PAIRED && !y1) return fail(T2I_ERR_NULL, "y1 must not be NULL when swiglu == 0");
   if (epi == EPI_RESIDUAL && !residual) return fail(T2I_ERR_NULL, "residual must not be NULL");
-  if (M < 1 || M > 64) return fail(T2I_ERR_SHAPE, "M=%d must be in [1, 64]", M);
+  if (M < 1 || M > T2I_MAX_ROWS) return fail(T2I_ERR_SHAPE, "M=%d must be in [1, %d]", M, T2I_MAX_ROWS);
   if (!aligned16(x) || !aligned16(y0) || (y1 && !aligned16(y1)) || (residual && !aligned16(residual)))
     return fail(T2I_ERR_ALIGN, "activation pointers must be 16-byte aligned");
   if (gamma) {

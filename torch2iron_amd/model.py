@@ -361,6 +361,56 @@ class Qwen3Model:
         nxt = ops.keys_to_tokens(self.keys)
         return nxt.cpu(), (self.logits.clone() if want_logits else None)
 
+    # ---- prompt pass (prefill) ----
+    def _prefill_buffers(self, t: int) -> dict:
+        """Activations of a prompt pass over ``B * t`` rows (kept for the next prompt of that length)."""
+        if getattr(self, "_pf", None) is not None and self._pf["t"] == t:
+            return self._pf
+        self._pf = None
+        c, r = self.cfg, self.batch * t
+        dev = self.device
+        self._pf = {
+            "t": t,
+            "x": torch.empty(r, c.hidden, dtype=BF16, device=dev),
+            "xn": torch.empty(r, c.hidden, dtype=BF16, device=dev),
+            "qkv": torch.empty(r, c.qkv_dim, dtype=BF16, device=dev),
+            "q": torch.empty(self.batch, c.n_heads, t, c.head_dim, dtype=BF16, device=dev),
+            "ctx": torch.empty(r, c.n_heads * c.head_dim, dtype=BF16, device=dev),
+            "h": torch.empty(r, c.intermediate, dtype=BF16, device=dev),
+            "last": (torch.arange(self.batch, dtype=torch.int32) * t + (t - 1)).to(dev),
+        }
+        return self._pf
+
+    def prefill(self, prompt: torch.Tensor) -> None:
+        """Consume ``prompt [B, T]`` from position 0 in one pass over all ``B * T`` rows
+        (every layer on the whole prompt batch, causal attention over the cache), then
+        greedy-pick the first new token from the last prompt row of each sequence:
+        afterwards ``tokens`` holds it, ``positions`` is ``T`` and ``history[:, 0]`` it.
+        Follows the prompt pass of ``quantized_qwen3/model.py:453-478`` for a batch.
+        """
+        c = self.cfg
+        b, t = prompt.shape
+        pf = self._prefill_buffers(t)
+        toks = prompt.reshape(-1).to(torch.int32).to(self.device)
+        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"])
+        for i, layer in enumerate(self.layers):
+            w = layer.w
+            if i == 0:
+                ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
+            else:
+                ops.rmsnorm_linear(pf["x"], w.ln1, c.eps, w.qkv, out=pf["qkv"])
+            ops.prefill_qk_rope_kv(pf["qkv"], b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, self.rope,
+                                   self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style, q_out=pf["q"])
+            ops.prefill_attention(pf["q"], 0, c.n_kv_heads, self.k_cache[i], self.v_cache[i], out=pf["ctx"])
+            ops.linear(pf["ctx"], w.o, residual=pf["x"], out=pf["x"])
+            ops.rmsnorm_gate_up(pf["x"], w.ln2, c.eps, w.gate_up, swiglu=True, out=pf["h"])
+            ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"])
+        # final norm of each sequence's last prompt row, then the tied lm_head + argmax
+        ops.rmsnorm(pf["x"], self.norm, c.eps, out=self.xn, tokens=pf["last"], x_out=self.x, argmax_keys=self.keys)
+        ops.lm_head_argmax(self.xn, self.embed, self.keys)
+        self.positions.fill_(t - 1)
+        ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+
     # ---- graph-captured greedy generation ----
     def _capture_graph(self, stream, fn):
         stream.wait_stream(torch.cuda.current_stream(self.device))
@@ -411,13 +461,18 @@ class Qwen3Model:
         self.k_cache.zero_()
         self.v_cache.zero_()
 
-    def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True, timings: dict | None = None):
+    def generate(self, prompt: torch.Tensor, new_tokens: int, use_graph: bool = True, timings: dict | None = None,
+                 prompt_mode: str = "prefill"):
         """Greedy decode as ``qwen_npu.py:309-325``: consume the prompt, then emit
         ``new_tokens`` tokens per sequence (the first from the last prompt position).
 
-        The prompt is consumed one position at a time through the decode path
-        (teacher forcing).  Returns int64 ``[B, new_tokens]`` on the host.
+        ``prompt_mode="prefill"``: the prompt goes through one prefill pass
+        (``prefill``).  ``"decode"``: it is consumed one position at a time
+        through the decode step (teacher forcing), as the NPU runner does.
+        Returns int64 ``[B, new_tokens]`` on the host.
         """
+        if prompt_mode not in ("prefill", "decode"):
+            raise ValueError("prompt_mode must be 'prefill' or 'decode'")
         prompt = torch.as_tensor(prompt)
         b, plen = prompt.shape
         if b != self.batch:
@@ -435,37 +490,37 @@ class Qwen3Model:
         self.positions.zero_()
         self.step.zero_()
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-        if use_graph:
-            if not self._captured:
-                # one eager step first: it allocates the attention workspaces outside the capture
-                self.forward_step(with_head=True)
-                torch.cuda.synchronize(self.device)
-                self._capture()
-            # restore the state the replays start from
+        if use_graph and not self._captured:
+            # one eager step first: it allocates the attention workspaces outside the capture
+            self.forward_step(with_head=True)
+            torch.cuda.synchronize(self.device)
+            self._capture()
+            # restore the state the prompt pass starts from
             self.tokens.copy_(self.prompt[:, 0])
             self.positions.zero_()
             self.step.zero_()
             self.reset()
             torch.cuda.synchronize(self.device)
-            ev[0].record()
+        ev[0].record()
+        if prompt_mode == "prefill":
+            self.prefill(prompt)
+        elif use_graph:
             for _ in range(plen - 1):
                 self._replay("prompt")
             self._replay("layers")          # last prompt position -> first new token
-            ev[1].record()
-            for _ in range(new_tokens - 1):
-                self._replay("layers")
-            ev[2].record()
         else:
-            ev[0].record()
             for _ in range(plen - 1):
                 self._fork(lambda m: (self._micro_layers(m), self._micro_prompt_advance(m)))
             self.forward_step(with_head=True)
             ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
-            ev[1].record()
-            for _ in range(new_tokens - 1):
+        ev[1].record()
+        for _ in range(new_tokens - 1):
+            if use_graph:
+                self._replay("layers")
+            else:
                 self.forward_step(with_head=True)
                 ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
-            ev[2].record()
+        ev[2].record()
         torch.cuda.synchronize(self.device)
         if timings is not None:
             timings["prompt_ms"] = ev[0].elapsed_time(ev[1])

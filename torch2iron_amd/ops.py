@@ -74,7 +74,8 @@ def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None
            out: torch.Tensor | None = None) -> torch.Tensor:
     """``y = x @ W^T`` (+ residual, rounded as bf16(bf16(x W^T) + residual)).
 
-    ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case), 1 <= M <= 64.
+    ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case): M = 1 is the GEMV,
+    M <= 64 a decode batch, more rows a prompt batch.
     """
     _check_weight(w)
     _check_dev("x", x, BF16)
@@ -250,6 +251,65 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n
                                   k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap, out.data_ptr(),
                                   _lib.ptr(ws), nbytes, _lib.stream_handle(qkv.device))
     _lib.check(rc, "t2i_decode_attention")
+    return out
+
+
+def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_kv_heads: int,
+                       q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float, rope: torch.Tensor,
+                       k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
+                       q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """q/k RMSNorm + RoPE of every prompt row and the KV-cache write of positions p0..p0+T-1.
+
+    ``qkv`` bf16 ``[B * T, (Hq + 2 Hkv) * D]`` (row ``b * T + t``); returns q
+    bf16 ``[B, Hq, T, D]``.
+    """
+    _check_dev("qkv", qkv, BF16)
+    for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_dev(n, t, BF16)
+    d = q_norm.numel()
+    rows = qkv.numel() // ((n_heads + 2 * n_kv_heads) * d)
+    if rows % batch or rows * (n_heads + 2 * n_kv_heads) * d != qkv.numel():
+        raise ValueError("qkv must be [B * T, (Hq + 2 Hkv) * D]")
+    t = rows // batch
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (batch, n_kv_heads):
+        raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
+    ctx_cap = k_cache.shape[2]
+    if rope.shape[0] < p0 + t:
+        raise ValueError("rope table shorter than the prompt positions")
+    if q_out is None:
+        q_out = torch.empty(batch, n_heads, t, d, dtype=BF16, device=qkv.device)
+    _check_dev("q_out", q_out, BF16)
+    if q_out.numel() != batch * n_heads * t * d:
+        raise ValueError("q_out must be [B, Hq, T, D]")
+    lib = _lib.load()
+    rc = lib.t2i_prefill_qk_rope_kv(qkv.data_ptr(), batch, t, p0, n_heads, n_kv_heads, d, q_norm.data_ptr(),
+                                    k_norm.data_ptr(), float(eps), rope.data_ptr(), int(rope_style),
+                                    q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap,
+                                    _lib.stream_handle(qkv.device))
+    _lib.check(rc, "t2i_prefill_qk_rope_kv")
+    return q_out
+
+
+def prefill_attention(q: torch.Tensor, p0: int, n_kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal GQA attention of prompt rows ``q [B, Hq, T, D]`` (positions p0..p0+T-1)
+    over cache slots ``0..p0+t``; returns bf16 ``[B * T, Hq * D]``."""
+    _check_dev("q", q, BF16)
+    _check_dev("k_cache", k_cache, BF16)
+    _check_dev("v_cache", v_cache, BF16)
+    b, hq, t, d = q.shape
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (b, n_kv_heads):
+        raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
+    if out is None:
+        out = torch.empty(b * t, hq * d, dtype=BF16, device=q.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != b * t * hq * d:
+        raise ValueError("out must be [B * T, Hq * D]")
+    lib = _lib.load()
+    rc = lib.t2i_prefill_attention(q.data_ptr(), b, t, p0, hq, n_kv_heads, d, k_cache.data_ptr(),
+                                   v_cache.data_ptr(), k_cache.shape[2], out.data_ptr(),
+                                   _lib.stream_handle(q.device))
+    _lib.check(rc, "t2i_prefill_attention")
     return out
 
 
