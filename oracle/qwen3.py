@@ -270,6 +270,9 @@ class DenseQwen3:
         self.cfg = cfg
         self.rnd = _Round(mode)
         self.embed = torch.as_tensor(np.asarray(tensors["model.embed_tokens.weight"], dtype=np.float32))
+        # tied lm_head unless the tensors hold their own (model.py:410-420)
+        self.lm_head = (torch.as_tensor(np.asarray(tensors["lm_head.weight"], dtype=np.float32))
+                        if "lm_head.weight" in tensors else self.embed)
         self.norm = torch.as_tensor(np.asarray(tensors["model.norm.weight"], dtype=np.float32))
         self.layers = [DenseLayer(tensors, f"model.layers.{i}", cfg) for i in range(cfg.n_layers)]
         self.angles = rope_angles(cfg.head_dim, ctx_cap, cfg.rope_theta)
@@ -285,7 +288,7 @@ class DenseQwen3:
     def logits(self, h: torch.Tensor) -> torch.Tensor:
         """Final RMSNorm then the tied bf16 lm_head, logits in fp32."""
         hn = rmsnorm(h, self.norm, self.cfg.eps, self.rnd)
-        return hn @ self.embed.T
+        return hn @ self.lm_head.T
 
     @torch.no_grad()
     def prefill(self, tokens: torch.Tensor) -> torch.Tensor:

@@ -107,15 +107,21 @@ def test_prefill_equals_stepwise_decode():
     assert torch.allclose(full, last, rtol=1e-4, atol=1e-3 * full.abs().max())
 
 
-def test_decoder_matches_transformers_qwen3():
+@pytest.mark.parametrize("tied", [True, False])
+def test_decoder_matches_transformers_qwen3(tied):
     """The oracle (fp32 mode, two-halves RoPE) against transformers' Qwen3ForCausalLM
-    holding the same dequantised weights."""
+    holding the same dequantised weights, with the tied embedding as lm_head or a
+    separate lm_head matrix."""
     transformers = pytest.importorskip("transformers")
     cfg, ocfg, t = _tiny()
+    if not tied:
+        t = dict(t)
+        t["lm_head.weight"] = (torch.randn(cfg.vocab, cfg.hidden, generator=torch.Generator().manual_seed(9))
+                               .to(torch.bfloat16).float().numpy())
     hf_cfg = transformers.Qwen3Config(
         vocab_size=cfg.vocab, hidden_size=cfg.hidden, intermediate_size=cfg.intermediate,
         num_hidden_layers=cfg.n_layers, num_attention_heads=cfg.n_heads, num_key_value_heads=cfg.n_kv_heads,
-        head_dim=cfg.head_dim, rms_norm_eps=cfg.eps, tie_word_embeddings=True, max_position_embeddings=64,
+        head_dim=cfg.head_dim, rms_norm_eps=cfg.eps, tie_word_embeddings=tied, max_position_embeddings=64,
         rope_parameters={"rope_theta": cfg.rope_theta, "rope_type": "default"}, attention_bias=False)
     torch.manual_seed(0)
     hf = transformers.Qwen3ForCausalLM(hf_cfg).float().eval()
@@ -127,7 +133,8 @@ def test_decoder_matches_transformers_qwen3():
                 ow.dequantize(t[base + ".qweight"], t[base + ".qzeros"], t[base + ".scales"]))
         elif name.endswith(".weight"):
             sd[name] = torch.as_tensor(np.asarray(t[name], dtype=np.float32))
-    sd["lm_head.weight"] = sd["model.embed_tokens.weight"]
+    if tied:
+        sd["lm_head.weight"] = sd["model.embed_tokens.weight"]
     missing, unexpected = hf.load_state_dict(sd, strict=False)
     assert not unexpected and all("rotary" in m for m in missing), (missing, unexpected)
     prompt = torch.randint(0, cfg.vocab, (2, 11), generator=torch.Generator().manual_seed(6))

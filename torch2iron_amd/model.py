@@ -270,6 +270,9 @@ class Qwen3Model:
         self.device = torch.device(device)
         self.rope = rope_table(cfg.head_dim, ctx_cap, cfg.rope_theta, self.device)
         self.embed = _bf16_dev(tensors["model.embed_tokens.weight"], self.device)
+        # the tied embedding is the lm_head unless the checkpoint holds its own (model.py:410-420)
+        self.lm_head = (_bf16_dev(tensors["lm_head.weight"], self.device) if "lm_head.weight" in tensors
+                        else self.embed)
         self.norm = _bf16_dev(tensors["model.norm.weight"], self.device)
         self.layers = [Qwen3DecodeLayer(Qwen3LayerWeights(tensors, i, cfg, self.device), cfg, self.rope)
                        for i in range(cfg.n_layers)]
@@ -286,6 +289,14 @@ class Qwen3Model:
         self.history = None
         self.prompt = None
         self.logits = None
+
+    @classmethod
+    def from_pretrained(cls, model_dir, batch: int, ctx_cap: int, device, streams: int = 1) -> "Qwen3Model":
+        """Load an AutoGPTQ W4A16 Qwen3 directory (``checkpoint.load_checkpoint``)."""
+        from torch2iron_amd.checkpoint import load_checkpoint
+
+        tensors, cfg = load_checkpoint(model_dir)
+        return cls(tensors, cfg, batch=batch, ctx_cap=ctx_cap, device=device, streams=streams)
 
     def set_streams(self, streams: int) -> None:
         """Split the batch into ``streams`` micro-batches (drops captured graphs)."""
@@ -321,7 +332,7 @@ class Qwen3Model:
         ops.rmsnorm(self.x, self.norm, c.eps, out=self.xn, argmax_keys=self.keys)
         if want_logits and self.logits is None:
             self.logits = torch.empty(self.batch, c.vocab, dtype=torch.float32, device=self.device)
-        ops.lm_head_argmax(self.xn, self.embed, self.keys, logits=self.logits if want_logits else None)
+        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=self.logits if want_logits else None)
 
     def _fork(self, fn):
         """Run ``fn(m)`` for every micro-batch on its stream, joined back to the current stream."""
@@ -407,7 +418,7 @@ class Qwen3Model:
             ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"])
         # final norm of each sequence's last prompt row, then the tied lm_head + argmax
         ops.rmsnorm(pf["x"], self.norm, c.eps, out=self.xn, tokens=pf["last"], x_out=self.x, argmax_keys=self.keys)
-        ops.lm_head_argmax(self.xn, self.embed, self.keys)
+        ops.lm_head_argmax(self.xn, self.lm_head, self.keys)
         self.positions.fill_(t - 1)
         ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
 
