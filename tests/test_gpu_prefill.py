@@ -148,9 +148,9 @@ def test_model_prefill_matches_oracle(gpu, weights):
 
 def test_generate_with_prefill_matches_oracle(gpu):
     """4 layers, batch 8: prefill + 24 greedy decode steps vs the fp32 oracle, divergences
-    only at near-ties; the teacher-forced prompt path lands on the same first token except
-    at near-ties too."""
-    from tests.test_gpu_decode import assert_near_tie
+    only at near-ties, and teacher-forced logits (prefill, then decode steps) no noisier
+    against fp32 than the oracle's bf16 mode."""
+    from tests.test_gpu_decode import assert_logit_noise_like_bf16_oracle, assert_near_tie
     cfg = gm.Qwen3Config(n_layers=4, vocab=8192)
     t = gm.random_qwen3_tensors(cfg, seed=21, weights="centered")
     b, plen, new = 8, 40, 24
@@ -167,4 +167,4 @@ def test_generate_with_prefill_matches_oracle(gpu):
         if len(diff):
             s = int(diff[0])
             assert_near_tie(o16, o32, prompt[i:i + 1], ref[i:i + 1, :s], margins[i, s], f"sequence {i} step {s}")
-    assert (got == ref).all(dim=1).float().mean() >= 0.5
+    assert_logit_noise_like_bf16_oracle(m, o16, o32, prompt, ref[:, :new - 1], "prefill")

@@ -115,9 +115,11 @@ __device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
   f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
 }
 
-// exp(m - M) as the weight of a softmax state with running max m under a new max M;
-// an empty state (m = -inf) weighs nothing.
-__device__ __forceinline__ float state_weight(float m, float M) { return m > -INFINITY ? expf(m - M) : 0.0f; }
+// Scores are kept in log2 units (scaled by log2 e), so every exponential is a
+// single v_exp_f32.  2^(m - M) is the weight of a softmax state with running max m
+// under a new max M; an empty state (m = -inf) weighs nothing.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float state_weight(float m, float M) { return m > -INFINITY ? exp2_fast(m - M) : 0.0f; }
 
 // One workgroup per (sequence b, kv head h, chunk of 16 * ROWS context slots).
 // A single workgroup per (b, h) streaming the whole context was measured 2-4x
@@ -149,7 +151,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
   const int rg = lane >> 4;
   const int grp = wave * 4 + rg;        // slot group 0..15
 
-  __shared__ float s_q[Q][D];
+  __shared__ __align__(16) uint16_t s_q[Q][D];    // q heads after norm + RoPE (bf16)
   __shared__ __align__(16) uint16_t s_kv[2][D];   // current k (after norm + RoPE) and v
   __shared__ float s_wm[4][Q], s_wl[4][Q];
   __shared__ float s_wacc[4][Q][D];
@@ -168,59 +170,58 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
 
   if (t0 < t1) {
     // ---- 1. prologue inputs, then the chunk's K / V rows ----
+    // Every load below is unconditional (clamped indices, results selected after
+    // the load): a load under a lane-divergent condition whose other side writes
+    // the same registers makes the compiler wait for all loads in flight there,
+    // which serialises the K / V rows into one memory round trip each.
     const int i0 = p.style == 0 ? lane : 2 * lane;        // pair (i0, i1) rotates together
     const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     float px0[NV], px1[NV], pg0[NV], pg1[NV];
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
-      const int vi = wave + 4 * n;
-      px0[n] = px1[n] = 0.0f;
-      pg0[n] = pg1[n] = 1.0f;
-      if (vi < Q + 2) {
-        const uint16_t* src;
-        const uint16_t* gamma = nullptr;
-        if (vi < Q) { src = p.qkv + qkv_row + (size_t)(h * Q + vi) * D; gamma = p.qn; }
-        else if (vi == Q) { src = p.qkv + qkv_row + (size_t)(p.Hq + h) * D; gamma = p.kn; }
-        else { src = p.qkv + qkv_row + (size_t)(p.Hq + p.Hkv + h) * D; }
-        px0[n] = bf16_to_f32(src[i0]);
-        px1[n] = bf16_to_f32(src[i1]);
-        if (gamma) { pg0[n] = bf16_to_f32(gamma[i0]); pg1[n] = bf16_to_f32(gamma[i1]); }
-      }
+      const int vi = min(wv + 4 * n, Q + 1);   // waves past the last vector reload it; unused
+      const int hrow = vi < Q ? h * Q + vi : (vi == Q ? p.Hq + h : p.Hq + p.Hkv + h);
+      const uint16_t* src = p.qkv + qkv_row + (size_t)hrow * D;
+      const uint16_t* gamma = vi < Q ? p.qn : p.kn;   // v takes no gamma; loaded, unused
+      px0[n] = bf16_to_f32(src[i0]);
+      px1[n] = bf16_to_f32(src[i1]);
+      pg0[n] = bf16_to_f32(gamma[i0]);
+      pg1[n] = bf16_to_f32(gamma[i1]);
     }
     const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
     const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+    __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of the K / V loads
 
+    // slots past the chunk's end reload its first slot; masked when scored
     u32x4 kreg[ROWS], vreg[ROWS];
 #pragma unroll
     for (int it = 0; it < ROWS; ++it) {
       const int t = t0 + it * 16 + grp;
-      if (t < t1 && t != pos) {
-        kreg[it] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)t * D + 8 * c);
-        vreg[it] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)t * D + 8 * c);
-      } else {
-        kreg[it] = vreg[it] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const int tl = t < t1 ? t : t0;
+      kreg[it] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)tl * D + 8 * c);
+      vreg[it] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)tl * D + 8 * c);
     }
 
     // ---- q heads and the current k: per-head RMSNorm then RoPE; v as is ----
+    // computed by every wave and selected (no branch that the loads above could
+    // be moved into, behind the K / V loads)
 #pragma unroll
     for (int n = 0; n < NV; ++n) {
-      const int vi = wave + 4 * n;
-      if (vi >= Q + 2) continue;
+      const int vi = wv + 4 * n;
       float x0 = px0[n], x1 = px1[n];
-      if (vi <= Q) {
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-        x0 = round_bf16(round_bf16(x0 * inv) * pg0[n]);
-        x1 = round_bf16(round_bf16(x1 * inv) * pg1[n]);
-        const float y0 = round_bf16(round_bf16(x0 * cs) + round_bf16(-x1 * sn));
-        const float y1 = round_bf16(round_bf16(x1 * cs) + round_bf16(x0 * sn));
-        x0 = y0;
-        x1 = y1;
-      }
+      const float ss = wave_sum(x0 * x0 + x1 * x1);
+      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+      const float n0 = round_bf16(round_bf16(x0 * inv) * pg0[n]);
+      const float n1 = round_bf16(round_bf16(x1 * inv) * pg1[n]);
+      const float y0 = round_bf16(round_bf16(n0 * cs) + round_bf16(-n1 * sn));
+      const float y1 = round_bf16(round_bf16(n1 * cs) + round_bf16(n0 * sn));
+      x0 = vi <= Q ? y0 : x0;
+      x1 = vi <= Q ? y1 : x1;
+      if (vi >= Q + 2) continue;
       if (vi < Q) {
-        s_q[vi][i0] = x0;
-        s_q[vi][i1] = x1;
+        s_q[vi][i0] = (uint16_t)f32_to_bf16(x0);
+        s_q[vi][i1] = (uint16_t)f32_to_bf16(x1);
       } else {
         const int which = vi - Q;   // 0 = k, 1 = v
         const uint16_t b0 = (uint16_t)f32_to_bf16(x0), b1 = (uint16_t)f32_to_bf16(x1);
@@ -236,35 +237,39 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     __syncthreads();
 
     // ---- 2. scores and the softmax state of each 16-lane group ----
-    float qf[Q][8];
+    u32x4 qv[Q];   // dims 8c .. 8c+7 of each q head, bf16 pairs
 #pragma unroll
-    for (int j = 0; j < Q; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[j][e] = s_q[j][8 * c + e];
-    const u32x4* kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0]);
-    const u32x4* vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0]);
+    for (int j = 0; j < Q; ++j) qv[j] = reinterpret_cast<const u32x4*>(&s_q[j][0])[c];
+    const u32x4 kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0])[c];
+    const u32x4 vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0])[c];
+    const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
+    const float sl2 = p.scale * 1.4426950408889634f;   // log2 units
     float sc[ROWS][Q];
 #pragma unroll
     for (int it = 0; it < ROWS; ++it) {
       const int t = t0 + it * 16 + grp;
-      if (t == pos) { kreg[it] = kcur[c]; vreg[it] = vcur[c]; }
-      float kf[8];
-      unpack8(kreg[it], kf);
+      // the current slot comes from LDS (the cache row is being replaced); a slot
+      // past the chunk's end scores -inf, and its V is zeroed so that its zero
+      // softmax weight cannot meet a non-finite value from the reload
+      const u32x4 kk = t == pos ? kcur : kreg[it];
+      vreg[it] = t < t1 ? (t == pos ? vcur : vreg[it]) : zero4;
 #pragma unroll
       for (int j = 0; j < Q; ++j) {
-        float d = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qf[j][e], kf[e], d);
+        float d = dot2_bf16(qv[j].x, kk.x, 0.0f);   // bf16 products are exact in fp32
+        d = dot2_bf16(qv[j].y, kk.y, d);
+        d = dot2_bf16(qv[j].z, kk.z, d);
+        d = dot2_bf16(qv[j].w, kk.w, d);
         d = row_sum16(d);
-        sc[it][j] = t < t1 ? d * p.scale : -INFINITY;
+        sc[it][j] = t < t1 ? d * sl2 : -INFINITY;
       }
     }
-    float m[Q], l[Q], acc[Q][8];
+    float m[Q], mz[Q], l[Q], acc[Q][8];
 #pragma unroll
     for (int j = 0; j < Q; ++j) {
       m[j] = sc[0][j];
 #pragma unroll
       for (int it = 1; it < ROWS; ++it) m[j] = fmaxf(m[j], sc[it][j]);
+      mz[j] = m[j] > -INFINITY ? m[j] : 0.0f;   // a group with no slot: 2^-inf = 0 below
       l[j] = 0.0f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
@@ -275,7 +280,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
       unpack8(vreg[it], vf);
 #pragma unroll
       for (int j = 0; j < Q; ++j) {
-        const float pe = sc[it][j] > -INFINITY ? expf(sc[it][j] - m[j]) : 0.0f;
+        const float pe = exp2_fast(sc[it][j] - mz[j]);
         l[j] += pe;
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pe, vf[e], acc[j][e]);
@@ -356,22 +361,17 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const Att
     for (int s0 = 0; s0 < p.splits; s0 += 8) {
       float ms[8], ls[8], os[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const size_t st = (size_t)bh * p.splits + s0 + u;
-        ms[u] = -INFINITY;
-        ls[u] = 0.0f;
-        os[u] = 0.0f;
-        if (s0 + u < p.splits) {
-          ms[u] = ld_agent(p.part_ml + (st * Q + j) * 2);
-          ls[u] = ld_agent(p.part_ml + (st * Q + j) * 2 + 1);
-          os[u] = ld_agent(p.part_o + (st * Q + j) * D + d);
-        }
+      for (int u = 0; u < 8; ++u) {   // unconditional loads (clamped), as above
+        const size_t st = (size_t)bh * p.splits + min(s0 + u, p.splits - 1);
+        ms[u] = ld_agent(p.part_ml + (st * Q + j) * 2);
+        ls[u] = ld_agent(p.part_ml + (st * Q + j) * 2 + 1);
+        os[u] = ld_agent(p.part_o + (st * Q + j) * D + d);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        if (ls[u] > 0.0f) {   // an empty chunk stored no context
+        if (ls[u] > 0.0f && s0 + u < p.splits) {   // an empty chunk stored no context
           const float mn = fmaxf(M, ms[u]);
-          const float fa = state_weight(M, mn), fb = expf(ms[u] - mn);
+          const float fa = state_weight(M, mn), fb = exp2_fast(ms[u] - mn);
           lsum = lsum * fa + ls[u] * fb;
           o = o * fa + os[u] * fb;
           M = mn;

@@ -330,9 +330,15 @@ class Qwen3Model:
         """Final RMSNorm of the whole batch and the tied lm_head with the fused argmax."""
         c = self.cfg
         ops.rmsnorm(self.x, self.norm, c.eps, out=self.xn, argmax_keys=self.keys)
-        if want_logits and self.logits is None:
-            self.logits = torch.empty(self.batch, c.vocab, dtype=torch.float32, device=self.device)
-        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=self.logits if want_logits else None)
+        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=self._logits_out(want_logits))
+
+    def _logits_out(self, want_logits: bool):
+        """The fp32 ``[batch, vocab]`` logits buffer when logits are wanted, else None."""
+        if not want_logits:
+            return None
+        if self.logits is None:
+            self.logits = torch.empty(self.batch, self.cfg.vocab, dtype=torch.float32, device=self.device)
+        return self.logits
 
     def _fork(self, fn):
         """Run ``fn(m)`` for every micro-batch on its stream, joined back to the current stream."""
@@ -392,11 +398,12 @@ class Qwen3Model:
         }
         return self._pf
 
-    def prefill(self, prompt: torch.Tensor) -> None:
+    def prefill(self, prompt: torch.Tensor, want_logits: bool = False):
         """Consume ``prompt [B, T]`` from position 0 in one pass over all ``B * T`` rows
         (every layer on the whole prompt batch, causal attention over the cache), then
         greedy-pick the first new token from the last prompt row of each sequence:
         afterwards ``tokens`` holds it, ``positions`` is ``T`` and ``history[:, 0]`` it.
+        Returns the fp32 logits of the last prompt rows when ``want_logits`` (else None).
         Follows the prompt pass of ``quantized_qwen3/model.py:453-478`` for a batch.
         """
         c = self.cfg
@@ -418,9 +425,12 @@ class Qwen3Model:
             ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"])
         # final norm of each sequence's last prompt row, then the tied lm_head + argmax
         ops.rmsnorm(pf["x"], self.norm, c.eps, out=self.xn, tokens=pf["last"], x_out=self.x, argmax_keys=self.keys)
-        ops.lm_head_argmax(self.xn, self.lm_head, self.keys)
+        logits = self._logits_out(want_logits)
+        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=logits)
         self.positions.fill_(t - 1)
+        self.step.zero_()                  # a prompt pass starts the token record
         ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
+        return logits.clone() if want_logits else None
 
     # ---- graph-captured greedy generation ----
     def _capture_graph(self, stream, fn):

@@ -341,11 +341,13 @@ def keys_to_tokens(keys: torch.Tensor) -> torch.Tensor:
 
 
 def greedy_advance(keys, tokens, positions, history, step):
-    """Device-side greedy bookkeeping between captured decode steps."""
+    """Device-side greedy bookkeeping between captured decode steps (``history`` may
+    be None: no token record)."""
     lib = _lib.load()
     b = tokens.numel()
     rc = lib.t2i_greedy_advance(keys.data_ptr(), b, tokens.data_ptr(), positions.data_ptr(),
-                                history.data_ptr(), history.shape[1], step.data_ptr(),
+                                history.data_ptr() if history is not None else None,
+                                history.shape[1] if history is not None else 0, step.data_ptr(),
                                 _lib.stream_handle(tokens.device))
     _lib.check(rc, "t2i_greedy_advance")
 
