@@ -136,14 +136,12 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
     load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
 #pragma unroll
   for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) {
-    const int m = mbase + mi * 16 + c;
+    // rows past M reload row M - 1 (an unconditional load): an MFMA output row
+    // depends on its own A row only, and rows past M are never stored
+    const int m = min(mbase + mi * 16 + c, p.M - 1);
 #pragma unroll
-    for (int j = 0; j < CK; ++j) {
-      if (m < p.M)
-        b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
-      else
-        b.x[mi][j] = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int j = 0; j < CK; ++j)
+      b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
   }
   const int g = ks0 / KSG;
   load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s);
@@ -247,51 +245,68 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
   }
 }
 
-// Fused RMSNorm prologue.  Wave w takes k-steps w, w + W, ...; for k-step ks
-// lane l = 16 r + row loads x[row][32 ks + 8 r .. + 7] and the matching norm
-// weight (all loads of the tile issued together, overlapping the first weight
-// chunk already in flight) and parks them in LDS at A-operand slot 64 ks + l,
-// so every LDS access of a wave is one contiguous 1 KB (no bank conflicts).
-// The per-row sums of squares meet through lane shuffles and a small table
-// (fixed order), then each lane normalises the slots it parked, rounding as the
-// standalone RMSNorm: bf16(bf16(x * inv) * w), inv = bf16(1 / sqrt(mean(x^2) + eps)).
-// Rows beyond M are zero.
+// Fused RMSNorm prologue, in two parts: norm_issue loads the row tile and the
+// norm weight before the first weight chunk is loaded (loads retire in issue
+// order, so norm_finish then waits for its own data only, while the weights
+// stay in flight), and norm_finish normalises.  Wave w takes k-steps w, w + W,
+// ... (KPW of them, a compile-time bound on K / 32 / W); for k-step ks lane
+// l = 16 r + row loads x[row][32 ks + 8 r .. + 7]; each thread loads 8 norm
+// weights.  All loads are unconditional (clamped indices, values discarded
+// after the load): a load under a lane-divergent condition makes the compiler
+// wait for every load in flight where the branches join.  The tile is parked
+// in LDS at A-operand slot 64 ks + l, so every LDS access of a wave is one
+// contiguous 1 KB (no bank conflicts).  The per-row sums of squares meet
+// through lane shuffles and a small table (fixed order), then each lane
+// normalises the slots it parked, rounding as the standalone RMSNorm:
+// bf16(bf16(x * inv) * w), inv = bf16(1 / sqrt(mean(x^2) + eps)).  Rows beyond
+// M are zero.
 constexpr int NORM_MAX_K = 4096;
 
-template <int W>
-__device__ __forceinline__ void norm_prologue(const LinearParams& p, int mbase, int wave, int lane, u32x4* a_lds) {
+template <int KPW>
+struct NormLoads {
+  u32x4 v[KPW];   // row-tile k-steps wave, wave + W, ...
+  u32x4 g;        // norm weight 8 t .. 8 t + 7 of thread t
+};
+
+template <int W, int KPW>
+__device__ __forceinline__ void norm_issue(const LinearParams& p, int mbase, int wave, int lane, NormLoads<KPW>& nl) {
+  const int ksteps = p.K / 32;
+  const int row = lane & 15, r = lane >> 4;
+  const uint16_t* xrow = p.x + (size_t)min(mbase + row, p.M - 1) * p.ldx + r * 8;
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    const int ks = min(wave + i * W, ksteps - 1);
+    nl.v[i] = *reinterpret_cast<const u32x4*>(xrow + ks * 32);
+  }
+  nl.g = *reinterpret_cast<const u32x4*>(p.gamma + 8 * min((int)threadIdx.x, p.K / 8 - 1));
+}
+
+template <int W, int KPW>
+__device__ __forceinline__ void norm_finish(const LinearParams& p, int mbase, int wave, int lane,
+                                            const NormLoads<KPW>& nl, u32x4* a_lds) {
   __shared__ float s_ss[W][16];
   __shared__ float s_inv[16];
   const int ksteps = p.K / 32;
   const int row = lane & 15, r = lane >> 4;
   const bool row_ok = mbase + row < p.M;
-  const uint16_t* xrow = p.x + (size_t)(mbase + row) * p.ldx + r * 8;
   u32x4* g_lds = a_lds + ksteps * 64;            // norm weight, 16 bytes per (k-step, sub-block)
+  // threads past K / 8 loaded the last 8 weights and store them again (same value):
+  // an unconditional store keeps the compiler from moving the load behind the weights
+  g_lds[min((int)threadIdx.x, p.K / 8 - 1)] = nl.g;
+  const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
   float ss = 0.0f;
-  for (int ks0 = wave; ks0 < ksteps; ks0 += 4 * W) {
-    u32x4 v[4], g[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ks = ks0 + i * W;
-      v[i] = g[i] = u32x4{0u, 0u, 0u, 0u};
-      if (ks < ksteps) {
-        if (row_ok) v[i] = *reinterpret_cast<const u32x4*>(xrow + ks * 32);
-        if (row == 0) g[i] = *reinterpret_cast<const u32x4*>(p.gamma + ks * 32 + r * 8);
-      }
+  for (int i = 0; i < KPW; ++i) {
+    const int ks = wave + i * W;
+    if (ks >= ksteps) continue;
+    const u32x4 v = row_ok ? nl.v[i] : zero4;
+    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
+      ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
     }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ks = ks0 + i * W;
-      if (ks >= ksteps) continue;
-      const uint32_t a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
-        ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
-      }
-      a_lds[ks * 64 + lane] = v[i];
-      if (row == 0) g_lds[ks * 4 + r] = g[i];
-    }
+    a_lds[ks * 64 + lane] = v;
   }
   ss += __shfl_xor(ss, 16, 64);                  // the four sub-blocks of a row
   ss += __shfl_xor(ss, 32, 64);
@@ -331,12 +346,15 @@ __device__ __forceinline__ int xcd_block(int b, int G) {
   return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
 }
 
-template <int MT, int LW, int W, int CK, bool NORM>
+// NKPW = 0: plain linear; NKPW > 0: the fused-RMSNorm variant, whose prologue
+// takes up to NKPW k-steps per wave (NKPW * W * 32 >= K).
+template <int MT, int LW, int W, int CK, int NKPW>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p) {
+  constexpr bool NORM = NKPW > 0;
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
   constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar control flow
   const int c = lane & 15;
   const int r = lane >> 4;
   const int ncol = xcd_block(blockIdx.x, gridDim.x) * (16 * LW) + LW * c;
@@ -360,14 +378,45 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
 #pragma unroll
       for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
 
-  Chunk<MT, LW, CK> A, B;
-  if (c_begin < c_end) load_chunk<MT, LW, CK, NORM>(p, c_begin, ncol, c, r, mbase, A);
+  // Load order: the norm prologue's row tile, then the first weight chunk (every
+  // wave loads one: a wave without chunks reloads the last and computes nothing),
+  // so that normalising waits for the tile only while the weights are in flight.
+  NormLoads<NORM ? NKPW : 1> nl;
+  if constexpr (NORM) norm_issue<W, NKPW>(p, mbase, wave, lane, nl);
+  __builtin_amdgcn_sched_barrier(0);   // keep this load order
+  Chunk<MT, LW, CK> A, B, C;
+  load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
+  __builtin_amdgcn_sched_barrier(0);
   if constexpr (NORM) {
-    // the first chunk's weights are in flight while the rows are normalised
-    norm_prologue<W>(p, mbase, wave, lane, a_lds);
+    norm_finish<W, NKPW>(p, mbase, wave, lane, nl, a_lds);
     __syncthreads();
   }
-  if (c_begin < c_end) {
+  // One word per lane: straight-line schedules for 1, 2 and 3 chunks per wave
+  // (every chunk of the wave in flight before the first is computed, each
+  // computation waiting for its own chunk only), else a double-buffered loop.
+  // Wider tiles use the loop alone, which keeps their registers (occupancy) as
+  // they were; their decode plans have one chunk per wave.
+  const int n = c_end - c_begin;   // wave-uniform
+  bool looped = true;
+  if constexpr (LW == 1) {
+    looped = false;
+    if (n == 1) {
+      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
+    } else if (n == 2) {
+      load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
+      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
+    } else if (n == 3) {
+      load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
+      load_chunk<MT, LW, CK, NORM>(p, c_begin + 2, ncol, c, r, mbase, C);
+      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(C, total, a_lds, (c_begin + 2) * CK, lane, zshift);
+    } else {
+      looped = true;
+    }
+  }
+  if (looped) {
     for (int ch = c_begin; ch < c_end; ch += 2) {
       if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
       compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, ch * CK, lane, zshift);
@@ -524,28 +573,52 @@ size_t norm_lds_bytes(const Plan& pl, int K) {
   return rows > red ? rows : red;
 }
 
-template <int MT, int LW, int W, int CK, bool NORM>
+template <int MT, int LW, int W, int CK, int NKPW>
 hipError_t launch_t(const LinearParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  if constexpr (NORM) {
+  if constexpr (NKPW > 0) {
     // raise the dynamic LDS limit once per kernel for tiles above 64 KB
     static thread_local size_t raised = 65536;
     if (lds > raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_mfma_kernel<MT, LW, W, CK, true>),
+      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_mfma_kernel<MT, LW, W, CK, NKPW>),
                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
       raised = lds;
     }
   }
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM>), grid, dim3(64 * W), lds, s, p);
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NKPW>), grid, dim3(64 * W), lds, s, p);
   return hipGetLastError();
+}
+
+// Bound on the fused-norm prologue's k-steps per wave: the smallest of 1, 2, 4,
+// 8, 16 that covers K / 32 / W (0: no fused norm).
+int norm_kpw(int K, int W) {
+  const int need = (K / 32 + W - 1) / W;
+  int k = 1;
+  while (k < need) k <<= 1;
+  return k;
+}
+
+template <int MT, int LW, int W, int CK>
+hipError_t launch_cfg(const LinearParams& p, dim3 grid, size_t lds, int kpw, hipStream_t s) {
+  switch (kpw) {
+    case 0: return launch_t<MT, LW, W, CK, 0>(p, grid, lds, s);
+    case 1: return launch_t<MT, LW, W, CK, 1>(p, grid, lds, s);
+    case 2: return launch_t<MT, LW, W, CK, 2>(p, grid, lds, s);
+    case 4: return launch_t<MT, LW, W, CK, 4>(p, grid, lds, s);
+    case 8: return launch_t<MT, LW, W, CK, 8>(p, grid, lds, s);
+    case 16: return launch_t<MT, LW, W, CK, 16>(p, grid, lds, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_plan(const Plan& pl, const LinearParams& p, bool norm, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
   const size_t lds = norm ? norm_lds_bytes(pl, p.K) : 0;
-#define T2I_LAUNCH(a, b, c, d)                                                          \
-  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)                              \
-    return norm ? launch_t<a, b, c, d, true>(p, grid, lds, s) : launch_t<a, b, c, d, false>(p, grid, lds, s);
+  // the fused norm's weight takes one 8-value load per thread: K <= 512 W
+  if (norm && p.K > 512 * pl.W) return hipErrorInvalidValue;
+  const int kpw = norm ? norm_kpw(p.K, pl.W) : 0;
+#define T2I_LAUNCH(a, b, c, d) \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_cfg<a, b, c, d>(p, grid, lds, kpw, s);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;
