@@ -98,8 +98,12 @@ __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&w)[LW
 
 // Raw fp16 scales of LW consecutive columns, two per word (converted only when
 // the chunk is computed, so issuing a chunk's loads never waits for them).
+// LW 16-bit values from src (fp16 scales or bf16 residuals) as 32-bit words.  One
+// value (odd: at an odd index) comes as the aligned word holding it (half_of picks
+// it): a 16-bit load would be widened right after the load, which makes the
+// compiler wait for it there.
 template <int LW>
-__device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[(LW + 1) / 2]) {
+__device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[(LW + 1) / 2], int odd = 0) {
   if constexpr (LW == 8) {
     const u32x4 a = *reinterpret_cast<const u32x4*>(src);
     s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w;
@@ -109,13 +113,15 @@ __device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[(
   } else if constexpr (LW == 2) {
     s[0] = *reinterpret_cast<const uint32_t*>(src);
   } else {
-    s[0] = *src;
+    s[0] = *reinterpret_cast<const uint32_t*>(src - odd);
   }
 }
 
+// Bits of value t of this lane's columns; odd: the lane's first column is odd (LW == 1).
 template <int LW>
-__device__ __forceinline__ float scale_of(const uint32_t (&s)[(LW + 1) / 2], int t) {
-  return f16_to_f32((t & 1) ? (s[t >> 1] >> 16) : (s[t >> 1] & 0xFFFFu));
+__device__ __forceinline__ uint32_t half_of(const uint32_t (&s)[(LW + 1) / 2], int t, bool odd) {
+  const bool hi = LW == 1 ? odd : (t & 1) != 0;
+  return hi ? (s[t >> 1] >> 16) : (s[t >> 1] & 0xFFFFu);
 }
 
 // Operands of one chunk (CK k-steps, all inside one quantisation group), as loaded.
@@ -144,15 +150,31 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
       b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
   }
   const int g = ks0 / KSG;
-  load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s);
+  load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
   b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
 }
 
 // a_lds (fused-norm variant): the normalised activations of the row tile in
 // A-operand order, 64 lanes x 16 bytes per k-step; k-step ks0 is this chunk's first.
+// Pins a loaded value at this point: code that uses it cannot be moved above the
+// pin (say, to a point shared by the chunk schedules, where it would wait for the
+// chunk's loads before the other chunks' loads are issued).
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
+
 template <int MT, int LW, int CK, bool NORM>
-__device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4],
+__device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4],
                                               const u32x4* a_lds, int ks0, int lane, int zshift) {
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+#pragma unroll
+    for (int t = 0; t < LW; ++t) pin(b.w[j][t]);
+#pragma unroll
+    for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) pin(b.x[mi][j]);
+  }
+#pragma unroll
+  for (int i = 0; i < (LW + 1) / 2; ++i) pin(b.s[i]);
+  pin(b.zw);
   const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
   const bf16x8 ones = ones_operand();
   f32x4 acc[MT][LW];
@@ -182,7 +204,7 @@ __device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float 
 #pragma unroll
   for (int t = 0; t < LW; ++t) {
     const float zb = -(float)(128 + 1 + ((zw >> (4 * t)) & 0xFu));
-    const float sc = scale_of<LW>(b.s, t);
+    const float sc = f16_to_f32(half_of<LW>(b.s, t, (zshift & 4) != 0));
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
@@ -191,18 +213,19 @@ __device__ __forceinline__ void compute_chunk(const Chunk<MT, LW, CK>& b, float 
   }
 }
 
-// Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32 sums v.
+// Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32
+// sums v; res holds the row's residual values (bf16 pairs), fetched at the start.
 template <int LW>
-__device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW]) {
+__device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW],
+                                          const uint32_t (&res)[(LW + 1) / 2]) {
   if (m >= p.M) return;
   if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
     float v[LW];
 #pragma unroll
     for (int t = 0; t < LW; ++t) v[t] = v_in[t];
     if (p.epi == EPI_RESIDUAL) {
-      const uint16_t* res = p.residual + (size_t)m * p.ldy + ncol;
 #pragma unroll
-      for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32(res[t]);
+      for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32((uint16_t)half_of<LW>(res, t, ncol & 1));
     }
     uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
     if constexpr (LW == 1) {
@@ -386,6 +409,14 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
   __builtin_amdgcn_sched_barrier(0);   // keep this load order
   Chunk<MT, LW, CK> A, B, C;
   load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
+  // The residual values this wave stores (residual epilogue) are fetched now, so
+  // the epilogue waits for nothing.  The load is unconditional: waves that store
+  // nothing fetch a clamped row and drop it, and without a residual the first
+  // scales row stands in (in bounds, unused).
+  const int st_mi = min(wave >> 2, MT - 1), st_i = wave & 3;
+  const int st_m = mbase + st_mi * 16 + r * 4 + st_i;   // the row this lane stores
+  uint32_t resv[(LW + 1) / 2];
+  load_scales<LW>(p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv, ncol & 1);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (NORM) {
     norm_finish<W, NKPW>(p, mbase, wave, lane, nl, a_lds);
@@ -430,8 +461,8 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
   // Every wave that had chunks parks its sums; then wave 4 mi + i adds row i of
   // m-tile mi over the waves in wave order and stores it.
   const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
-  if constexpr (W > 1) {
-    static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
+  static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
+  {
     __shared__ float red_static[NORM ? 1 : W * E * 64];
     float* red = NORM ? reinterpret_cast<float*>(dyn_lds) : red_static;
     if constexpr (NORM) __syncthreads();   // every wave is done with the normalised rows
@@ -446,26 +477,15 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
     }
     __syncthreads();
     if (wave >= 4 * MT) return;
-    const int mi = wave >> 2, i = wave & 3;
     float v[LW];
 #pragma unroll
     for (int t = 0; t < LW; ++t) v[t] = 0.0f;
     for (int w = 0; w < nw; ++w) {
       const float* src = red + w * E * 64 + lane;
 #pragma unroll
-      for (int t = 0; t < LW; ++t) v[t] += src[((mi * LW + t) * 4 + i) * 64];
+      for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
     }
-    store_row<LW>(p, ncol, mbase + mi * 16 + r * 4 + i, v);
-  } else {
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float v[LW];
-#pragma unroll
-        for (int t = 0; t < LW; ++t) v[t] = total[mi][t][i];
-        store_row<LW>(p, ncol, mbase + mi * 16 + r * 4 + i, v);
-      }
+    store_row<LW>(p, ncol, st_m, v, resv);
   }
 }
 
