@@ -411,17 +411,20 @@ class Qwen3Model:
         pf = self._prefill_buffers(t)
         toks = prompt.reshape(-1).to(torch.int32).to(self.device)
         ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"])
+        # Over prompt-sized batches the norms run as their own pass: the fused-norm
+        # linear normalises its row tile once per column block, which at thousands of
+        # rows costs more than one extra launch.
         for i, layer in enumerate(self.layers):
             w = layer.w
-            if i == 0:
-                ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
-            else:
-                ops.rmsnorm_linear(pf["x"], w.ln1, c.eps, w.qkv, out=pf["qkv"])
+            if i > 0:
+                ops.rmsnorm(pf["x"], w.ln1, c.eps, out=pf["xn"])
+            ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
             ops.prefill_qk_rope_kv(pf["qkv"], b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, self.rope,
                                    self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style, q_out=pf["q"])
             ops.prefill_attention(pf["q"], 0, c.n_kv_heads, self.k_cache[i], self.v_cache[i], out=pf["ctx"])
             ops.linear(pf["ctx"], w.o, residual=pf["x"], out=pf["x"])
-            ops.rmsnorm_gate_up(pf["x"], w.ln2, c.eps, w.gate_up, swiglu=True, out=pf["h"])
+            ops.rmsnorm(pf["x"], w.ln2, c.eps, out=pf["xn"])
+            ops.gate_up(pf["xn"], w.gate_up, swiglu=True, out=pf["h"])
             ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"])
         # final norm of each sequence's last prompt row, then the tied lm_head + argmax
         ops.rmsnorm(pf["x"], self.norm, c.eps, out=self.xn, tokens=pf["last"], x_out=self.x, argmax_keys=self.keys)
