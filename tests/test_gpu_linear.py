@@ -123,6 +123,61 @@ def test_gate_up_paired_and_swiglu(gpu, m, k, inter):
     assert np.abs(h - truth).max() / np.abs(truth).max() <= 1e-2
 
 
+# Prompt-sized M (at least 512 rows, N a multiple of 128) runs the LDS-tiled GEMM:
+# 128 x 128 output tiles, ragged last row tile, one k-tile (an odd count included).
+PROMPT_CASES = [(512, 1024, 4096), (600, 2048, 1024), (1030, 3072, 1024), (777, 1024, 256), (520, 128, 128),
+                (513, 384, 384)]
+
+
+@pytest.mark.parametrize("m,k,n", PROMPT_CASES, ids=[f"M{m}-K{k}-N{n}" for m, k, n in PROMPT_CASES])
+def test_prompt_rows_match_oracle(gpu, m, k, n):
+    qw, qz, sc, x = _inputs(m, k, n, seed=2000 + m + k + n)
+    ref = ow.linear(x.float().numpy(), qw, qz, sc, accumulate="fp64")
+    w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
+    y = ops.linear(x.to(gpu), w)
+    check_linear(y, ref)
+    assert torch.equal(y, ops.linear(x.to(gpu), w)), "repeat call differs"
+
+
+def test_prompt_rows_residual(gpu):
+    m, k, n = 700, 2048, 1024
+    qw, qz, sc, x = _inputs(m, k, n, seed=41)
+    res = torch.randn(m, n, generator=torch.Generator().manual_seed(42)).to(torch.bfloat16)
+    lin = ow.linear(x.float().numpy(), qw, qz, sc, accumulate="fp64")
+    ref = lin + res.float().numpy()
+    out = res.clone().to(gpu)
+    y = ops.linear(x.to(gpu), W4A16Weight.from_numpy(qw, qz, sc, device=gpu), residual=out, out=out)
+    err = np.abs(y.float().cpu().numpy() - ref)
+    bound = 2.0 ** -8 * (np.abs(lin) + np.abs(ref)) * 1.01 + 1e-4 * np.abs(ref).max()
+    assert (err <= bound).all()
+
+
+def test_prompt_rows_gate_up(gpu):
+    m, k, inter = 600, 1024, 3072
+    gate = ow.synthetic_tensors(k, inter, seed=43)
+    up = ow.synthetic_tensors(k, inter, seed=44)
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(45)).to(torch.bfloat16)
+    g_ref = ow.linear(x.float().numpy(), *gate, accumulate="fp64")
+    u_ref = ow.linear(x.float().numpy(), *up, accumulate="fp64")
+    w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
+    g, u = ops.gate_up(x.to(gpu), w, swiglu=False)
+    check_linear(g, g_ref)
+    check_linear(u, u_ref)
+    h = ops.gate_up(x.to(gpu), w, swiglu=True).float().cpu()
+    h_chain = (torch.nn.functional.silu(g.float().cpu()).to(torch.bfloat16).float() * u.float().cpu())
+    h_chain = h_chain.to(torch.bfloat16).float()
+    assert (h - h_chain).abs().max() <= 2.0 ** -7 * h_chain.abs().max()
+    assert (h == h_chain).float().mean() > 0.999
+
+
+def test_prompt_rows_other_widths(gpu):
+    """N not a multiple of 128 stays on the 16-row-tile kernel at any M."""
+    m, k, n = 640, 1024, 192
+    qw, qz, sc, x = _inputs(m, k, n, seed=46)
+    ref = ow.linear(x.float().numpy(), qw, qz, sc, accumulate="fp64")
+    check_linear(ops.linear(x.to(gpu), W4A16Weight.from_numpy(qw, qz, sc, device=gpu)), ref)
+
+
 def test_golden_fixture_on_gpu(gpu):
     """The brute-force fixture (tests/golden/make_golden.py): bit-exact weights, linear within tolerance."""
     from pathlib import Path

@@ -489,6 +489,270 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const LinearParams p
   }
 }
 
+// ============================================================================
+// Prompt-sized GEMM (hundreds of rows and more): a 128 x 128 output tile per
+// 512-thread workgroup, 8 waves of 32 x 64 (4 along M x 2 along N; two waves a
+// SIMD within 256 registers), one 128-k tile (= one quantisation group) per step.
+//   * Every operand of a k-tile (activations, packed weights, the group's scale
+//     and zero words) is loaded straight into LDS (global_load_lds, no
+//     registers); three k-tiles are in flight, in three stage buffers.
+//   * The pipeline's waits are all explicit: a wave waits (vmcnt) until its own
+//     loads of the k-tile it is about to compute have landed, the workgroup meets
+//     at a barrier (then everyone's have), and LDS is read with ds_read in inline
+//     asm followed by explicit lgkmcnt waits.  The compiler's own waits for loads
+//     into LDS cover every load in flight (no per-buffer tracking across a loop),
+//     which would serialise the pipeline, and __syncthreads would do the same.
+//   * LDS holds each A fragment as 64 lanes x 16 bytes (row c, k 8 r .. 8 r + 7
+//     of lane 16 r + c, in memory order: one contiguous read, no bank conflicts);
+//     the packed weights as the k-tile's 16 qweight rows in pairs (one 1 KB load
+//     per pair, 128 bytes of padding between pairs: the four rows of a fragment
+//     read meet two-way bank conflicts at most).
+//   * Arithmetic as the decode kernel: MFMA over bf16(128 + q), an all-ones MFMA
+//     for the row sums, per group and column total += scale * (dot + zb * rowsum).
+// ============================================================================
+constexpr int GM_BM = 128, GM_BN = 128;
+constexpr int GM_WAVES = 8;
+constexpr int GM_THREADS = 64 * GM_WAVES;
+constexpr int GM_WN = GM_BN / 64;                        // waves along N (64 columns each)
+constexpr int GM_MF = GM_BM / (GM_WAVES / GM_WN) / 16;   // 16-row fragments per wave (2)
+constexpr int GM_AF = GM_BM / 16 * KSG;       // A fragments per k-tile (1 KB each)
+constexpr int GM_AF_W = GM_AF / GM_WAVES;     // issued per wave
+constexpr int GM_BPAIR = GS / 8 / 2;          // qweight row pairs per k-tile (1 KB each with GM_BN = 128)
+constexpr int GM_BROW = GM_BN;                // words per qweight row of the tile
+constexpr int GM_BPAIR_W = 2 * GM_BROW + 32;  // words per padded row pair
+static_assert(GM_BPAIR == GM_WAVES && GM_BN == 128, "one weight row pair per wave, 1 KB loads");
+// loads per wave per k-tile: its A fragments and its weight row pair; wave 0 also
+// loads the scale and zero words
+constexpr int GM_OPS = GM_AF_W + 1;
+constexpr int GM_OPS0 = GM_OPS + 2;
+constexpr int GM_STAGES = 3;
+
+struct GemmStage {
+  u32x4 a[GM_AF * 64];
+  uint32_t b[GM_BPAIR * GM_BPAIR_W];
+  uint32_t qs[64];          // fp16 scales of the tile's 128 columns, two per word
+  uint32_t qz[64];          // qzeros words of the tile's columns (16 used)
+};
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void global_void_t;
+
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds((global_void_t*)src, (lds_void_t*)lds, 4, 0, 0);
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+__device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+
+// Workgroup barrier that orders memory accesses for the compiler without the
+// hardware waits of __syncthreads (loads it must cover are waited for first).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// k-tile kt into stage st (rows past M reload row M - 1; their outputs are never
+// stored).  Each wave issues GM_OPS loads, wave 0 GM_OPS0.
+__device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0, int kt, int wave, int lane,
+                                           GemmStage& st) {
+  const int c = lane & 15, r = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < GM_AF_W; ++i) {
+    const int f = wave * GM_AF_W + i, mi = f / KSG, ks = f % KSG;
+    const int m = min(m0 + 16 * mi + c, p.M - 1);
+    lds_dma16(p.x + (size_t)m * p.ldx + kt * GS + 32 * ks + 8 * r, &st.a[f * 64]);
+  }
+  // qweight rows 2 wave, 2 wave + 1 of the k-tile: lane l takes words 4 (l % 32) .. + 3 of row 2 wave + l / 32
+  lds_dma16(p.qw + (size_t)(kt * (GS / 8) + 2 * wave + (lane >> 5)) * p.N + n0 + 4 * (lane & 31),
+            &st.b[wave * GM_BPAIR_W]);
+  if (wave == 0) {
+    lds_dma4(p.sc + (size_t)kt * p.N + n0 + 2 * lane, &st.qs[0]);
+    lds_dma4(p.qz + (size_t)kt * (p.N >> 3) + (n0 >> 3) + min(lane, GM_BN / 8 - 1), &st.qz[0]);
+  }
+}
+
+// Waits until this wave's loads of the k-tile before the most recent one have landed.
+__device__ __forceinline__ void gemm_wait(int wave) {
+  if (wave == 0) wait_vm<GM_OPS0>();
+  else wait_vm<GM_OPS>();
+}
+
+// Fragments of k-step ks: A of this wave's rows, B of its columns.
+struct GemmFrags {
+  u32x4 a[GM_MF];
+  uint32_t b[4];
+};
+
+__device__ __forceinline__ void gemm_read(uint32_t abase, uint32_t bbase, int ks, int wm, int wn, GemmFrags& f) {
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi) f.a[mi] = lds_read16(abase + ((GM_MF * wm + mi) * KSG + ks) * 1024);
+  // qweight row 4 ks + r (lane r = lane / 16, folded into bbase), column 64 wn + 16 j + c
+#pragma unroll
+  for (int j = 0; j < 4; ++j) f.b[j] = lds_read4(bbase + 4 * (2 * ks * GM_BPAIR_W + 64 * wn + 16 * j));
+}
+
+// Waits for the LDS reads in flight except the most recent N (register ties keep
+// the uses of the waited fragments after the wait).
+template <int N>
+__device__ __forceinline__ void wait_lds(GemmFrags& f) {
+  static_assert(N == 0 || N == 2 + 4, "one k-step of fragments or none");
+  if constexpr (N == 0)
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.b[0]), "+v"(f.b[1]), "+v"(f.b[2]),
+                 "+v"(f.b[3]));
+  else
+    asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.b[0]), "+v"(f.b[1]), "+v"(f.b[2]),
+                 "+v"(f.b[3]));
+}
+
+__device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn, int lane, int ncol0,
+                                             f32x4 (&total)[GM_MF][4]) {
+  static_assert(GM_MF == 2, "wait_lds ties two A fragments");
+  const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane;
+  // lane (r, c): qweight row 4 ks + r = pair 2 ks + r / 2, row r % 2 of the pair; column c
+  const int rr = lane >> 4, cc = lane & 15;
+  const uint32_t bbase = lds_addr(&st.b[0]) + 4 * ((rr >> 1) * GM_BPAIR_W + (rr & 1) * GM_BROW + cc);
+  // this lane's columns: ncol0 + 16 j, tile-local 64 wn + c + 16 j
+  const int lc = ncol0 & (GM_BN - 1);
+  uint32_t sw[4], zw[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sw[j] = lds_read4(lds_addr(&st.qs[0]) + 4 * ((lc + 16 * j) >> 1));
+    zw[j] = lds_read4(lds_addr(&st.qz[0]) + 4 * ((lc + 16 * j) >> 3));
+  }
+  const bf16x8 ones = ones_operand();
+  f32x4 P[GM_MF][4], xs[GM_MF];
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi) {
+    xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) P[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  GemmFrags f0, f1;
+  gemm_read(abase, bbase, 0, wm, wn, f0);
+#pragma unroll
+  for (int ks = 0; ks < KSG; ++ks) {
+    GemmFrags& cur = (ks & 1) ? f1 : f0;
+    GemmFrags& nxt = (ks & 1) ? f0 : f1;
+    if (ks + 1 < KSG) {
+      gemm_read(abase, bbase, ks + 1, wm, wn, nxt);
+      wait_lds<6>(cur);
+    } else {
+      wait_lds<0>(cur);
+    }
+    bf16x8 a[GM_MF], b[4];
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi) a[mi] = a_operand(cur.a[mi]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) b[j] = b_operand(cur.b[j]);
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi) {
+      xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], ones, xs[mi], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], b[j], P[mi][j], 0, 0, 0);
+    }
+  }
+  // the scale and zero reads were issued first: done with the last wait
+  const int zshift = (ncol0 & 7) * 4;   // the same for every fragment (16 j keeps the low bits)
+  const bool odd = ncol0 & 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float zb = -(float)(128 + 1 + ((zw[j] >> zshift) & 0xFu));
+    const float sc = f16_to_f32(odd ? (sw[j] >> 16) : (sw[j] & 0xFFFFu));
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[mi][j][i] = fmaf(sc, fmaf(zb, xs[mi][i], P[mi][j][i]), total[mi][j][i]);
+  }
+}
+
+__global__ __launch_bounds__(GM_THREADS) void w4a16_gemm_kernel(const LinearParams p) {
+  __shared__ GemmStage stg[GM_STAGES];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / GM_WN, wn = wave % GM_WN;
+  const int c = lane & 15, r = lane >> 4;
+  // tiles in row-major order (row tile major), each XCD taking one contiguous
+  // range of them so that the row tiles it works on stay in its L2
+  const int MT = (p.M + GM_BM - 1) / GM_BM, NT = p.N / GM_BN;
+  const int T = MT * NT, id = blockIdx.x;
+  const int tile = (T & 7) ? id : (id & 7) * (T >> 3) + (id >> 3);
+  const int m0 = (tile / NT) * GM_BM, n0 = (tile % NT) * GM_BN;
+  const int ncol0 = n0 + 64 * wn + c;          // this lane's column in fragment 0
+  const int KT = p.K / GS;
+
+  f32x4 total[GM_MF][4];
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) total[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Step kt: load k-tile kt + 2 (a prefetch past the last k-tile loads the last
+  // one again into a stage no longer read, so every step issues the same loads),
+  // compute k-tile kt, then wait until this wave's loads of k-tile kt + 1 have
+  // landed and meet the other waves (their loads have landed, and the stage of
+  // k-tile kt is free).
+  gemm_issue(p, m0, n0, 0, wave, lane, stg[0]);
+  gemm_issue(p, m0, n0, min(1, KT - 1), wave, lane, stg[1]);
+  gemm_wait(wave);
+  lds_barrier();
+  for (int kt = 0; kt < KT; ++kt) {
+    gemm_issue(p, m0, n0, min(kt + 2, KT - 1), wave, lane, stg[(kt + 2) % GM_STAGES]);
+    gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
+    gemm_wait(wave);
+    lds_barrier();
+  }
+  wait_vm<0>();   // no load into LDS may outlive the workgroup
+
+  // epilogue: total[mi][j][i] is row m0 + 16 (GM_MF wm + mi) + 4 r + i, column ncol0 + 16 j
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + 16 * (GM_MF * wm + mi) + 4 * r + i;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = ncol0 + 16 * j;
+        float v = total[mi][j][i];
+        if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
+          if (m < p.M) {
+            if (p.epi == EPI_RESIDUAL) v = round_bf16(v) + bf16_to_f32(p.residual[(size_t)m * p.ldy + n]);
+            p.y0[(size_t)m * p.ldy + n] = (uint16_t)f32_to_bf16(v);
+          }
+        } else {
+          // interleaved pair: gate in the even column (this lane when c is even), up in the odd
+          const float other = __shfl_xor(v, 1, 64);
+          if ((c & 1) == 0 && m < p.M) {
+            const float g = round_bf16(v), u = round_bf16(other);
+            const size_t off = (size_t)m * p.ldy + (n >> 1);
+            if (p.epi == EPI_SWIGLU) {
+              p.y0[off] = (uint16_t)f32_to_bf16(round_bf16(silu_f32(g)) * u);
+            } else {
+              p.y0[off] = (uint16_t)f32_to_bf16(g);
+              p.y1[off] = (uint16_t)f32_to_bf16(u);
+            }
+          }
+        }
+      }
+    }
+}
+
 __global__ void dequant_f32_kernel(const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
                                    const uint16_t* __restrict__ sc, int K, int N, float* __restrict__ W) {
   const int n = blockIdx.x;
@@ -644,6 +908,14 @@ hipError_t launch_plan(const Plan& pl, const LinearParams& p, bool norm, hipStre
   return hipErrorInvalidValue;
 }
 
+// Rows from which the LDS-tiled GEMM replaces the 16-row-tile kernel.
+int gemm_min_rows() {
+#ifdef T2I_TUNING
+  if (const char* env = getenv("T2I_GEMM_MIN_M")) return atoi(env);
+#endif
+  return 512;
+}
+
 int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
                   int K, int N, int group_size) {
   if (!qweight || !qzeros || !scales) return fail(T2I_ERR_NULL, "qweight/qzeros/scales must not be NULL");
@@ -673,6 +945,24 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
   }
   const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
+  if (!gamma && M >= gemm_min_rows() && N % GM_BN == 0) {
+    // prompt-sized: the LDS-tiled GEMM
+    LinearParams p{};
+    p.x = x;
+    p.qw = reinterpret_cast<const uint32_t*>(qweight);
+    p.qz = reinterpret_cast<const uint32_t*>(qzeros);
+    p.sc = scales;
+    p.residual = residual;
+    p.y0 = y0;
+    p.y1 = y1;
+    p.M = M; p.K = K; p.N = N;
+    p.ldx = K;
+    p.ldy = paired ? N / 2 : N;
+    p.epi = epi;
+    const unsigned tiles = (unsigned)((M + GM_BM - 1) / GM_BM) * (unsigned)(N / GM_BN);
+    hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p);
+    return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
+  }
   const Plan pl = plan_linear(M, K, N, paired);
   LinearParams p{};
   p.x = x;
