@@ -130,11 +130,14 @@ def test_decode_attention_out_of_range_position_is_inert(gpu):
     assert torch.equal(kc, kc0)
 
 
-@pytest.mark.parametrize("m,v", [(16, 151936), (1, 4096), (5, 1040), (20, 2048)])
-def test_lm_head_argmax(gpu, m, v):
-    g = torch.Generator().manual_seed(v)
-    h = torch.randn(m, 1024, generator=g).to(BF16)
-    e = torch.randn(v, 1024, generator=g).to(BF16)
+@pytest.mark.parametrize("m,v,k", [(16, 151936, 1024), (1, 4096, 1024), (5, 1040, 1024), (20, 2048, 1024),
+                                   (3, 1040, 64), (7, 528, 128), (16, 2064, 192), (2, 4096, 2048)])
+def test_lm_head_argmax(gpu, m, v, k):
+    """Slices of 64 k: one (peeled), two, an odd count after the loop, and K = 2048
+    (the staged tile spans two load batches)."""
+    g = torch.Generator().manual_seed(v + k)
+    h = torch.randn(m, k, generator=g).to(BF16)
+    e = torch.randn(v, k, generator=g).to(BF16)
     ref = h.double() @ e.double().T
     keys = torch.zeros(m, dtype=torch.int64, device=gpu)
     logits = torch.empty(m, v, dtype=torch.float32, device=gpu)
