@@ -146,25 +146,31 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
 #pragma unroll
   for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per thread
+  // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per thread.
+  // K chunk q: key q / 16, dims 8 (q % 16) (a wave stores 4 whole rows, 16 bytes a
+  // lane).  V chunk q: key q % 64, dims 8 (q / 64): the transposed store then
+  // writes 64 consecutive keys of one dim per instruction (conflict-free), where
+  // the K mapping would put the 16 lanes of a key row 8 rows of s_vt apart, all in
+  // one bank.  Loads are unconditional (keys past kend reload key kend - 1 and are
+  // zeroed after the load).
   auto load_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int q16 = tid + 256 * u;        // chunk: key q16 / 16, dims 8 * (q16 % 16)
-      const int key = kb * PF_KEYS + (q16 >> 4);
-      kr[u] = vr[u] = u32x4{0u, 0u, 0u, 0u};
-      if (key < kend) {
-        kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)key * D + 8 * (q16 & 15));
-        vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)key * D + 8 * (q16 & 15));
-      }
+      const int q16 = tid + 256 * u;
+      const int kkey = kb * PF_KEYS + (q16 >> 4);
+      const int vkey = kb * PF_KEYS + (q16 & 63);
+      kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)min(kkey, kend - 1) * D + 8 * (q16 & 15));
+      vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)min(vkey, kend - 1) * D + 8 * (q16 >> 6));
+      kr[u] = kkey < kend ? kr[u] : u32x4{0u, 0u, 0u, 0u};
+      vr[u] = vkey < kend ? vr[u] : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_block = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int q16 = tid + 256 * u;
-      const int key = q16 >> 4, d0 = 8 * (q16 & 15);
-      *reinterpret_cast<u32x4*>(s_k + key * PF_KLD + d0) = kr[u];
+      *reinterpret_cast<u32x4*>(s_k + (q16 >> 4) * PF_KLD + 8 * (q16 & 15)) = kr[u];
+      const int key = q16 & 63, d0 = 8 * (q16 >> 6);
       const uint32_t w[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
