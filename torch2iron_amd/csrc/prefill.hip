@@ -80,6 +80,7 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepPara
 // causal GQA flash attention over the cache
 // ============================================================================
 constexpr int PF_ROWS = 64;                 // query rows per workgroup (over the kv head's q heads)
+constexpr int PF_MF = 1;                    // 16-row fragments per wave (4 waves x 16 rows)
 constexpr int PF_KEYS = 64;                 // keys per block
 constexpr int PF_KLD = PF_D + 8;            // K tile row stride (bf16): 272 bytes
 constexpr int PF_VLD = PF_KEYS + 8;         // transposed V tile row stride: 144 bytes
@@ -94,15 +95,19 @@ struct PrefillAttnParams {
   float scale_log2;       // D^-1/2 * log2(e)
 };
 
-// One workgroup per (query block, kv head h, sequence b); 4 waves of 16 query
-// rows.  Row j of the 64 is q head h * Q + j / BQ at prompt row t0 + j % BQ
-// (BQ = 64 / Q), so the q heads sharing kv head h share every K / V block.
+// One workgroup per (query block, kv head h, sequence b); 4 waves of PF_MF
+// 16-row MFMA fragments.  Row j of the PF_ROWS is q head h * Q + j / BQ at
+// prompt row t0 + j % BQ (BQ = PF_ROWS / Q), so the q heads sharing kv head h
+// share every K / V block.  Measured slower at 16 sequences x 512 rows: two
+// fragments a wave (128 rows a workgroup: 141 against 121 us a layer), and P
+// written as 32-bit words of key pairs swapped between neighbouring lanes.
 //   S = Q K^T: A = q rows (registers, 4 k-steps of 32 dims), B = K from LDS;
 //   online softmax per row in fp32 (rows 4r + i of the lane's MFMA output);
 //   O += P V: P goes to A layout through a per-wave LDS tile, B = V^T from LDS.
 template <int Q>
 __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAttnParams p) {
   constexpr int D = PF_D;
+  constexpr int MF = PF_MF;
   constexpr int BQ = PF_ROWS / Q;           // prompt rows per q head in the tile
   const int t0 = blockIdx.x * BQ;
   const int h = blockIdx.y;
@@ -115,36 +120,41 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
 
   __shared__ __align__(16) uint16_t s_k[PF_KEYS * PF_KLD];     // [key][dim]
   __shared__ __align__(16) uint16_t s_vt[D * PF_VLD];          // [dim][key]
-  __shared__ __align__(16) uint16_t s_p[4][16 * PF_PLD];       // per wave [row][key]
+  __shared__ __align__(16) uint16_t s_p[4][MF * 16 * PF_PLD];  // per wave [row][key]
 
-  // ---- the wave's 16 query rows as A operands (row c of the wave) ----
-  const int jrow_a = wave * 16 + c;
-  const int t_a = t0 + jrow_a % BQ;
-  const int head_a = h * Q + jrow_a / BQ;
-  u32x4 qa[4];
+  // ---- the wave's query rows as A operands (fragment mi: row c) ----
+  u32x4 qa[MF][4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    qa[ks] = u32x4{0u, 0u, 0u, 0u};
-    if (t_a < p.T)
-      qa[ks] = *reinterpret_cast<const u32x4*>(p.q + (((size_t)b * p.Hq + head_a) * p.T + t_a) * D + ks * 32 + 8 * r);
-  }
-  // the rows this lane holds in MFMA outputs: 4r + i of the wave
-  int qpos[4];
+  for (int mi = 0; mi < MF; ++mi) {
+    const int jrow = wave * 16 * MF + mi * 16 + c;
+    const int t_a = t0 + jrow % BQ;
+    const int head_a = h * Q + jrow / BQ;
+    const uint16_t* src = p.q + (((size_t)b * p.Hq + head_a) * p.T + min(t_a, p.T - 1)) * D + 8 * r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int j = wave * 16 + 4 * r + i;
-    qpos[i] = p.p0 + t0 + j % BQ;            // absolute query position (masks keys beyond it)
+    for (int ks = 0; ks < 4; ++ks) qa[mi][ks] = *reinterpret_cast<const u32x4*>(src + ks * 32);
   }
+  // the rows this lane holds in MFMA outputs: 4r + i of each fragment
+  int qpos[MF][4];
+#pragma unroll
+  for (int mi = 0; mi < MF; ++mi)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = wave * 16 * MF + mi * 16 + 4 * r + i;
+      qpos[mi][i] = p.p0 + t0 + j % BQ;        // absolute query position (masks keys beyond it)
+    }
   const int last_t = min(t0 + BQ, p.T) - 1;
   const int kend = p.p0 + last_t + 1;        // keys [0, kend) can be attended
   const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.cap * D;
 
-  float m[4], l[4];
-  f32x4 o[8];
+  float m[MF][4], l[MF][4];
+  f32x4 o[MF][8];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { m[i] = -INFINITY; l[i] = 0.0f; }
+  for (int mi = 0; mi < MF; ++mi) {
 #pragma unroll
-  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 4; ++i) { m[mi][i] = -INFINITY; l[mi][i] = 0.0f; }
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per thread.
   // K chunk q: key q / 16, dims 8 (q % 16) (a wave stores 4 whole rows, 16 bytes a
@@ -181,6 +191,7 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
   };
 
   const int nblocks = (kend + PF_KEYS - 1) / PF_KEYS;
+  uint16_t* pt = s_p[wave];
   u32x4 kr[4], vr[4];
   load_block(0, kr, vr);
   for (int kb = 0; kb < nblocks; ++kb) {
@@ -189,79 +200,90 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
     __syncthreads();
     if (kb + 1 < nblocks) load_block(kb + 1, kr, vr);   // next block in flight during this one
 
-    // ---- S = Q K^T for 4 key tiles of 16 ----
-    f32x4 s[4];
+    // ---- S = Q K^T for 4 key tiles of 16; each K fragment feeds every row fragment ----
+    f32x4 s[MF][4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi) s[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const u32x4 kb16 = *reinterpret_cast<const u32x4*>(s_k + (n * 16 + c) * PF_KLD + ks * 32 + 8 * r);
-        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[ks]),
-                                                       __builtin_bit_cast(bf16x8, kb16), s[n], 0, 0, 0);
+#pragma unroll
+        for (int mi = 0; mi < MF; ++mi)
+          s[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[mi][ks]),
+                                                             __builtin_bit_cast(bf16x8, kb16), s[mi][n], 0, 0, 0);
       }
     }
-    // ---- online softmax (log2 domain), causal mask ----
-    float pv[4][4];   // [i][n]
+    // ---- online softmax (log2 domain), causal mask; P into the wave's LDS tile ----
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = -INFINITY;
+    for (int mi = 0; mi < MF; ++mi) {
+      float pv[4][4];   // [i][n]
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const int key = kb * PF_KEYS + n * 16 + c;
-        const float v = key <= qpos[i] ? s[n][i] * p.scale_log2 : -INFINITY;
-        pv[i][n] = v;
-        mx = fmaxf(mx, v);
+      for (int i = 0; i < 4; ++i) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const int key = kb * PF_KEYS + n * 16 + c;
+          const float v = key <= qpos[mi][i] ? s[mi][n][i] * p.scale_log2 : -INFINITY;
+          pv[i][n] = v;
+          mx = fmaxf(mx, v);
+        }
+        mx = row_max16(mx);
+        const float mn = fmaxf(m[mi][i], mx);
+        const float f = m[mi][i] > -INFINITY ? __builtin_amdgcn_exp2f(m[mi][i] - mn) : 0.0f;
+        float sum = 0.0f;
+#pragma unroll
+        for (int n = 0; n < 4; ++n) {
+          const float e = pv[i][n] > -INFINITY ? round_bf16(__builtin_amdgcn_exp2f(pv[i][n] - mn)) : 0.0f;
+          pv[i][n] = e;
+          sum += e;
+        }
+        sum = row_sum16(sum);
+        l[mi][i] = l[mi][i] * f + sum;
+        m[mi][i] = mn;
+#pragma unroll
+        for (int n = 0; n < 8; ++n) o[mi][n][i] *= f;
       }
-      mx = row_max16(mx);
-      const float mn = fmaxf(m[i], mx);
-      const float f = m[i] > -INFINITY ? exp2f(m[i] - mn) : 0.0f;
-      float sum = 0.0f;
 #pragma unroll
-      for (int n = 0; n < 4; ++n) {
-        const float e = pv[i][n] > -INFINITY ? round_bf16(exp2f(pv[i][n] - mn)) : 0.0f;
-        pv[i][n] = e;
-        sum += e;
-      }
-      sum = row_sum16(sum);
-      l[i] = l[i] * f + sum;
-      m[i] = mn;
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int n = 0; n < 8; ++n) o[n][i] *= f;
+        for (int n = 0; n < 4; ++n) pt[(mi * 16 + 4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
     }
-    // ---- P to A layout through the wave's LDS tile ----
-    uint16_t* pt = s_p[wave];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int n = 0; n < 4; ++n) pt[(4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
     __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): the wave's P writes are done
     __builtin_amdgcn_wave_barrier();
-    // ---- O += P V: 2 k-steps of 32 keys, 8 dim tiles ----
+    // ---- O += P V: 2 k-steps of 32 keys, 8 dim tiles; each V fragment feeds every row fragment ----
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const u32x4 pa = *reinterpret_cast<const u32x4*>(pt + c * PF_PLD + ks * 32 + 8 * r);
+      u32x4 pa[MF];
+#pragma unroll
+      for (int mi = 0; mi < MF; ++mi)
+        pa[mi] = *reinterpret_cast<const u32x4*>(pt + (mi * 16 + c) * PF_PLD + ks * 32 + 8 * r);
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
         const u32x4 vb = *reinterpret_cast<const u32x4*>(s_vt + (n * 16 + c) * PF_VLD + ks * 32 + 8 * r);
-        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa),
-                                                       __builtin_bit_cast(bf16x8, vb), o[n], 0, 0, 0);
+#pragma unroll
+        for (int mi = 0; mi < MF; ++mi)
+          o[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[mi]),
+                                                             __builtin_bit_cast(bf16x8, vb), o[mi][n], 0, 0, 0);
       }
     }
   }
 
   // ---- normalise and store: lane holds rows 4r + i, dims n * 16 + c ----
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int j = wave * 16 + 4 * r + i;
-    const int t = t0 + j % BQ;
-    if (t >= p.T) continue;
-    const int head = h * Q + j / BQ;
-    uint16_t* dst = p.out + ((size_t)b * p.T + t) * p.Hq * D + (size_t)head * D;
-    const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+  for (int mi = 0; mi < MF; ++mi)
 #pragma unroll
-    for (int n = 0; n < 8; ++n) dst[n * 16 + c] = (uint16_t)f32_to_bf16(o[n][i] * inv);
-  }
+    for (int i = 0; i < 4; ++i) {
+      const int j = wave * 16 * MF + mi * 16 + 4 * r + i;
+      const int t = t0 + j % BQ;
+      if (t >= p.T) continue;
+      const int head = h * Q + j / BQ;
+      uint16_t* dst = p.out + ((size_t)b * p.T + t) * p.Hq * D + (size_t)head * D;
+      const float inv = l[mi][i] > 0.0f ? 1.0f / l[mi][i] : 0.0f;
+#pragma unroll
+      for (int n = 0; n < 8; ++n) dst[n * 16 + c] = (uint16_t)f32_to_bf16(o[mi][n][i] * inv);
+    }
 }
 
 }  // namespace t2i
