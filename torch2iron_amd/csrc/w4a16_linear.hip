@@ -526,6 +526,10 @@ static_assert(GM_BPAIR == GM_WAVES && GM_BN == 128, "one weight row pair per wav
 constexpr int GM_OPS = GM_AF_W + 1;
 constexpr int GM_OPS0 = GM_OPS + 2;
 constexpr int GM_STAGES = 3;
+// epilogue: each wave parks its 32 x 64 results as bf16 in LDS (rows padded to
+// 72 values) and stores them back as 16-byte row pieces
+constexpr int GM_EP_LD = 64 + 8;
+constexpr int GM_EP_WAVE = 2 * 32 * GM_EP_LD;   // two regions (paired: gate and up outputs)
 
 struct GemmStage {
   u32x4 a[GM_AF * 64];
@@ -703,54 +707,100 @@ __global__ __launch_bounds__(GM_THREADS) void w4a16_gemm_kernel(const LinearPara
 #pragma unroll
     for (int j = 0; j < 4; ++j) total[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Step kt: load k-tile kt + 2 (a prefetch past the last k-tile loads the last
-  // one again into a stage no longer read, so every step issues the same loads),
-  // compute k-tile kt, then wait until this wave's loads of k-tile kt + 1 have
-  // landed and meet the other waves (their loads have landed, and the stage of
-  // k-tile kt is free).
+  // Step kt: load k-tile kt + 2, compute k-tile kt, then wait until this wave's
+  // loads of k-tile kt + 1 have landed and meet the other waves (their loads have
+  // landed, and the stage of k-tile kt is free).  The last two steps issue no
+  // loads (peeled), so nothing is in flight when the epilogue starts.
   gemm_issue(p, m0, n0, 0, wave, lane, stg[0]);
-  gemm_issue(p, m0, n0, min(1, KT - 1), wave, lane, stg[1]);
-  gemm_wait(wave);
+  if (KT > 1) {
+    gemm_issue(p, m0, n0, 1, wave, lane, stg[1]);
+    gemm_wait(wave);
+  } else {
+    wait_vm<0>();
+  }
   lds_barrier();
-  for (int kt = 0; kt < KT; ++kt) {
-    gemm_issue(p, m0, n0, min(kt + 2, KT - 1), wave, lane, stg[(kt + 2) % GM_STAGES]);
+  int kt = 0;
+  for (; kt + 2 < KT; ++kt) {
+    gemm_issue(p, m0, n0, kt + 2, wave, lane, stg[(kt + 2) % GM_STAGES]);
     gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
     gemm_wait(wave);
     lds_barrier();
   }
-  wait_vm<0>();   // no load into LDS may outlive the workgroup
+  if (kt + 1 < KT) {
+    gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
+    wait_vm<0>();
+    lds_barrier();
+    ++kt;
+  }
+  gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
+  lds_barrier();   // every wave is done reading the stages: they become the epilogue's tiles
 
-  // epilogue: total[mi][j][i] is row m0 + 16 (GM_MF wm + mi) + 4 r + i, column ncol0 + 16 j
+  // ---- epilogue: total[mi][j][i] is row 16 (GM_MF wm + mi) + 4 r + i, column
+  // 64 wn + 16 j + c of the tile.  Each wave parks its bf16 results in its own
+  // LDS region, row-major, then stores them as 16-byte row pieces (a lane's
+  // MFMA outputs are one column of four rows, which would take 2-byte stores).
+  uint16_t* ep = reinterpret_cast<uint16_t*>(&stg[0]) + wave * GM_EP_WAVE;
+  const int row0 = m0 + 16 * GM_MF * wm;       // the wave's first row
+  if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
 #pragma unroll
-  for (int mi = 0; mi < GM_MF; ++mi)
+    for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + 16 * (GM_MF * wm + mi) + 4 * r + i;
+      for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int n = ncol0 + 16 * j;
-        float v = total[mi][j][i];
-        if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
-          if (m < p.M) {
-            if (p.epi == EPI_RESIDUAL) v = round_bf16(v) + bf16_to_f32(p.residual[(size_t)m * p.ldy + n]);
-            p.y0[(size_t)m * p.ldy + n] = (uint16_t)f32_to_bf16(v);
-          }
-        } else {
-          // interleaved pair: gate in the even column (this lane when c is even), up in the odd
+        for (int j = 0; j < 4; ++j)
+          ep[(16 * mi + 4 * r + i) * GM_EP_LD + 16 * j + c] = (uint16_t)f32_to_bf16(total[mi][j][i]);
+    __builtin_amdgcn_wave_barrier();
+    // 32 rows x 64 columns = 256 pieces of 8 values, 4 a lane
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q = lane + 64 * u, row = q >> 3, ch = q & 7;
+      const int m = row0 + row;
+      const size_t off = (size_t)min(m, p.M - 1) * p.ldy + n0 + 64 * wn + 8 * ch;
+      u32x4 v = *reinterpret_cast<const u32x4*>(ep + row * GM_EP_LD + 8 * ch);
+      if (p.epi == EPI_RESIDUAL) {
+        const u32x4 rv = *reinterpret_cast<const u32x4*>(p.residual + off);
+        v.x = pack_bf16x2(bf16_lo(v.x) + bf16_lo(rv.x), bf16_hi(v.x) + bf16_hi(rv.x));
+        v.y = pack_bf16x2(bf16_lo(v.y) + bf16_lo(rv.y), bf16_hi(v.y) + bf16_hi(rv.y));
+        v.z = pack_bf16x2(bf16_lo(v.z) + bf16_lo(rv.z), bf16_hi(v.z) + bf16_hi(rv.z));
+        v.w = pack_bf16x2(bf16_lo(v.w) + bf16_lo(rv.w), bf16_hi(v.w) + bf16_hi(rv.w));
+      }
+      if (m < p.M) *reinterpret_cast<u32x4*>(p.y0 + off) = v;
+    }
+  } else {
+    // interleaved pairs: gate in the even column, up in the odd one; output column
+    // (64 wn + 16 j + c) / 2 of the tile's 64.  SwiGLU: the even lane parks
+    // bf16(silu(g)) * u in region 0; paired: gate to region 0, up to region 1.
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float v = total[mi][j][i];
           const float other = __shfl_xor(v, 1, 64);
-          if ((c & 1) == 0 && m < p.M) {
-            const float g = round_bf16(v), u = round_bf16(other);
-            const size_t off = (size_t)m * p.ldy + (n >> 1);
-            if (p.epi == EPI_SWIGLU) {
-              p.y0[off] = (uint16_t)f32_to_bf16(round_bf16(silu_f32(g)) * u);
-            } else {
-              p.y0[off] = (uint16_t)f32_to_bf16(g);
-              p.y1[off] = (uint16_t)f32_to_bf16(u);
-            }
+          const int slot = (16 * mi + 4 * r + i) * GM_EP_LD + 8 * j + (c >> 1);
+          if (p.epi == EPI_SWIGLU) {
+            if ((c & 1) == 0)
+              ep[slot] = (uint16_t)f32_to_bf16(round_bf16(silu_f32(round_bf16(v))) * round_bf16(other));
+          } else {
+            ep[slot + ((c & 1) ? 32 * GM_EP_LD : 0)] = (uint16_t)f32_to_bf16(v);
           }
         }
+    __builtin_amdgcn_wave_barrier();
+    // 32 rows x 32 output columns per region = 128 pieces of 8 values, 2 a lane
+    const int regions = p.epi == EPI_SWIGLU ? 1 : 2;
+    for (int reg = 0; reg < regions; ++reg) {
+      uint16_t* dst = reg ? p.y1 : p.y0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int q = lane + 64 * u, row = q >> 2, ch = q & 3;
+        const int m = row0 + row;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ep + reg * 32 * GM_EP_LD + row * GM_EP_LD + 8 * ch);
+        if (m < p.M)
+          *reinterpret_cast<u32x4*>(dst + (size_t)m * p.ldy + ((n0 + 64 * wn) >> 1) + 8 * ch) = v;
       }
     }
+  }
 }
 
 __global__ void dequant_f32_kernel(const uint32_t* __restrict__ qw, const uint32_t* __restrict__ qz,
