@@ -44,6 +44,9 @@ def build(verbose: bool = False) -> Path:
         "-fPIC",
         # packed fp32 VALU forms are kept out of the device code
         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        # leading scalar kernel arguments arrive in SGPRs at wave launch (no
+        # kernarg load before the first address can be formed)
+        "-mllvm", "-amdgpu-kernarg-preload-count=16",
         f"-I{INCLUDE}",
         f"-I{CSRC}",
         *[str(s) for s in sources()],

@@ -135,8 +135,17 @@ __device__ __forceinline__ float state_weight(float m, float M) { return m > -IN
 //   3. with several chunks per (b, h), each chunk stores its state agent-coherently and
 //      the last chunk to arrive merges all of them in chunk order (deterministic) and
 //      writes the bf16 context; it also resets the arrival counter for the next launch.
+// The arguments the first loads need (pos, the qkv rows, the caches, the RoPE
+// table and the shape) lead the argument list as scalars, which the library is
+// built to preload into SGPRs at wave launch; the rest come from p_.
 template <int Q, int ROWS>
-__global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const AttnParams p) {
+__global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int32_t* pos_, const uint16_t* qkv_,
+                                                                       uint16_t* kc_, uint16_t* vc_,
+                                                                       const uint16_t* rope_, int Hkv_, int ctx_cap_,
+                                                                       int Hq_, int splits_, const AttnParams p_) {
+  AttnParams p = p_;
+  p.pos = pos_; p.qkv = qkv_; p.kc = kc_; p.vc = vc_; p.rope = rope_;
+  p.Hkv = Hkv_; p.ctx_cap = ctx_cap_; p.Hq = Hq_; p.splits = splits_;
   constexpr int D = ATT_D;
   constexpr int CHUNK = 16 * ROWS;
   constexpr int NV = (Q + 2 + 3) / 4;   // prologue vectors (q heads, k, v) per wave
@@ -597,7 +606,8 @@ AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
 
 template <int Q, int ROWS>
 hipError_t launch_attention(const AttnParams& p, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_attention_kernel<Q, ROWS>), grid, dim3(ATT_THREADS), 0, s, p);
+  hipLaunchKernelGGL((decode_attention_kernel<Q, ROWS>), grid, dim3(ATT_THREADS), 0, s, p.pos, p.qkv, p.kc, p.vc, p.rope,
+                     p.Hkv, p.ctx_cap, p.Hq, p.splits, p);
   return hipGetLastError();
 }
 
