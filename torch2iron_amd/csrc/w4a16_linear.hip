@@ -77,6 +77,12 @@ __device__ __forceinline__ bf16x8 ones_operand() {
 }
 
 __device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+// g * sigmoid(g) on v_exp_f32 and v_rcp_f32: a few ulp of fp32 from silu_f32 (the
+// result is rounded to bf16 right after).  For the prompt GEMM's epilogue, where
+// the libm exponential and the IEEE division cost more than its k-loop's last steps.
+__device__ __forceinline__ float silu_fast(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
 
 template <int LW>
 __device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&w)[LW]) {
@@ -779,24 +785,32 @@ __global__ __launch_bounds__(GM_THREADS) void w4a16_gemm_kernel(const LinearPara
     }
   } else {
     // interleaved pairs: gate in the even column, up in the odd one; output column
-    // (64 wn + 16 j + c) / 2 of the tile's 64.  SwiGLU: the even lane parks
-    // bf16(silu(g)) * u in region 0; paired: gate to region 0, up to region 1.
+    // (64 wn + 16 j + c) / 2 of the tile's 64.  SwiGLU: of MFMA rows i0, i0 + 1 the
+    // even lane computes row i0 and the odd lane row i0 + 1 (one exchange gives
+    // each its other operand), so every lane evaluates SiLU 16 times, not 32;
+    // results go to region 0.  Paired: gate to region 0, up to region 1.
+    const bool odd = c & 1;
 #pragma unroll
     for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 4; ++j) {
+        if (p.epi == EPI_SWIGLU) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float v = total[mi][j][i];
-          const float other = __shfl_xor(v, 1, 64);
-          const int slot = (16 * mi + 4 * r + i) * GM_EP_LD + 8 * j + (c >> 1);
-          if (p.epi == EPI_SWIGLU) {
-            if ((c & 1) == 0)
-              ep[slot] = (uint16_t)f32_to_bf16(round_bf16(silu_f32(round_bf16(v))) * round_bf16(other));
-          } else {
-            ep[slot + ((c & 1) ? 32 * GM_EP_LD : 0)] = (uint16_t)f32_to_bf16(v);
+          for (int i0 = 0; i0 < 4; i0 += 2) {
+            const float send = odd ? total[mi][j][i0] : total[mi][j][i0 + 1];
+            const float recv = __shfl_xor(send, 1, 64);
+            const float g = round_bf16(odd ? recv : total[mi][j][i0]);
+            const float u = round_bf16(odd ? total[mi][j][i0 + 1] : recv);
+            const int row = 16 * mi + 4 * r + i0 + (odd ? 1 : 0);
+            ep[row * GM_EP_LD + 8 * j + (c >> 1)] = (uint16_t)f32_to_bf16(round_bf16(silu_fast(g)) * u);
           }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            ep[(16 * mi + 4 * r + i) * GM_EP_LD + 8 * j + (c >> 1) + (odd ? 32 * GM_EP_LD : 0)] =
+                (uint16_t)f32_to_bf16(total[mi][j][i]);
         }
+      }
     __builtin_amdgcn_wave_barrier();
     // 32 rows x 32 output columns per region = 128 pieces of 8 values, 2 a lane
     const int regions = p.epi == EPI_SWIGLU ? 1 : 2;
