@@ -507,9 +507,12 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 }
 
 // ============================================================================
-// Prompt-sized GEMM (hundreds of rows and more): a 128 x 128 output tile per
-// 512-thread workgroup, 8 waves of 32 x 64 (4 along M x 2 along N; two waves a
-// SIMD within 256 registers), one 128-k tile (= one quantisation group) per step.
+// Prompt-sized GEMM (hundreds of rows and more): a 64 x 128 output tile per
+// 256-thread workgroup, 4 waves of 32 x 64 (2 along M x 2 along N), one 128-k
+// tile (= one quantisation group) per step.  76.5 KB of LDS and 184 registers a
+// lane let two workgroups share a CU, so one's barriers, prologue and epilogue
+// overlap the other's k-loop (measured faster than one 128 x 128 workgroup of 8
+// waves a CU: gate_up at 8192 rows 225 -> 209 us).
 //   * Every operand of a k-tile (activations, packed weights, the group's scale
 //     and zero words) is loaded straight into LDS (global_load_lds, no
 //     registers); three k-tiles are in flight, in three stage buffers.
@@ -527,8 +530,8 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 //   * Arithmetic as the decode kernel: MFMA over bf16(128 + q), an all-ones MFMA
 //     for the row sums, per group and column total += scale * (dot + zb * rowsum).
 // ============================================================================
-constexpr int GM_BM = 128, GM_BN = 128;
-constexpr int GM_WAVES = 8;
+constexpr int GM_BM = 64, GM_BN = 128;
+constexpr int GM_WAVES = 4;
 constexpr int GM_THREADS = 64 * GM_WAVES;
 constexpr int GM_WN = GM_BN / 64;                        // waves along N (64 columns each)
 constexpr int GM_MF = GM_BM / (GM_WAVES / GM_WN) / 16;   // 16-row fragments per wave (2)
@@ -537,10 +540,11 @@ constexpr int GM_AF_W = GM_AF / GM_WAVES;     // issued per wave
 constexpr int GM_BPAIR = GS / 8 / 2;          // qweight row pairs per k-tile (1 KB each with GM_BN = 128)
 constexpr int GM_BROW = GM_BN;                // words per qweight row of the tile
 constexpr int GM_BPAIR_W = 2 * GM_BROW + 32;  // words per padded row pair
-static_assert(GM_BPAIR == GM_WAVES && GM_BN == 128, "one weight row pair per wave, 1 KB loads");
+constexpr int GM_BPAIR_PW = GM_BPAIR / GM_WAVES;   // weight row pairs loaded per wave
+static_assert(GM_BPAIR % GM_WAVES == 0 && GM_BN == 128, "whole weight row pairs per wave, 1 KB loads");
 // loads per wave per k-tile: its A fragments and its weight row pair; wave 0 also
 // loads the scale and zero words
-constexpr int GM_OPS = GM_AF_W + 1;
+constexpr int GM_OPS = GM_AF_W + GM_BPAIR_PW;
 constexpr int GM_OPS0 = GM_OPS + 2;
 constexpr int GM_STAGES = 3;
 // epilogue: each wave parks its 32 x 64 results as bf16 in LDS (rows padded to
@@ -600,9 +604,13 @@ __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0
     const int m = min(m0 + 16 * mi + c, p.M - 1);
     lds_dma16(p.x + (size_t)m * p.ldx + kt * GS + 32 * ks + 8 * r, &st.a[f * 64]);
   }
-  // qweight rows 2 wave, 2 wave + 1 of the k-tile: lane l takes words 4 (l % 32) .. + 3 of row 2 wave + l / 32
-  lds_dma16(p.qw + (size_t)(kt * (GS / 8) + 2 * wave + (lane >> 5)) * p.N + n0 + 4 * (lane & 31),
-            &st.b[wave * GM_BPAIR_W]);
+  // qweight row pair q = rows 2 q, 2 q + 1 of the k-tile: lane l takes words 4 (l % 32) .. + 3 of row 2 q + l / 32
+#pragma unroll
+  for (int i = 0; i < GM_BPAIR_PW; ++i) {
+    const int q = wave * GM_BPAIR_PW + i;
+    lds_dma16(p.qw + (size_t)(kt * (GS / 8) + 2 * q + (lane >> 5)) * p.N + n0 + 4 * (lane & 31),
+              &st.b[q * GM_BPAIR_W]);
+  }
   if (wave == 0) {
     lds_dma4(p.sc + (size_t)kt * p.N + n0 + 2 * lane, &st.qs[0]);
     lds_dma4(p.qz + (size_t)kt * (p.N >> 3) + (n0 >> 3) + min(lane, GM_BN / 8 - 1), &st.qz[0]);
