@@ -365,6 +365,78 @@ __device__ __forceinline__ void norm_finish(const LinearParams& p, int mbase, in
   }
 }
 
+// Fused RMSNorm when every wave has one chunk (K <= 32 W CK): each wave loads
+// the row tile's values for its own chunk's k-steps straight in A-operand layout
+// (lane 16 r + row: row, k 8 r .. 8 r + 7 of the k-step) with the norm weight of
+// those k, the per-row sums of squares meet through lane shuffles and a small
+// table (fixed order), and the wave normalises its registers, rounding as the
+// standalone RMSNorm (bf16(bf16(x * inv) * w), two values per conversion), into
+// its chunk's A operands: no tile in LDS, no pass over it, one barrier fewer.
+// (Every lane summing its row itself, to drop the second barrier, measured no
+// faster.)
+// Rows past M reload row M - 1: an MFMA output row depends on its own A row only,
+// and rows past M are never stored.
+template <int CK>
+struct NormOwn {
+  u32x4 v[CK];   // the wave's k-steps of the row tile, A layout
+  u32x4 g[CK];   // norm weight 8 r .. 8 r + 7 of each
+};
+
+template <int CK>
+__device__ __forceinline__ void norm_issue_own(const LinearParams& p, int mbase, int ks0, int lane, NormOwn<CK>& nl) {
+  const int row = lane & 15, r = lane >> 4;
+  const uint16_t* xrow = p.x + (size_t)min(mbase + row, p.M - 1) * p.ldx + r * 8;
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+    nl.v[j] = *reinterpret_cast<const u32x4*>(xrow + (ks0 + j) * 32);
+    nl.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
+  }
+}
+
+template <int W, int CK, int LW>
+__device__ __forceinline__ void norm_own(const LinearParams& p, int wave, int lane, bool has_chunk,
+                                         NormOwn<CK>& nl, Chunk<1, LW, CK>& A) {
+  __shared__ float s_ss[W][16];
+  __shared__ float s_inv[16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+    pin(nl.v[j]);
+    const uint32_t a[4] = {nl.v[j].x, nl.v[j].y, nl.v[j].z, nl.v[j].w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
+      ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
+    }
+  }
+  ss = has_chunk ? ss : 0.0f;   // a wave past the last chunk loaded the last k-steps again
+  ss += __shfl_xor(ss, 16, 64);   // the four sub-blocks of a row
+  ss += __shfl_xor(ss, 32, 64);
+  if (lane < 16) s_ss[wave][lane] = ss;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) t += s_ss[w][threadIdx.x];
+    s_inv[threadIdx.x] = round_bf16(1.0f / sqrtf(t / (float)p.K + p.eps));
+  }
+  __syncthreads();
+  const float inv = s_inv[lane & 15];
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+    pin(nl.g[j]);
+    const uint32_t a[4] = {nl.v[j].x, nl.v[j].y, nl.v[j].z, nl.v[j].w};
+    const uint32_t g[4] = {nl.g[j].x, nl.g[j].y, nl.g[j].z, nl.g[j].w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t n1 = pack_bf16x2(bf16_lo(a[e]) * inv, bf16_hi(a[e]) * inv);
+      o[e] = pack_bf16x2(bf16_lo(n1) * bf16_lo(g[e]), bf16_hi(n1) * bf16_hi(g[e]));
+    }
+    A.x[0][j] = u32x4{o[0], o[1], o[2], o[3]};   // memory k order; compute_chunk permutes it
+  }
+}
+
 // Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
 // its own L2.  Neighbouring column blocks share 128-byte lines of qweight,
 // scales and qzeros, so the blocks are renumbered to give each XCD one
@@ -391,6 +463,9 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   p.x = x_; p.qw = qw_; p.sc = sc_; p.qz = qz_; p.N = N_; p.M = M_; p.K = K_; p.ldx = K_; p.chunks = K_ / (32 * CK);
   if constexpr (NKPW > 0) p.gamma = aux_; else p.residual = aux_;
   constexpr bool NORM = NKPW > 0;
+  // NKPW == CK: K <= 32 W CK, so every wave has at most one chunk (registers path)
+  constexpr bool NREG = NORM && NKPW == CK;
+  constexpr bool NLDS = NORM && !NREG;   // the row tile goes through LDS
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
   constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
@@ -421,8 +496,10 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   // Load order: the norm prologue's row tile, then the first weight chunk (every
   // wave loads one: a wave without chunks reloads the last and computes nothing),
   // so that normalising waits for the tile only while the weights are in flight.
-  NormLoads<NORM ? NKPW : 1> nl;
-  if constexpr (NORM) norm_issue<W, NKPW>(p, mbase, wave, lane, nl);
+  NormLoads<NLDS ? NKPW : 1> nl;
+  NormOwn<NREG ? CK : 1> no;
+  if constexpr (NLDS) norm_issue<W, NKPW>(p, mbase, wave, lane, nl);
+  if constexpr (NREG) norm_issue_own<CK>(p, mbase, min(c_begin, p.chunks - 1) * CK, lane, no);
   __builtin_amdgcn_sched_barrier(0);   // keep this load order
   Chunk<MT, LW, CK> A, B, C;
   load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
@@ -435,10 +512,11 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   uint32_t resv[(LW + 1) / 2];
   load_scales<LW>(p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv, ncol & 1);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (NORM) {
+  if constexpr (NLDS) {
     norm_finish<W, NKPW>(p, mbase, wave, lane, nl, a_lds);
     __syncthreads();
   }
+  if constexpr (NREG) norm_own<W, CK, LW>(p, wave, lane, c_begin < c_end, no, A);
   // One word per lane: straight-line schedules for 1, 2 and 3 chunks per wave
   // (every chunk of the wave in flight before the first is computed, each
   // computation waiting for its own chunk only), else a double-buffered loop.
@@ -449,17 +527,17 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   if constexpr (LW == 1) {
     looped = false;
     if (n == 1) {
-      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
     } else if (n == 2) {
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
     } else if (n == 3) {
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 2, ncol, c, r, mbase, C);
-      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, c_begin * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NORM>(C, total, a_lds, (c_begin + 2) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(C, total, a_lds, (c_begin + 2) * CK, lane, zshift);
     } else {
       looped = true;
     }
@@ -467,10 +545,10 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   if (looped) {
     for (int ch = c_begin; ch < c_end; ch += 2) {
       if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NORM>(A, total, a_lds, ch * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, ch * CK, lane, zshift);
       if (ch + 1 >= c_end) break;
       if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 2, ncol, c, r, mbase, A);
-      compute_chunk<MT, LW, CK, NORM>(B, total, a_lds, (ch + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (ch + 1) * CK, lane, zshift);
     }
   }
 
@@ -482,7 +560,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   {
     __shared__ float red_static[NORM ? 1 : W * E * 64];
     float* red = NORM ? reinterpret_cast<float*>(dyn_lds) : red_static;
-    if constexpr (NORM) __syncthreads();   // every wave is done with the normalised rows
+    if constexpr (NLDS) __syncthreads();   // every wave is done with the normalised rows
     if (wave < nw) {
       float* dst = red + wave * E * 64 + lane;
 #pragma unroll
