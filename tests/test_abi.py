@@ -138,6 +138,13 @@ def test_workspace_sizes_are_consistent():
         n = lib.t2i_decode_attention_workspace_bytes(b, hq, hkv, cap)
         assert need <= n <= need + 512, (b, hq, hkv, cap, n, need)
     assert lib.t2i_decode_attention_workspace_bytes(0, 16, 8, 640) == 0
+    # batch 16 x 8 kv heads at 640 slots: 6 splits (768 workgroups, a multiple of the
+    # 256 CUs) instead of 5; at 1088 slots, 9 splits stay (12 would be a third more)
+    for b, cap, splits in ((16, 640, 6), (8, 1088, 9), (32, 640, 5)):
+        units, q = b * 8, 2
+        need = units * 4 + units * splits * q * 2 * 4 + units * splits * q * 128 * 4
+        n = lib.t2i_decode_attention_workspace_bytes(b, 16, 8, cap)
+        assert need <= n <= need + 512, (b, cap, n, need)
 
 
 def test_split_batch_covers_rows():

@@ -99,6 +99,9 @@ def _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed):
     (2, 16, 2, 256, [255, 17]),                                     # 8 q heads per kv head
     (2, 16, 8, 1100, [1099, 300]),                                  # few sequences, long context: split chunks
     (1, 16, 8, 3000, [2500]),                                       # one sequence, 24 chunks (merge groups of 8)
+    # batch 16: 5 chunks of 128 slots would give 640 workgroups, so 6 chunks of 107
+    # (768 = 3 x 256); positions at and around the chunk boundaries
+    (16, 16, 8, 640, [0, 105, 106, 107, 108, 213, 214, 320, 321, 427, 428, 533, 534, 535, 600, 639]),
 ])
 def test_decode_attention_matches_oracle(gpu, b, hq, hkv, ctx_cap, positions, style):
     out, ref, kd, vd, kref, vref, pos = _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed=b + hq)
