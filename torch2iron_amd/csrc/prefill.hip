@@ -14,6 +14,8 @@
 // before that product), and each row's normaliser sums those bf16 weights.
 #include <math.h>
 
+#include <type_traits>
+
 #include "t2i_common.h"
 
 namespace t2i {
@@ -142,6 +144,10 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
       const int j = wave * 16 * MF + mi * 16 + 4 * r + i;
       qpos[mi][i] = p.p0 + t0 + j % BQ;        // absolute query position (masks keys beyond it)
     }
+  // the smallest query position of the wave's rows (wave-uniform): rows j0 ..
+  // j0 + 16 MF - 1 of the tile are prompt rows t0 + j % BQ
+  const int j0 = __builtin_amdgcn_readfirstlane(wave) * 16 * MF;
+  const int qmin = p.p0 + t0 + ((j0 % BQ) + 16 * MF <= BQ ? j0 % BQ : 0);
   const int last_t = min(t0 + BQ, p.T) - 1;
   const int kend = p.p0 + last_t + 1;        // keys [0, kend) can be attended
   const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.cap * D;
@@ -216,40 +222,48 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
       }
     }
     // ---- online softmax (log2 domain), causal mask; P into the wave's LDS tile ----
+    // Blocks that every row of the wave sees whole skip the mask and its guards.
+    auto softmax = [&](auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
 #pragma unroll
-    for (int mi = 0; mi < MF; ++mi) {
-      float pv[4][4];   // [i][n]
+      for (int mi = 0; mi < MF; ++mi) {
+        float pv[4][4];   // [i][n]
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        float mx = -INFINITY;
+        for (int i = 0; i < 4; ++i) {
+          float mx = -INFINITY;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const int key = kb * PF_KEYS + n * 16 + c;
-          const float v = key <= qpos[mi][i] ? s[mi][n][i] * p.scale_log2 : -INFINITY;
-          pv[i][n] = v;
-          mx = fmaxf(mx, v);
+          for (int n = 0; n < 4; ++n) {
+            const int key = kb * PF_KEYS + n * 16 + c;
+            const float v = (!MASK || key <= qpos[mi][i]) ? s[mi][n][i] * p.scale_log2 : -INFINITY;
+            pv[i][n] = v;
+            mx = fmaxf(mx, v);
+          }
+          mx = row_max16(mx);
+          const float mn = fmaxf(m[mi][i], mx);
+          const float f = m[mi][i] > -INFINITY ? __builtin_amdgcn_exp2f(m[mi][i] - mn) : 0.0f;
+          float sum = 0.0f;
+#pragma unroll
+          for (int n = 0; n < 4; ++n) {
+            const float x = round_bf16(__builtin_amdgcn_exp2f(pv[i][n] - mn));
+            const float e = (!MASK || pv[i][n] > -INFINITY) ? x : 0.0f;
+            pv[i][n] = e;
+            sum += e;
+          }
+          sum = row_sum16(sum);
+          l[mi][i] = l[mi][i] * f + sum;
+          m[mi][i] = mn;
+#pragma unroll
+          for (int n = 0; n < 8; ++n) o[mi][n][i] *= f;
         }
-        mx = row_max16(mx);
-        const float mn = fmaxf(m[mi][i], mx);
-        const float f = m[mi][i] > -INFINITY ? __builtin_amdgcn_exp2f(m[mi][i] - mn) : 0.0f;
-        float sum = 0.0f;
 #pragma unroll
-        for (int n = 0; n < 4; ++n) {
-          const float e = pv[i][n] > -INFINITY ? round_bf16(__builtin_amdgcn_exp2f(pv[i][n] - mn)) : 0.0f;
-          pv[i][n] = e;
-          sum += e;
-        }
-        sum = row_sum16(sum);
-        l[mi][i] = l[mi][i] * f + sum;
-        m[mi][i] = mn;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int n = 0; n < 8; ++n) o[mi][n][i] *= f;
+          for (int n = 0; n < 4; ++n)
+            pt[(mi * 16 + 4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int n = 0; n < 4; ++n) pt[(mi * 16 + 4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
-    }
+    };
+    if (kb * PF_KEYS + PF_KEYS - 1 <= qmin) softmax(std::false_type{});
+    else softmax(std::true_type{});
     __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): the wave's P writes are done
     __builtin_amdgcn_wave_barrier();
     // ---- O += P V: 2 k-steps of 32 keys, 8 dim tiles; each V fragment feeds every row fragment ----
