@@ -620,7 +620,7 @@ constexpr int GM_BROW = GM_BN;                // words per qweight row of the ti
 constexpr int GM_BPAIR_W = 2 * GM_BROW + 32;  // words per padded row pair
 constexpr int GM_BPAIR_PW = GM_BPAIR / GM_WAVES;   // weight row pairs loaded per wave
 static_assert(GM_BPAIR % GM_WAVES == 0 && GM_BN == 128, "whole weight row pairs per wave, 1 KB loads");
-// loads per wave per k-tile: its A fragments and its weight row pair; wave 0 also
+// loads per wave per k-tile: its A fragments and its weight row pairs; wave 0 also
 // loads the scale and zero words
 constexpr int GM_OPS = GM_AF_W + GM_BPAIR_PW;
 constexpr int GM_OPS0 = GM_OPS + 2;
