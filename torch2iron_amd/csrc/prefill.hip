@@ -39,6 +39,12 @@ struct PrefillPrepParams {
 
 // One workgroup (4 waves) per prompt row; wave w takes vectors w, w + 4, ...
 // of the row's Hq + 2 Hkv heads; a lane holds the rotation pair (i0, i1).
+// The vectors go in batches of PREP_BATCH a wave: every load of a batch (and the
+// norm weights) is issued before the first vector is normalised, so a batch
+// costs one memory round trip, not one per vector.  The loads are unconditional
+// (a wave past its last vector reloads it and drops it).
+constexpr int PREP_BATCH = 8;
+
 __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepParams p) {
   constexpr int D = PF_D;
   const int row = blockIdx.x;
@@ -46,35 +52,50 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepPara
   const int t = row - b * p.T;
   const int pos = p.p0 + t;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nvec = p.Hq + 2 * p.Hkv;
   const int i0 = p.style == 0 ? lane : 2 * lane;
   const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
+  const uint16_t* src_row = p.qkv + (size_t)row * nvec * D;
   const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
   const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
-  const uint16_t* src_row = p.qkv + (size_t)row * nvec * D;
-  for (int vi = wave; vi < nvec; vi += 4) {
-    const uint16_t* src = src_row + (size_t)vi * D;
-    float x0 = bf16_to_f32(src[i0]);
-    float x1 = bf16_to_f32(src[i1]);
-    uint16_t* dst;
-    if (vi < p.Hq + p.Hkv) {
-      const uint16_t* gamma = vi < p.Hq ? p.qn : p.kn;
-      const float ss = wave_sum(x0 * x0 + x1 * x1);
-      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-      x0 = round_bf16(round_bf16(x0 * inv) * bf16_to_f32(gamma[i0]));
-      x1 = round_bf16(round_bf16(x1 * inv) * bf16_to_f32(gamma[i1]));
-      const float y0 = round_bf16(round_bf16(x0 * cs) + round_bf16(-x1 * sn));
-      const float y1 = round_bf16(round_bf16(x1 * cs) + round_bf16(x0 * sn));
-      x0 = y0;
-      x1 = y1;
-      if (vi < p.Hq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
-      else dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
-    } else {
-      dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
+  const float gq0 = bf16_to_f32(p.qn[i0]), gq1 = bf16_to_f32(p.qn[i1]);
+  const float gk0 = bf16_to_f32(p.kn[i0]), gk1 = bf16_to_f32(p.kn[i1]);
+  for (int base = wave; base < nvec; base += 4 * PREP_BATCH) {
+    float x0[PREP_BATCH], x1[PREP_BATCH];
+#pragma unroll
+    for (int j = 0; j < PREP_BATCH; ++j) {
+      const uint16_t* src = src_row + (size_t)min(base + 4 * j, nvec - 1) * D;
+      x0[j] = bf16_to_f32(src[i0]);
+      x1[j] = bf16_to_f32(src[i1]);
     }
-    dst[i0] = (uint16_t)f32_to_bf16(x0);
-    dst[i1] = (uint16_t)f32_to_bf16(x1);
+    // all of the batch's loads before its first use (the compiler would sink a
+    // vector's loads behind the previous vector's normalisation)
+#pragma unroll
+    for (int j = 0; j < PREP_BATCH; ++j) asm volatile("" : "+v"(x0[j]), "+v"(x1[j]));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < PREP_BATCH; ++j) {
+      const int vi = base + 4 * j;   // wave-uniform
+      if (vi >= nvec) break;
+      float y0 = x0[j], y1 = x1[j];
+      uint16_t* dst;
+      if (vi < p.Hq + p.Hkv) {
+        const bool isq = vi < p.Hq;
+        const float ss = wave_sum(y0 * y0 + y1 * y1);
+        const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+        const float n0 = round_bf16(round_bf16(y0 * inv) * (isq ? gq0 : gk0));
+        const float n1 = round_bf16(round_bf16(y1 * inv) * (isq ? gq1 : gk1));
+        y0 = round_bf16(round_bf16(n0 * cs) + round_bf16(-n1 * sn));
+        y1 = round_bf16(round_bf16(n1 * cs) + round_bf16(n0 * sn));
+        if (isq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
+        else dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
+      } else {
+        dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
+      }
+      dst[i0] = (uint16_t)f32_to_bf16(y0);
+      dst[i1] = (uint16_t)f32_to_bf16(y1);
+    }
   }
 }
 
