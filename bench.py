@@ -321,8 +321,9 @@ def cpu_baseline(seconds: float):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the W4A16 path would shard by output columns, see DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the W4A16 path runs "
+              "on one GPU (data-parallel decode would replicate the weights and split the batch)",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     from torch2iron_amd import _lib
