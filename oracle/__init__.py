@@ -3,8 +3,8 @@
 This package restates, on the CPU, the arithmetic of torch2iron's W4A16
 reference path so that the HIP kernels can be checked against it.  Only
 ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and only as the checker or as the timed CPU
-baseline.  The product path (``torch2iron_amd``) never imports it and fails
+``bench.py`` may import it, and only as what results are compared against
+or as the timed CPU baseline.  The product path (``torch2iron_amd``) never imports it and fails
 loudly when its HIP library is missing.
 
 Modules
