@@ -23,6 +23,9 @@ CASES = [(1, 1024, 3072)]
 CASES += [(m, k, n) for (k, n) in QWEN3_06B for m in (1, 8, 16, 32, 64)]
 CASES += [(m, k, n) for (k, n) in QWEN3_17B for m in (1, 16, 64)]
 CASES += [(3, 1024, 3072), (17, 2048, 1024), (50, 1024, 4096), (33, 3072, 1024), (5, 128, 64)]
+# row tiles shorter than 16 rows (few column blocks): 4-row tiles with a 1-row last
+# tile, 1-row tiles, 2-row tiles
+CASES += [(13, 2048, 1024), (16, 1024, 256), (6, 3072, 1024)]
 
 
 def _inputs(m, k, n, seed):
@@ -62,7 +65,7 @@ def test_gemv_vector_input(gpu):
     check_linear(y.view(1, -1), ref)
 
 
-@pytest.mark.parametrize("m,k,n", [(16, 2048, 1024), (64, 1024, 4096), (1, 3072, 1024)])
+@pytest.mark.parametrize("m,k,n", [(16, 2048, 1024), (64, 1024, 4096), (1, 3072, 1024), (13, 3072, 1024)])
 def test_linear_residual(gpu, m, k, n):
     qw, qz, sc, x = _inputs(m, k, n, seed=31 + m)
     res = torch.randn(m, n, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
@@ -190,7 +193,7 @@ def test_golden_fixture_on_gpu(gpu):
 
 
 NORM_CASES = [(1, 1024, 4096), (8, 1024, 4096), (16, 1024, 6144), (33, 2048, 4096), (64, 1024, 1024),
-              (5, 4096, 512), (16, 2048, 12288)]
+              (5, 4096, 512), (16, 2048, 12288), (16, 1024, 1024), (7, 1024, 2048)]
 
 
 @pytest.mark.parametrize("m,k,n", NORM_CASES, ids=[f"M{m}-K{k}-N{n}" for m, k, n in NORM_CASES])

@@ -19,9 +19,11 @@
 //     is s * (acc - (128 + z) * xs), accumulated in fp32 (scale after dot).
 //
 // A workgroup of W waves owns one column block of 16*LW columns and one tile
-// of 16 rows (more rows go to grid.z and share the weights through L2); its
-// waves split the K range (double-buffered chunks of CK k-steps) and their
-// fp32 sums meet in LDS in a fixed tree, so results do not depend on timing.
+// of 16 rows (more rows go to grid.z and share the weights through L2; an
+// output with few column blocks takes shorter row tiles, so that it still gets
+// up to 256 workgroups); its waves split the K range
+// (double-buffered chunks of CK k-steps) and their fp32 sums meet in LDS in a
+// fixed order, so results do not depend on timing.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -50,6 +52,7 @@ struct LinearParams {
   int ldx, ldy;
   int chunks;           // K / (32 * CK)
   int epi;
+  int rt;               // rows per row tile: 16, or fewer to give a narrow output more workgroups
 };
 
 __device__ __forceinline__ bf16x8 b_operand(uint32_t w) {
@@ -139,6 +142,14 @@ struct Chunk {
   uint32_t zw;                // qzeros word holding this lane's columns
 };
 
+// Activation row held by A-operand row `local` of the row tile at mbase.  A tile
+// of p.rt rows repeats its last row in the MFMA rows past p.rt, and rows past M
+// repeat row M - 1: the loads stay unconditional, an MFMA output row depends on
+// its own A row only, and the repeats are never stored.
+__device__ __forceinline__ int tile_row(const LinearParams& p, int mbase, int local) {
+  return min(mbase + min(local, p.rt - 1), p.M - 1);
+}
+
 template <int MT, int LW, int CK, bool NORM>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
@@ -148,9 +159,7 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
     load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
 #pragma unroll
   for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) {
-    // rows past M reload row M - 1 (an unconditional load): an MFMA output row
-    // depends on its own A row only, and rows past M are never stored
-    const int m = min(mbase + mi * 16 + c, p.M - 1);
+    const int m = tile_row(p, mbase, mi * 16 + c);
 #pragma unroll
     for (int j = 0; j < CK; ++j)
       b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
@@ -301,7 +310,7 @@ template <int W, int KPW>
 __device__ __forceinline__ void norm_issue(const LinearParams& p, int mbase, int wave, int lane, NormLoads<KPW>& nl) {
   const int ksteps = p.K / 32;
   const int row = lane & 15, r = lane >> 4;
-  const uint16_t* xrow = p.x + (size_t)min(mbase + row, p.M - 1) * p.ldx + r * 8;
+  const uint16_t* xrow = p.x + (size_t)tile_row(p, mbase, row) * p.ldx + r * 8;
 #pragma unroll
   for (int i = 0; i < KPW; ++i) {
     const int ks = min(wave + i * W, ksteps - 1);
@@ -374,8 +383,7 @@ __device__ __forceinline__ void norm_finish(const LinearParams& p, int mbase, in
 // its chunk's A operands: no tile in LDS, no pass over it, one barrier fewer.
 // (Every lane summing its row itself, to drop the second barrier, measured no
 // faster.)
-// Rows past M reload row M - 1: an MFMA output row depends on its own A row only,
-// and rows past M are never stored.
+// Rows outside the tile reload a row of it (tile_row).
 template <int CK>
 struct NormOwn {
   u32x4 v[CK];   // the wave's k-steps of the row tile, A layout
@@ -385,7 +393,7 @@ struct NormOwn {
 template <int CK>
 __device__ __forceinline__ void norm_issue_own(const LinearParams& p, int mbase, int ks0, int lane, NormOwn<CK>& nl) {
   const int row = lane & 15, r = lane >> 4;
-  const uint16_t* xrow = p.x + (size_t)min(mbase + row, p.M - 1) * p.ldx + r * 8;
+  const uint16_t* xrow = p.x + (size_t)tile_row(p, mbase, row) * p.ldx + r * 8;
 #pragma unroll
   for (int j = 0; j < CK; ++j) {
     nl.v[j] = *reinterpret_cast<const u32x4*>(xrow + (ks0 + j) * 32);
@@ -455,12 +463,15 @@ __device__ __forceinline__ int xcd_block(int b, int G) {
 // SGPRs at wave launch: the first loads are issued without waiting for a load of
 // the kernel arguments (measured 4.8 -> 4.4 us per launch over the decode shapes).
 // The other fields come from p_ (the epilogue's, needed once the data is in).
+// M_ carries log2 of the row-tile height in bits 24 and up (M < 2^24).
 template <int MT, int LW, int W, int CK, int NKPW>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, const uint32_t* qw_, const uint16_t* sc_,
                                                              const uint32_t* qz_, const uint16_t* aux_, int N_, int M_,
                                                              int K_, int G_, const LinearParams p_) {
   LinearParams p = p_;
-  p.x = x_; p.qw = qw_; p.sc = sc_; p.qz = qz_; p.N = N_; p.M = M_; p.K = K_; p.ldx = K_; p.chunks = K_ / (32 * CK);
+  p.x = x_; p.qw = qw_; p.sc = sc_; p.qz = qz_; p.N = N_; p.K = K_; p.ldx = K_; p.chunks = K_ / (32 * CK);
+  p.M = M_ & 0xFFFFFF;
+  p.rt = 1 << (M_ >> 24);
   if constexpr (NKPW > 0) p.gamma = aux_; else p.residual = aux_;
   constexpr bool NORM = NKPW > 0;
   // NKPW == CK: K <= 32 W CK, so every wave has at most one chunk (registers path)
@@ -474,7 +485,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   const int r = lane >> 4;
   const int ncol = xcd_block(blockIdx.x, G_) * (16 * LW) + LW * c;
   const int zshift = (ncol & 7) * 4;
-  const int mbase = blockIdx.z * (16 * MT);   // row tile of this workgroup
+  const int mbase = blockIdx.z * p.rt;   // row tile of this workgroup
 
   // this wave's chunks: a contiguous slice of K
   const int per_wave = (p.chunks + W - 1) / W;
@@ -508,7 +519,8 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   // nothing fetch a clamped row and drop it, and without a residual the first
   // scales row stands in (in bounds, unused).
   const int st_mi = min(wave >> 2, MT - 1), st_i = wave & 3;
-  const int st_m = mbase + st_mi * 16 + r * 4 + st_i;   // the row this lane stores
+  const int st_local = st_mi * 16 + r * 4 + st_i;
+  const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // the row this lane stores (M: none)
   uint32_t resv[(LW + 1) / 2];
   load_scales<LW>(p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv, ncol & 1);
   __builtin_amdgcn_sched_barrier(0);
@@ -956,7 +968,8 @@ using t2i_host::fail;
 
 struct Plan {
   int MT, LW, W, CK;
-  int mz;       // row tiles of 16*MT rows (grid.z)
+  int rt;       // rows per row tile (16 * MT, or fewer)
+  int mz;       // row tiles (grid.z)
   int cbs;      // column blocks (grid.x)
   int chunks;   // K / (32 * CK)
 };
@@ -969,9 +982,26 @@ bool config_exists(int MT, int LW, int W, int CK) {
 }
 
 void finish_plan(Plan& pl, int M, int K, int N) {
-  pl.mz = (M + 16 * pl.MT - 1) / (16 * pl.MT);
   pl.cbs = N / (16 * pl.LW);
   pl.chunks = K / (32 * pl.CK);
+  // Row tiles shorter than 16 rows when the column blocks alone leave CUs idle:
+  // every workgroup reads all K of its rows, so at 64 column blocks and 16 rows a
+  // workgroup reads 4x more activation than weight bytes; 4 tiles of 4 rows give
+  // 256 workgroups of a quarter of that (the tiles of a column block share its
+  // weights in one L2, see xcd_block).  Measured on the Qwen3-0.6B o_proj / down
+  // (64 column blocks): 4.6 -> 3.8 and 5.9 -> 4.7 us at M = 16, 5.0 -> 4.5 us
+  // (down, M = 8).  More than 256 workgroups (two a CU) measured slower at every
+  // point, and so did narrower column blocks at M = 1 (4 or 8 columns of the 16
+  // MFMA columns: no faster, or 3 % slower).
+  pl.rt = 16 * pl.MT;
+  while (pl.MT == 1 && pl.rt > 1 && pl.cbs * ((M + pl.rt / 2 - 1) / (pl.rt / 2)) <= 256) pl.rt /= 2;
+#ifdef T2I_TUNING
+  if (const char* env = getenv("T2I_RT")) {
+    const int rt = atoi(env);
+    if (pl.MT == 1 && rt >= 1 && rt <= 16 && (rt & (rt - 1)) == 0) pl.rt = rt;
+  }
+#endif
+  pl.mz = (M + pl.rt - 1) / pl.rt;
 }
 
 // Tile choice, from an HBM-cold sweep (graph-launched, 42-300 weight copies)
@@ -1032,8 +1062,10 @@ hipError_t launch_t(const LinearParams& p, dim3 grid, size_t lds, hipStream_t s)
   }
   // the kernel takes x rows of K values (ldx = K) and K / (32 CK) chunks, as every plan here sets them
   if (p.ldx != p.K || p.chunks != p.K / (32 * CK)) return hipErrorInvalidValue;
+  if (p.M >= (1 << 24) || p.rt < 1 || p.rt > 16 * MT || (p.rt & (p.rt - 1))) return hipErrorInvalidValue;
+  const int m_rt = p.M | (__builtin_ctz((unsigned)p.rt) << 24);   // M and log2 of the row-tile height
   hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NKPW>), grid, dim3(64 * W), lds, s, p.x, p.qw, p.sc, p.qz,
-                     NKPW > 0 ? p.gamma : p.residual, p.N, p.M, p.K, (int)grid.x, p);
+                     NKPW > 0 ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
   return hipGetLastError();
 }
 
@@ -1143,6 +1175,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   p.ldy = paired ? N / 2 : N;
   p.chunks = pl.chunks;
   p.epi = epi;
+  p.rt = pl.rt;
   return t2i_host::hip_status(launch_plan(pl, p, gamma != nullptr, reinterpret_cast<hipStream_t>(stream)),
                               "w4a16 linear launch");
 }
