@@ -55,22 +55,34 @@ struct LinearParams {
   int rt;               // rows per row tile: 16, or fewer to give a narrow output more workgroups
 };
 
-__device__ __forceinline__ bf16x8 b_operand(uint32_t w) {
+// MAGIC in a VGPR.  A VALU instruction reads at most one scalar operand (SGPR or
+// literal) on gfx9, so with the nibble mask as that operand the AND-OR takes
+// MAGIC from a VGPR and stays one v_and_or_b32; with both as constants the
+// compiler splits it into an AND and an OR.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+  uint32_t m = MAGIC;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
+// magic: MAGIC, held in a VGPR (magic_vgpr).
+__device__ __forceinline__ bf16x8 b_operand(uint32_t w, uint32_t magic) {
   u32x4 d;
-  d.x = (w & NIB2) | MAGIC;           // (k0, k4)
-  d.y = ((w >> 4) & NIB2) | MAGIC;    // (k1, k5)
-  d.z = ((w >> 8) & NIB2) | MAGIC;    // (k2, k6)
-  d.w = ((w >> 12) & NIB2) | MAGIC;   // (k3, k7)
+  d.x = (w & NIB2) | magic;           // (k0, k4)
+  d.y = ((w >> 4) & NIB2) | magic;    // (k1, k5)
+  d.z = ((w >> 8) & NIB2) | magic;    // (k2, k6)
+  d.w = ((w >> 12) & NIB2) | magic;   // (k3, k7)
   return __builtin_bit_cast(bf16x8, d);
 }
 
-// v holds bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7); reorder to match b_operand.
+// v holds bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7); reorder to match b_operand,
+// one byte permute (v_perm_b32) per output word.
 __device__ __forceinline__ bf16x8 a_operand(u32x4 v) {
   u32x4 d;
-  d.x = (v.x & 0xFFFFu) | (v.z << 16);
-  d.y = (v.x >> 16) | (v.z & 0xFFFF0000u);
-  d.z = (v.y & 0xFFFFu) | (v.w << 16);
-  d.w = (v.y >> 16) | (v.w & 0xFFFF0000u);
+  d.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);   // (lo x, lo z)
+  d.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);   // (hi x, hi z)
+  d.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  d.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
   return __builtin_bit_cast(bf16x8, d);
 }
 
@@ -192,6 +204,7 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
   pin(b.zw);
   const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
   const bf16x8 ones = ones_operand();
+  const uint32_t magic = magic_vgpr();
   f32x4 acc[MT][LW];
   f32x4 xs[MT];
 #pragma unroll
@@ -204,7 +217,7 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
   for (int j = 0; j < CK; ++j) {
     bf16x8 bop[LW];
 #pragma unroll
-    for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t]);
+    for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t], magic);
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) {
       bf16x8 a;
@@ -661,14 +674,20 @@ __device__ __forceinline__ void lds_dma4(const void* src, void* lds) {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
+// LDS reads at addr + OFF, OFF in the instruction's 16-bit offset field (no
+// address arithmetic per read).
+template <int OFF = 0>
 __device__ __forceinline__ u32x4 lds_read16(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   u32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
+template <int OFF = 0>
 __device__ __forceinline__ uint32_t lds_read4(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
   uint32_t v;
-  asm volatile("ds_read_b32 %0, %1" : "=v"(v) : "v"(addr));
+  asm volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
   return v;
 }
 
@@ -719,12 +738,19 @@ struct GemmFrags {
   uint32_t b[4];
 };
 
-__device__ __forceinline__ void gemm_read(uint32_t abase, uint32_t bbase, int ks, int wm, int wn, GemmFrags& f) {
-#pragma unroll
-  for (int mi = 0; mi < GM_MF; ++mi) f.a[mi] = lds_read16(abase + ((GM_MF * wm + mi) * KSG + ks) * 1024);
-  // qweight row 4 ks + r (lane r = lane / 16, folded into bbase), column 64 wn + 16 j + c
-#pragma unroll
-  for (int j = 0; j < 4; ++j) f.b[j] = lds_read4(bbase + 4 * (2 * ks * GM_BPAIR_W + 64 * wn + 16 * j));
+// abase: this lane's slot of the wave's first A fragment; bbase: this lane's word
+// of k-step 0, fragment 0 (qweight row r = lane / 16, column 64 wn + c).  Every
+// other read is a constant offset from these.
+template <int KS, int I = 0>
+__device__ __forceinline__ void gemm_read(uint32_t abase, uint32_t bbase, GemmFrags& f) {
+  if constexpr (I < GM_MF) {
+    f.a[I] = lds_read16<(I * KSG + KS) * 1024>(abase);
+    gemm_read<KS, I + 1>(abase, bbase, f);
+  } else if constexpr (I < GM_MF + 4) {
+    constexpr int j = I - GM_MF;   // qweight row 4 KS + r, column 64 wn + 16 j + c
+    f.b[j] = lds_read4<4 * (2 * KS * GM_BPAIR_W + 16 * j)>(bbase);
+    gemm_read<KS, I + 1>(abase, bbase, f);
+  }
 }
 
 // Waits for the LDS reads in flight except the most recent N (register ties keep
@@ -740,22 +766,50 @@ __device__ __forceinline__ void wait_lds(GemmFrags& f) {
                  "+v"(f.b[3]));
 }
 
+// k-step KS of a k-tile: read k-step KS + 1's fragments into nxt, then compute
+// KS from cur (read one k-step earlier).
+template <int KS>
+__device__ __forceinline__ void gemm_kstep(uint32_t abase, uint32_t bbase, GemmFrags& cur, GemmFrags& nxt,
+                                           uint32_t magic, f32x4 (&P)[GM_MF][4], f32x4 (&xs)[GM_MF]) {
+  if constexpr (KS + 1 < KSG) {
+    gemm_read<KS + 1>(abase, bbase, nxt);
+    wait_lds<6>(cur);
+  } else {
+    wait_lds<0>(cur);
+  }
+  const bf16x8 ones = ones_operand();
+  bf16x8 a[GM_MF], b[4];
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi) a[mi] = a_operand(cur.a[mi]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b[j] = b_operand(cur.b[j], magic);
+#pragma unroll
+  for (int mi = 0; mi < GM_MF; ++mi) {
+    xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], ones, xs[mi], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], b[j], P[mi][j], 0, 0, 0);
+  }
+  if constexpr (KS + 1 < KSG) gemm_kstep<KS + 1>(abase, bbase, nxt, cur, magic, P, xs);
+}
+
 __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn, int lane, int ncol0,
                                              f32x4 (&total)[GM_MF][4]) {
   static_assert(GM_MF == 2, "wait_lds ties two A fragments");
-  const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane;
-  // lane (r, c): qweight row 4 ks + r = pair 2 ks + r / 2, row r % 2 of the pair; column c
+  const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane + GM_MF * wm * KSG * 1024;
+  // lane (r, c): qweight row 4 ks + r = pair 2 ks + r / 2, row r % 2 of the pair; column 64 wn + c
   const int rr = lane >> 4, cc = lane & 15;
-  const uint32_t bbase = lds_addr(&st.b[0]) + 4 * ((rr >> 1) * GM_BPAIR_W + (rr & 1) * GM_BROW + cc);
-  // this lane's columns: ncol0 + 16 j, tile-local 64 wn + c + 16 j
+  const uint32_t bbase = lds_addr(&st.b[0]) + 4 * ((rr >> 1) * GM_BPAIR_W + (rr & 1) * GM_BROW + 64 * wn + cc);
+  // this lane's columns: ncol0 + 16 j, tile-local lc + 16 j; their scales are words
+  // (lc >> 1) + 8 j, their zero words (lc >> 3) + 2 j
   const int lc = ncol0 & (GM_BN - 1);
+  const uint32_t sbase = lds_addr(&st.qs[0]) + 4 * (lc >> 1);
+  const uint32_t zbase = lds_addr(&st.qz[0]) + 4 * (lc >> 3);
   uint32_t sw[4], zw[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    sw[j] = lds_read4(lds_addr(&st.qs[0]) + 4 * ((lc + 16 * j) >> 1));
-    zw[j] = lds_read4(lds_addr(&st.qz[0]) + 4 * ((lc + 16 * j) >> 3));
-  }
-  const bf16x8 ones = ones_operand();
+  sw[0] = lds_read4<0>(sbase);  zw[0] = lds_read4<0>(zbase);
+  sw[1] = lds_read4<32>(sbase); zw[1] = lds_read4<8>(zbase);
+  sw[2] = lds_read4<64>(sbase); zw[2] = lds_read4<16>(zbase);
+  sw[3] = lds_read4<96>(sbase); zw[3] = lds_read4<24>(zbase);
+  const uint32_t magic = magic_vgpr();
   f32x4 P[GM_MF][4], xs[GM_MF];
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi) {
@@ -764,29 +818,8 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn
     for (int j = 0; j < 4; ++j) P[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   GemmFrags f0, f1;
-  gemm_read(abase, bbase, 0, wm, wn, f0);
-#pragma unroll
-  for (int ks = 0; ks < KSG; ++ks) {
-    GemmFrags& cur = (ks & 1) ? f1 : f0;
-    GemmFrags& nxt = (ks & 1) ? f0 : f1;
-    if (ks + 1 < KSG) {
-      gemm_read(abase, bbase, ks + 1, wm, wn, nxt);
-      wait_lds<6>(cur);
-    } else {
-      wait_lds<0>(cur);
-    }
-    bf16x8 a[GM_MF], b[4];
-#pragma unroll
-    for (int mi = 0; mi < GM_MF; ++mi) a[mi] = a_operand(cur.a[mi]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = b_operand(cur.b[j]);
-#pragma unroll
-    for (int mi = 0; mi < GM_MF; ++mi) {
-      xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], ones, xs[mi], 0, 0, 0);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], b[j], P[mi][j], 0, 0, 0);
-    }
-  }
+  gemm_read<0>(abase, bbase, f0);
+  gemm_kstep<0>(abase, bbase, f0, f1, magic, P, xs);
   // the scale and zero reads were issued first: done with the last wait
   const int zshift = (ncol0 & 7) * 4;   // the same for every fragment (16 j keeps the low bits)
   const bool odd = ncol0 & 1;
