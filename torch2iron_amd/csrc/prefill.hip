@@ -118,7 +118,7 @@ struct PrefillAttnParams {
   float scale_log2;       // D^-1/2 * log2(e)
 };
 
-// One workgroup per (query block, kv head h, sequence b); 4 waves of PF_MF
+// One workgroup per (sequence b, kv head h, query block); 4 waves of PF_MF
 // 16-row MFMA fragments.  Row j of the PF_ROWS is q head h * Q + j / BQ at
 // prompt row t0 + j % BQ (BQ = PF_ROWS / Q), so the q heads sharing kv head h
 // share every K / V block.  Measured slower at 16 sequences x 512 rows: two
@@ -132,9 +132,12 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
   constexpr int D = PF_D;
   constexpr int MF = PF_MF;
   constexpr int BQ = PF_ROWS / Q;           // prompt rows per q head in the tile
-  const int t0 = blockIdx.x * BQ;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
+  // Query blocks are dealt last block first (grid.y counts down): the causal
+  // work of a block grows with its position, so the longest go out first and
+  // the short ones fill the tail.
+  const int t0 = (gridDim.y - 1 - blockIdx.y) * BQ;
+  const int h = blockIdx.x % p.Hkv;
+  const int b = blockIdx.x / p.Hkv;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -357,7 +360,8 @@ extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, in
   const int Q = Hq / Hkv;
   if (Q != 1 && Q != 2 && Q != 4 && Q != 8) return fail(T2I_ERR_SHAPE, "Hq/Hkv=%d must be 1, 2, 4 or 8", Q);
   if (p0 < 0 || ctx_cap < 1 || p0 + T > ctx_cap) return fail(T2I_ERR_SHAPE, "positions %d..%d exceed the cache (%d)", p0, p0 + T - 1, ctx_cap);
-  if (B > 65535 || Hkv > 65535) return fail(T2I_ERR_SHAPE, "B=%d or Hkv=%d exceeds the grid", B, Hkv);
+  if ((long long)B * Hkv > 0x7FFFFFFF || (T + t2i::PF_ROWS / (Hq / Hkv) - 1) / (t2i::PF_ROWS / (Hq / Hkv)) > 65535)
+    return fail(T2I_ERR_SHAPE, "B=%d Hkv=%d T=%d exceed the grid", B, Hkv, T);
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
     return fail(T2I_ERR_ALIGN, "prefill attention tensors must be 16-byte aligned");
   t2i::PrefillAttnParams p{};
@@ -365,7 +369,7 @@ extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, in
   p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.cap = ctx_cap; p.p0 = p0;
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)D));
   const int bq = t2i::PF_ROWS / Q;
-  const dim3 grid((T + bq - 1) / bq, Hkv, B);
+  const dim3 grid(B * Hkv, (T + bq - 1) / bq);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (Q) {
     case 1: hipLaunchKernelGGL((t2i::prefill_attention_kernel<1>), grid, dim3(256), 0, s, p); break;
