@@ -128,7 +128,7 @@ struct PrefillAttnParams {
 //   online softmax per row in fp32 (rows 4r + i of the lane's MFMA output);
 //   O += P V: P goes to A layout through a per-wave LDS tile, B = V^T from LDS.
 template <int Q>
-__global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAttnParams p) {
+__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const PrefillAttnParams p) {
   constexpr int D = PF_D;
   constexpr int MF = PF_MF;
   constexpr int BQ = PF_ROWS / Q;           // prompt rows per q head in the tile
@@ -191,8 +191,10 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
   // lane).  V chunk q: key q % 64, dims 8 (q / 64): the transposed store then
   // writes 64 consecutive keys of one dim per instruction (conflict-free), where
   // the K mapping would put the 16 lanes of a key row 8 rows of s_vt apart, all in
-  // one bank.  Loads are unconditional (keys past kend reload key kend - 1 and are
-  // zeroed after the load).
+  // one bank.  Loads are unconditional (keys past kend reload key kend - 1), and
+  // those keys are zeroed when the block is staged, not right after the load: a
+  // select there would make the compiler wait for the load at once, leaving
+  // nothing in flight behind the compute.
   auto load_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -201,17 +203,20 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
       const int vkey = kb * PF_KEYS + (q16 & 63);
       kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)min(kkey, kend - 1) * D + 8 * (q16 & 15));
       vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)min(vkey, kend - 1) * D + 8 * (q16 >> 6));
-      kr[u] = kkey < kend ? kr[u] : u32x4{0u, 0u, 0u, 0u};
-      vr[u] = vkey < kend ? vr[u] : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  auto store_block = [&](const u32x4 (&kr)[4], const u32x4 (&vr)[4]) {
+  auto store_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      asm volatile("" : "+v"(kr[u]), "+v"(vr[u]));   // the loads are waited for here, not earlier
       const int q16 = tid + 256 * u;
-      *reinterpret_cast<u32x4*>(s_k + (q16 >> 4) * PF_KLD + 8 * (q16 & 15)) = kr[u];
+      const int kkey = kb * PF_KEYS + (q16 >> 4);
       const int key = q16 & 63, d0 = 8 * (q16 >> 6);
-      const uint32_t w[4] = {vr[u].x, vr[u].y, vr[u].z, vr[u].w};
+      const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
+      const u32x4 kv = kkey < kend ? kr[u] : zero4;
+      const u32x4 vv = kb * PF_KEYS + key < kend ? vr[u] : zero4;
+      *reinterpret_cast<u32x4*>(s_k + (q16 >> 4) * PF_KLD + 8 * (q16 & 15)) = kv;
+      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         s_vt[(d0 + 2 * e) * PF_VLD + key] = (uint16_t)(w[e] & 0xFFFFu);
@@ -222,14 +227,17 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
 
   const int nblocks = (kend + PF_KEYS - 1) / PF_KEYS;
   uint16_t* pt = s_p[wave];
-  u32x4 kr[4], vr[4];
-  load_block(0, kr, vr);
-  for (int kb = 0; kb < nblocks; ++kb) {
+  // Block kb: stage its K / V (loaded two blocks earlier) in LDS, refill the
+  // register set with block kb + 2, then compute.  Two sets in flight hide the
+  // load latency behind two blocks of compute.  Every load is issued, also past
+  // the last block (clamped: all lanes read key kend - 1), so that the compiler
+  // knows that the other set's loads are in flight behind this set's and waits
+  // for this set only; with the loads under a condition it waits for all.
+  auto step = [&](const int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
     __syncthreads();                          // the previous block's tiles are consumed
-    store_block(kr, vr);
+    store_block(kb, kr, vr);
     __syncthreads();
-    if (kb + 1 < nblocks) load_block(kb + 1, kr, vr);   // next block in flight during this one
-
+    load_block(kb + 2, kr, vr);
     // ---- S = Q K^T for 4 key tiles of 16; each K fragment feeds every row fragment ----
     f32x4 s[MF][4];
 #pragma unroll
@@ -306,7 +314,16 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(const PrefillAtt
                                                              __builtin_bit_cast(bf16x8, vb), o[mi][n], 0, 0, 0);
       }
     }
+  };
+  u32x4 kr0[4], vr0[4], kr1[4], vr1[4];
+  load_block(0, kr0, vr0);
+  load_block(1, kr1, vr1);
+  int kb = 0;
+  for (; kb + 1 < nblocks; kb += 2) {
+    step(kb, kr0, vr0);
+    step(kb + 1, kr1, vr1);
   }
+  if (kb < nblocks) step(kb, kr0, vr0);
 
   // ---- normalise and store: lane holds rows 4r + i, dims n * 16 + c ----
 #pragma unroll
