@@ -343,6 +343,27 @@ def main():
     value = cold.bytes_per_step / (ms_per_step * 1e-3) / 1e12
     avg_launch_us = ms_per_step * 1e3 / cold.launches_per_step
     log(f"HBM-cold sweep: {value:.3f} TB/s, {ms_per_step:.3f} ms/step, avg launch {avg_launch_us:.2f} us")
+    floor_us = None
+    if not args.eager:
+        # the same number of back-to-back graph launches of a one-element fill: what a
+        # dependent launch costs on this stream before any kernel does work
+        tiny = torch.zeros(1, device=dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(cold.launches_per_step):
+                tiny.fill_(0.0)
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        floor_us = e0.elapsed_time(e1) * 1e3 / (args.steps * cold.launches_per_step)
+        log(f"launch floor (one-element fill, graph): {floor_us:.2f} us per launch")
+        del g, tiny
     breakdown = {}
     for gr, t in zip(cold.groups, per_group):
         breakdown[gr["label"]] = {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
@@ -420,6 +441,7 @@ def main():
             "traffic_source": (traffic or {}).get("source"),
             "kernel": "w4a16_mfma_kernel",
             "avg_launch_us": round(avg_launch_us, 3),
+            "launch_floor_us": None if floor_us is None else round(floor_us, 3),
         },
         "cpu_baseline": cpu,
         "breakdown": breakdown,
