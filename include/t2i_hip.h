@@ -88,10 +88,11 @@ int t2i_w4a16_gate_up(const uint16_t* x, int32_t M,
                       int32_t swiglu, uint16_t* y0, uint16_t* y1, void* stream);
 
 /* ---------------------------------------------------------------------------
- * RMSNorm prologue fused into the linear: each workgroup normalises the rows it
- * multiplies, y = W4A16(xn), xn = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * norm_weight)
- * (rounded as t2i_rmsnorm).  K <= 4096; other limits as t2i_w4a16_linear /
- * t2i_w4a16_gate_up.  x is the un-normalised residual stream [M, K].
+ * RMSNorm fused into the linear: y = inv * W4A16(bf16(x * norm_weight)) per row,
+ * inv = bf16(rsqrt(mean(x^2)+eps)) as t2i_rmsnorm rounds it.  This equals
+ * W4A16(RMSNorm(x)) up to where the products are rounded to bf16 (the norm scale
+ * multiplies the fp32 sums instead of each activation).  Limits as
+ * t2i_w4a16_linear / t2i_w4a16_gate_up.  x is the un-normalised residual stream [M, K].
  * Replaces: fast_qwen3/operators/q4nx_fused_qkv_projection/op.py:30-136
  *           (Q4NXFusedQKVProjection: hidden, norm_weight, W, out) and
  *           fast_qwen3/operators/q4nx_fused_up_gate_projection/op.py:30-126

@@ -63,7 +63,7 @@ def test_fused_norm_entry_points_validate():
     f = lib.t2i_w4a16_rmsnorm_linear
     assert f(FAKE, 16, None, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_NULL
     assert f(FAKE, 16, FAKE, 0.0, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_VALUE
-    assert f(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 8192, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert f(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1000, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert f(FAKE, 0, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert f(FAKE + 2, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 4096, 128, FAKE, None) == _lib.T2I_ERR_ALIGN
     g = lib.t2i_w4a16_rmsnorm_gate_up

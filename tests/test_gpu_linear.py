@@ -196,11 +196,26 @@ NORM_CASES = [(1, 1024, 4096), (8, 1024, 4096), (16, 1024, 6144), (33, 2048, 409
               (5, 4096, 512), (16, 2048, 12288), (16, 1024, 1024), (7, 1024, 2048)]
 
 
+def check_rounding_of_activations(fused: torch.Tensor, unfused: torch.Tensor, xn: np.ndarray, w_nk: np.ndarray):
+    """The fused kernel multiplies bf16(x * gamma) and scales each row's sums by its
+    bf16 1 / rms; the unfused pair multiplies bf16(bf16(x * inv) * gamma).  Both
+    activations are within 1.5 bf16 half-units of the same real number x * inv *
+    gamma, so the outputs may differ by at most 2^-7 sum_k |xn_k| |W_nk|, plus each
+    output's own bf16 rounding (2^-9 relative each).  A bound from the arithmetic,
+    with no tolerance fitted to the kernel."""
+    f = fused.float().cpu().numpy().astype(np.float64)
+    u = unfused.float().cpu().numpy().astype(np.float64)
+    budget = 2.0 ** -7 * (np.abs(xn.astype(np.float64)) @ np.abs(w_nk.astype(np.float64)).T)
+    bound = budget * 1.01 + 2.0 ** -9 * (np.abs(f) + np.abs(u)) * 1.01 + 1e-6
+    err = np.abs(f - u)
+    assert (err <= bound).all(), f"{(err > bound).sum()} outputs beyond the rounding budget; worst {err.max():.4e}"
+
+
 @pytest.mark.parametrize("m,k,n", NORM_CASES, ids=[f"M{m}-K{k}-N{n}" for m, k, n in NORM_CASES])
-def test_rmsnorm_linear_fused_equals_unfused(gpu, m, k, n):
-    """The RMSNorm done inside the linear kernel rounds exactly as t2i_rmsnorm, so the
-    fused call is bit-identical to rmsnorm-then-linear, and within the linear bar of
-    the oracle (bf16 RMSNorm chain, fp64 product)."""
+def test_rmsnorm_linear_fused(gpu, m, k, n):
+    """RMSNorm inside the linear kernel: within the linear bar of the oracle (bf16
+    RMSNorm chain, fp64 product), and within the activation-rounding budget of the
+    unfused rmsnorm-then-linear pair; two calls give the same bits."""
     from oracle import qwen3 as oq
     qw, qz, sc, x = _inputs(m, k, n, seed=77 + m + k)
     x = (x.float() * 3.0).to(torch.bfloat16)           # residual-stream-like magnitude
@@ -208,21 +223,33 @@ def test_rmsnorm_linear_fused_equals_unfused(gpu, m, k, n):
     w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
     xd, gd = x.to(gpu), gam.to(gpu)
     fused = ops.rmsnorm_linear(xd, gd, 1e-6, w)
+    assert torch.equal(fused, ops.rmsnorm_linear(xd, gd, 1e-6, w)), "repeat call differs"
     unfused = ops.linear(ops.rmsnorm(xd, gd, 1e-6), w)
-    assert torch.equal(fused, unfused)
-    xn = oq.rmsnorm(x.float(), gam.float(), 1e-6, oq._Round("bf16"))
-    check_linear(fused, ow.linear(xn.numpy(), qw, qz, sc, accumulate="fp64"))
+    xn = oq.rmsnorm(x.float(), gam.float(), 1e-6, oq._Round("bf16")).numpy()
+    ref = ow.linear(xn, qw, qz, sc, accumulate="fp64")
+    assert np.abs(fused.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= 1e-2
+    check_rounding_of_activations(fused, unfused, xn, ow.dequantize(qw, qz, sc))
 
 
 @pytest.mark.parametrize("m,k,inter", [(1, 1024, 3072), (16, 1024, 3072), (40, 2048, 6144)])
-def test_rmsnorm_gate_up_fused_equals_unfused(gpu, m, k, inter):
+def test_rmsnorm_gate_up_fused(gpu, m, k, inter):
+    """Paired outputs within the activation-rounding budget of the unfused pair; the
+    SwiGLU output is the bf16 chain of the fused kernel's own gate and up values."""
+    from oracle import qwen3 as oq
     gate = ow.synthetic_tensors(k, inter, seed=21)
     up = ow.synthetic_tensors(k, inter, seed=22)
-    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(23)) * 3.0).to(torch.bfloat16).to(gpu)
-    gam = (torch.rand(k, generator=torch.Generator().manual_seed(24)) * 0.2 + 0.9).to(torch.bfloat16).to(gpu)
+    xc = (torch.randn(m, k, generator=torch.Generator().manual_seed(23)) * 3.0).to(torch.bfloat16)
+    gamc = (torch.rand(k, generator=torch.Generator().manual_seed(24)) * 0.2 + 0.9).to(torch.bfloat16)
+    x, gam = xc.to(gpu), gamc.to(gpu)
     w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
-    xn = ops.rmsnorm(x, gam, 1e-6)
-    assert torch.equal(ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=True), ops.gate_up(xn, w, swiglu=True))
+    xn_gpu = ops.rmsnorm(x, gam, 1e-6)
+    xn = oq.rmsnorm(xc.float(), gamc.float(), 1e-6, oq._Round("bf16")).numpy()
     g1, u1 = ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=False)
-    g2, u2 = ops.gate_up(xn, w, swiglu=False)
-    assert torch.equal(g1, g2) and torch.equal(u1, u2)
+    g2, u2 = ops.gate_up(xn_gpu, w, swiglu=False)
+    check_rounding_of_activations(g1, g2, xn, ow.dequantize(*gate))
+    check_rounding_of_activations(u1, u2, xn, ow.dequantize(*up))
+    h = ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=True).float().cpu()
+    gb, ub = g1.float().cpu(), u1.float().cpu()
+    h_chain = (torch.nn.functional.silu(gb).to(torch.bfloat16).float() * ub).to(torch.bfloat16).float()
+    assert (h - h_chain).abs().max() <= 2.0 ** -7 * h_chain.abs().max()
+    assert (h == h_chain).float().mean() > 0.999

@@ -65,7 +65,7 @@ def test_operators_match_functional_layer(gpu):
     nw = torch.ones(1024, dtype=BF16, device=gpu)
     h = torch.empty(16, 3072, dtype=BF16, device=gpu)
     O.Qwen3FusedUpGateProjection(1024, 3072, rows=16)(a, nw, wp, h)
-    assert torch.equal(h, ops.gate_up(ops.rmsnorm(a, nw, 1e-6), wp, swiglu=True))
+    assert torch.equal(h, ops.rmsnorm_gate_up(a, nw, 1e-6, wp, swiglu=True))
     wo = formats.W4A16Weight.from_numpy(*ow.synthetic_tensors(3072, 1024, seed=5), device=gpu)
     res = torch.randn(16, 1024, generator=g).to(BF16).to(gpu)
     out = torch.empty_like(res)

@@ -150,6 +150,7 @@ template <int MT, int LW, int CK>
 struct Chunk {
   uint32_t w[CK][LW];
   u32x4 x[MT][CK];
+  u32x4 g[CK];                // fused-norm variant: norm weight of k 8 r .. 8 r + 7 of each k-step
   uint32_t s[(LW + 1) / 2];   // fp16 scales of this lane's LW columns
   uint32_t zw;                // qzeros word holding this lane's columns
 };
@@ -170,34 +171,40 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
   for (int j = 0; j < CK; ++j)
     load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
 #pragma unroll
-  for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) {
+  for (int mi = 0; mi < MT; ++mi) {
     const int m = tile_row(p, mbase, mi * 16 + c);
 #pragma unroll
     for (int j = 0; j < CK; ++j)
       b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < CK; ++j) b.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
   }
   const int g = ks0 / KSG;
   load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
   b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
 }
 
-// a_lds (fused-norm variant): the normalised activations of the row tile in
-// A-operand order, 64 lanes x 16 bytes per k-step; k-step ks0 is this chunk's first.
 // Pins a loaded value at this point: code that uses it cannot be moved above the
 // pin (say, to a point shared by the chunk schedules, where it would wait for the
 // chunk's loads before the other chunks' loads are issued).
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
 
+// NORM (fused-norm variant, MT = 1): the A operand is bf16(x * gamma), and the
+// lane's share of its row's sum of squares accumulates in ss; the row's 1 / rms
+// multiplies the finished sums (see the kernel).
 template <int MT, int LW, int CK, bool NORM>
-__device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4],
-                                              const u32x4* a_lds, int ks0, int lane, int zshift) {
+__device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4], float& ss,
+                                              int zshift) {
 #pragma unroll
   for (int j = 0; j < CK; ++j) {
 #pragma unroll
     for (int t = 0; t < LW; ++t) pin(b.w[j][t]);
 #pragma unroll
-    for (int mi = 0; mi < (NORM ? 0 : MT); ++mi) pin(b.x[mi][j]);
+    for (int mi = 0; mi < MT; ++mi) pin(b.x[mi][j]);
+    if constexpr (NORM) pin(b.g[j]);
   }
 #pragma unroll
   for (int i = 0; i < (LW + 1) / 2; ++i) pin(b.s[i]);
@@ -220,9 +227,21 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
     for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t], magic);
 #pragma unroll
     for (int mi = 0; mi < MT; ++mi) {
-      bf16x8 a;
-      if constexpr (NORM) a = __builtin_bit_cast(bf16x8, a_lds[(ks0 + j) * 64 + lane]);
-      else a = a_operand(b.x[mi][j]);
+      u32x4 xv = b.x[mi][j];
+      if constexpr (NORM) {
+        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t ga[4] = {b.g[j].x, b.g[j].y, b.g[j].z, b.g[j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16_lo(xa[e]), hi = bf16_hi(xa[e]);
+          ss = fmaf(lo, lo, ss);
+          ss = fmaf(hi, hi, ss);
+          o[e] = pack_bf16x2(lo * bf16_lo(ga[e]), hi * bf16_hi(ga[e]));
+        }
+        xv = u32x4{o[0], o[1], o[2], o[3]};
+      }
+      const bf16x8 a = a_operand(xv);
       xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
 #pragma unroll
       for (int t = 0; t < LW; ++t)
@@ -296,168 +315,6 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
   }
 }
 
-// Fused RMSNorm prologue, in two parts: norm_issue loads the row tile and the
-// norm weight before the first weight chunk is loaded (loads retire in issue
-// order, so norm_finish then waits for its own data only, while the weights
-// stay in flight), and norm_finish normalises.  Wave w takes k-steps w, w + W,
-// ... (KPW of them, a compile-time bound on K / 32 / W); for k-step ks lane
-// l = 16 r + row loads x[row][32 ks + 8 r .. + 7]; each thread loads 8 norm
-// weights.  All loads are unconditional (clamped indices, values discarded
-// after the load): a load under a lane-divergent condition makes the compiler
-// wait for every load in flight where the branches join.  The tile is parked
-// in LDS at A-operand slot 64 ks + l, so every LDS access of a wave is one
-// contiguous 1 KB (no bank conflicts).  The per-row sums of squares meet
-// through lane shuffles and a small table (fixed order), then each lane
-// normalises the slots it parked, rounding as the standalone RMSNorm:
-// bf16(bf16(x * inv) * w), inv = bf16(1 / sqrt(mean(x^2) + eps)).  Rows beyond
-// M are zero.
-constexpr int NORM_MAX_K = 4096;
-
-template <int KPW>
-struct NormLoads {
-  u32x4 v[KPW];   // row-tile k-steps wave, wave + W, ...
-  u32x4 g;        // norm weight 8 t .. 8 t + 7 of thread t
-};
-
-template <int W, int KPW>
-__device__ __forceinline__ void norm_issue(const LinearParams& p, int mbase, int wave, int lane, NormLoads<KPW>& nl) {
-  const int ksteps = p.K / 32;
-  const int row = lane & 15, r = lane >> 4;
-  const uint16_t* xrow = p.x + (size_t)tile_row(p, mbase, row) * p.ldx + r * 8;
-#pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    const int ks = min(wave + i * W, ksteps - 1);
-    nl.v[i] = *reinterpret_cast<const u32x4*>(xrow + ks * 32);
-  }
-  nl.g = *reinterpret_cast<const u32x4*>(p.gamma + 8 * min((int)threadIdx.x, p.K / 8 - 1));
-}
-
-template <int W, int KPW>
-__device__ __forceinline__ void norm_finish(const LinearParams& p, int mbase, int wave, int lane,
-                                            const NormLoads<KPW>& nl, u32x4* a_lds) {
-  __shared__ float s_ss[W][16];
-  __shared__ float s_inv[16];
-  const int ksteps = p.K / 32;
-  const int row = lane & 15, r = lane >> 4;
-  const bool row_ok = mbase + row < p.M;
-  u32x4* g_lds = a_lds + ksteps * 64;            // norm weight, 16 bytes per (k-step, sub-block)
-  // threads past K / 8 loaded the last 8 weights and store them again (same value):
-  // an unconditional store keeps the compiler from moving the load behind the weights
-  g_lds[min((int)threadIdx.x, p.K / 8 - 1)] = nl.g;
-  const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    const int ks = wave + i * W;
-    if (ks >= ksteps) continue;
-    const u32x4 v = row_ok ? nl.v[i] : zero4;
-    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
-      ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
-    }
-    a_lds[ks * 64 + lane] = v;
-  }
-  ss += __shfl_xor(ss, 16, 64);                  // the four sub-blocks of a row
-  ss += __shfl_xor(ss, 32, 64);
-  if (lane < 16) s_ss[wave][lane] = ss;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    float t = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) t += s_ss[w][threadIdx.x];
-    s_inv[threadIdx.x] = round_bf16(1.0f / sqrtf(t / (float)p.K + p.eps));
-  }
-  __syncthreads();
-  const float inv = s_inv[row];
-  for (int ks = wave; ks < ksteps; ks += W) {
-    const u32x4 v = a_lds[ks * 64 + lane];
-    const u32x4 g = g_lds[ks * 4 + r];
-    const uint32_t a[4] = {v.x, v.y, v.z, v.w};
-    const uint32_t w[4] = {g.x, g.y, g.z, g.w};
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = round_bf16(round_bf16(bf16_lo(a[e]) * inv) * bf16_lo(w[e]));
-      const float hi = round_bf16(round_bf16(bf16_hi(a[e]) * inv) * bf16_hi(w[e]));
-      o[e] = pack_bf16x2(lo, hi);
-    }
-    a_lds[ks * 64 + lane] = __builtin_bit_cast(u32x4, a_operand(u32x4{o[0], o[1], o[2], o[3]}));
-  }
-}
-
-// Fused RMSNorm when every wave has one chunk (K <= 32 W CK): each wave loads
-// the row tile's values for its own chunk's k-steps straight in A-operand layout
-// (lane 16 r + row: row, k 8 r .. 8 r + 7 of the k-step) with the norm weight of
-// those k, the per-row sums of squares meet through lane shuffles and a small
-// table (fixed order), and the wave normalises its registers, rounding as the
-// standalone RMSNorm (bf16(bf16(x * inv) * w), two values per conversion), into
-// its chunk's A operands: no tile in LDS, no pass over it, one barrier fewer.
-// (Every lane summing its row itself, to drop the second barrier, measured no
-// faster.)
-// Rows outside the tile reload a row of it (tile_row).
-template <int CK>
-struct NormOwn {
-  u32x4 v[CK];   // the wave's k-steps of the row tile, A layout
-  u32x4 g[CK];   // norm weight 8 r .. 8 r + 7 of each
-};
-
-template <int CK>
-__device__ __forceinline__ void norm_issue_own(const LinearParams& p, int mbase, int ks0, int lane, NormOwn<CK>& nl) {
-  const int row = lane & 15, r = lane >> 4;
-  const uint16_t* xrow = p.x + (size_t)tile_row(p, mbase, row) * p.ldx + r * 8;
-#pragma unroll
-  for (int j = 0; j < CK; ++j) {
-    nl.v[j] = *reinterpret_cast<const u32x4*>(xrow + (ks0 + j) * 32);
-    nl.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
-  }
-}
-
-template <int W, int CK, int LW>
-__device__ __forceinline__ void norm_own(const LinearParams& p, int wave, int lane, bool has_chunk,
-                                         NormOwn<CK>& nl, Chunk<1, LW, CK>& A) {
-  __shared__ float s_ss[W][16];
-  __shared__ float s_inv[16];
-  float ss = 0.0f;
-#pragma unroll
-  for (int j = 0; j < CK; ++j) {
-    pin(nl.v[j]);
-    const uint32_t a[4] = {nl.v[j].x, nl.v[j].y, nl.v[j].z, nl.v[j].w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ss = fmaf(bf16_lo(a[e]), bf16_lo(a[e]), ss);
-      ss = fmaf(bf16_hi(a[e]), bf16_hi(a[e]), ss);
-    }
-  }
-  ss = has_chunk ? ss : 0.0f;   // a wave past the last chunk loaded the last k-steps again
-  ss += __shfl_xor(ss, 16, 64);   // the four sub-blocks of a row
-  ss += __shfl_xor(ss, 32, 64);
-  if (lane < 16) s_ss[wave][lane] = ss;
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    float t = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) t += s_ss[w][threadIdx.x];
-    s_inv[threadIdx.x] = round_bf16(1.0f / sqrtf(t / (float)p.K + p.eps));
-  }
-  __syncthreads();
-  const float inv = s_inv[lane & 15];
-#pragma unroll
-  for (int j = 0; j < CK; ++j) {
-    pin(nl.g[j]);
-    const uint32_t a[4] = {nl.v[j].x, nl.v[j].y, nl.v[j].z, nl.v[j].w};
-    const uint32_t g[4] = {nl.g[j].x, nl.g[j].y, nl.g[j].z, nl.g[j].w};
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t n1 = pack_bf16x2(bf16_lo(a[e]) * inv, bf16_hi(a[e]) * inv);
-      o[e] = pack_bf16x2(bf16_lo(n1) * bf16_lo(g[e]), bf16_hi(n1) * bf16_hi(g[e]));
-    }
-    A.x[0][j] = u32x4{o[0], o[1], o[2], o[3]};   // memory k order; compute_chunk permutes it
-  }
-}
-
 // Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
 // its own L2.  Neighbouring column blocks share 128-byte lines of qweight,
 // scales and qzeros, so the blocks are renumbered to give each XCD one
@@ -468,8 +325,14 @@ __device__ __forceinline__ int xcd_block(int b, int G) {
   return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
 }
 
-// NKPW = 0: plain linear; NKPW > 0: the fused-RMSNorm variant, whose prologue
-// takes up to NKPW k-steps per wave (NKPW * W * 32 >= K).
+// NORM: the fused-RMSNorm variant.  RMSNorm(x) W = (1 / rms) (x * gamma) W for
+// each row, so the waves multiply bf16(x * gamma) by the weights as soon as
+// their own loads land, summing each row's squares alongside, and the row's
+// 1 / rms, bf16(1 / sqrt(mean(x^2) + eps)) as the standalone RMSNorm rounds it,
+// multiplies the finished sums.  Normalising before the product needs every
+// row's full sum of squares first, that is two workgroup barriers ahead of the
+// MFMAs (measured 0.92 against 0.86 ms per decode step); the only change is
+// where the products are rounded to bf16.
 // Everything the first loads' addresses need comes as leading scalar arguments
 // (x, qweight, scales, qzeros, the residual or norm weight, N, M, K and the
 // column-block count G = gridDim.x), which the library is built to preload into
@@ -477,7 +340,7 @@ __device__ __forceinline__ int xcd_block(int b, int G) {
 // the kernel arguments (measured 4.8 -> 4.4 us per launch over the decode shapes).
 // The other fields come from p_ (the epilogue's, needed once the data is in).
 // M_ carries log2 of the row-tile height in bits 24 and up (M < 2^24).
-template <int MT, int LW, int W, int CK, int NKPW>
+template <int MT, int LW, int W, int CK, bool NORM>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, const uint32_t* qw_, const uint16_t* sc_,
                                                              const uint32_t* qz_, const uint16_t* aux_, int N_, int M_,
                                                              int K_, int G_, const LinearParams p_) {
@@ -485,11 +348,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   p.x = x_; p.qw = qw_; p.sc = sc_; p.qz = qz_; p.N = N_; p.K = K_; p.ldx = K_; p.chunks = K_ / (32 * CK);
   p.M = M_ & 0xFFFFFF;
   p.rt = 1 << (M_ >> 24);
-  if constexpr (NKPW > 0) p.gamma = aux_; else p.residual = aux_;
-  constexpr bool NORM = NKPW > 0;
-  // NKPW == CK: K <= 32 W CK, so every wave has at most one chunk (registers path)
-  constexpr bool NREG = NORM && NKPW == CK;
-  constexpr bool NLDS = NORM && !NREG;   // the row tile goes through LDS
+  if constexpr (NORM) p.gamma = aux_; else p.residual = aux_;
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
   constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
@@ -505,10 +364,6 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   const int c_begin = wave * per_wave;
   const int c_end = min(c_begin + per_wave, p.chunks);
 
-  // fused-norm variant: the normalised row tile (K / 32 KB), later reused for the wave reduction
-  extern __shared__ __align__(16) char dyn_lds[];
-  u32x4* a_lds = reinterpret_cast<u32x4*>(dyn_lds);
-
   float total[MT][LW][4];
 #pragma unroll
   for (int mi = 0; mi < MT; ++mi)
@@ -516,15 +371,9 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
     for (int t = 0; t < LW; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
+  float ss = 0.0f;   // fused norm: this lane's share of its A row's sum of squares
 
-  // Load order: the norm prologue's row tile, then the first weight chunk (every
-  // wave loads one: a wave without chunks reloads the last and computes nothing),
-  // so that normalising waits for the tile only while the weights are in flight.
-  NormLoads<NLDS ? NKPW : 1> nl;
-  NormOwn<NREG ? CK : 1> no;
-  if constexpr (NLDS) norm_issue<W, NKPW>(p, mbase, wave, lane, nl);
-  if constexpr (NREG) norm_issue_own<CK>(p, mbase, min(c_begin, p.chunks - 1) * CK, lane, no);
-  __builtin_amdgcn_sched_barrier(0);   // keep this load order
+  // every wave loads a first chunk (a wave without chunks reloads the last and computes nothing)
   Chunk<MT, LW, CK> A, B, C;
   load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
   // The residual values this wave stores (residual epilogue) are fetched now, so
@@ -535,13 +384,9 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   const int st_local = st_mi * 16 + r * 4 + st_i;
   const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // the row this lane stores (M: none)
   uint32_t resv[(LW + 1) / 2];
-  load_scales<LW>(p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv, ncol & 1);
+  load_scales<LW>(!NORM && p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
+                  ncol & 1);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (NLDS) {
-    norm_finish<W, NKPW>(p, mbase, wave, lane, nl, a_lds);
-    __syncthreads();
-  }
-  if constexpr (NREG) norm_own<W, CK, LW>(p, wave, lane, c_begin < c_end, no, A);
   // One word per lane: straight-line schedules for 1, 2 and 3 chunks per wave
   // (every chunk of the wave in flight before the first is computed, each
   // computation waiting for its own chunk only), else a double-buffered loop.
@@ -552,17 +397,17 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   if constexpr (LW == 1) {
     looped = false;
     if (n == 1) {
-      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
     } else if (n == 2) {
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
     } else if (n == 3) {
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
       load_chunk<MT, LW, CK, NORM>(p, c_begin + 2, ncol, c, r, mbase, C);
-      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, c_begin * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (c_begin + 1) * CK, lane, zshift);
-      compute_chunk<MT, LW, CK, NLDS>(C, total, a_lds, (c_begin + 2) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
+      compute_chunk<MT, LW, CK, NORM>(C, total, ss, zshift);
     } else {
       looped = true;
     }
@@ -570,22 +415,26 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   if (looped) {
     for (int ch = c_begin; ch < c_end; ch += 2) {
       if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NLDS>(A, total, a_lds, ch * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
       if (ch + 1 >= c_end) break;
       if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 2, ncol, c, r, mbase, A);
-      compute_chunk<MT, LW, CK, NLDS>(B, total, a_lds, (ch + 1) * CK, lane, zshift);
+      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
     }
   }
 
   // ---- reduce the waves of this workgroup in LDS: one barrier, fixed order ----
-  // Every wave that had chunks parks its sums; then wave 4 mi + i adds row i of
-  // m-tile mi over the waves in wave order and stores it.
+  // Every wave that had chunks parks its sums (and, fused norm, its rows' sums of
+  // squares); then wave 4 mi + i adds row i of m-tile mi over the waves in wave
+  // order and stores it.
   const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
   static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
   {
-    __shared__ float red_static[NORM ? 1 : W * E * 64];
-    float* red = NORM ? reinterpret_cast<float*>(dyn_lds) : red_static;
-    if constexpr (NLDS) __syncthreads();   // every wave is done with the normalised rows
+    __shared__ float red[W * E * 64];
+    __shared__ float s_ss[NORM ? W : 1][16];
+    if constexpr (NORM) {
+      ss += __shfl_xor(ss, 16, 64);   // the four k sub-blocks of A row c
+      ss += __shfl_xor(ss, 32, 64);
+    }
     if (wave < nw) {
       float* dst = red + wave * E * 64 + lane;
 #pragma unroll
@@ -594,16 +443,26 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
         for (int t = 0; t < LW; ++t)
 #pragma unroll
           for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
+      if constexpr (NORM) {
+        if (lane < 16) s_ss[wave][lane] = ss;
+      }
     }
     __syncthreads();
     if (wave >= 4 * MT) return;
     float v[LW];
 #pragma unroll
     for (int t = 0; t < LW; ++t) v[t] = 0.0f;
+    float t_ss = 0.0f;   // fused norm: output row st_local of the tile is A row st_local (MT = 1)
     for (int w = 0; w < nw; ++w) {
       const float* src = red + w * E * 64 + lane;
 #pragma unroll
       for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
+      if constexpr (NORM) t_ss += s_ss[w][st_local];
+    }
+    if constexpr (NORM) {
+      const float inv = round_bf16(1.0f / sqrtf(t_ss / (float)p.K + p.eps));
+#pragma unroll
+      for (int t = 0; t < LW; ++t) v[t] *= inv;
     }
     store_row<LW>(p, ncol, st_m, v, resv);
   }
@@ -1073,65 +932,22 @@ Plan plan_linear(int M, int K, int N, bool paired) {
   return pl;
 }
 
-// LDS of the fused-norm variant: the normalised row tile, later reused by the
-// wave reduction.
-size_t norm_lds_bytes(const Plan& pl, int K) {
-  const size_t rows = (size_t)K * 32 + (size_t)K * 2;                  // K / 32 k-steps x 1 KB + norm weight
-  const size_t red = (size_t)pl.W * pl.MT * pl.LW * 4 * 64 * sizeof(float);
-  return rows > red ? rows : red;
-}
-
-template <int MT, int LW, int W, int CK, int NKPW>
-hipError_t launch_t(const LinearParams& p, dim3 grid, size_t lds, hipStream_t s) {
-  if constexpr (NKPW > 0) {
-    // raise the dynamic LDS limit once per kernel for tiles above 64 KB
-    static thread_local size_t raised = 65536;
-    if (lds > raised) {
-      hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(w4a16_mfma_kernel<MT, LW, W, CK, NKPW>),
-                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-      raised = lds;
-    }
-  }
+template <int MT, int LW, int W, int CK, bool NORM>
+hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   // the kernel takes x rows of K values (ldx = K) and K / (32 CK) chunks, as every plan here sets them
   if (p.ldx != p.K || p.chunks != p.K / (32 * CK)) return hipErrorInvalidValue;
   if (p.M >= (1 << 24) || p.rt < 1 || p.rt > 16 * MT || (p.rt & (p.rt - 1))) return hipErrorInvalidValue;
   const int m_rt = p.M | (__builtin_ctz((unsigned)p.rt) << 24);   // M and log2 of the row-tile height
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NKPW>), grid, dim3(64 * W), lds, s, p.x, p.qw, p.sc, p.qz,
-                     NKPW > 0 ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc, p.qz,
+                     NORM ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
   return hipGetLastError();
-}
-
-// Bound on the fused-norm prologue's k-steps per wave: the smallest of 1, 2, 4,
-// 8, 16 that covers K / 32 / W (0: no fused norm).
-int norm_kpw(int K, int W) {
-  const int need = (K / 32 + W - 1) / W;
-  int k = 1;
-  while (k < need) k <<= 1;
-  return k;
-}
-
-template <int MT, int LW, int W, int CK>
-hipError_t launch_cfg(const LinearParams& p, dim3 grid, size_t lds, int kpw, hipStream_t s) {
-  switch (kpw) {
-    case 0: return launch_t<MT, LW, W, CK, 0>(p, grid, lds, s);
-    case 1: return launch_t<MT, LW, W, CK, 1>(p, grid, lds, s);
-    case 2: return launch_t<MT, LW, W, CK, 2>(p, grid, lds, s);
-    case 4: return launch_t<MT, LW, W, CK, 4>(p, grid, lds, s);
-    case 8: return launch_t<MT, LW, W, CK, 8>(p, grid, lds, s);
-    case 16: return launch_t<MT, LW, W, CK, 16>(p, grid, lds, s);
-    default: return hipErrorInvalidValue;
-  }
 }
 
 hipError_t launch_plan(const Plan& pl, const LinearParams& p, bool norm, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
-  const size_t lds = norm ? norm_lds_bytes(pl, p.K) : 0;
-  // the fused norm's weight takes one 8-value load per thread: K <= 512 W
-  if (norm && p.K > 512 * pl.W) return hipErrorInvalidValue;
-  const int kpw = norm ? norm_kpw(p.K, pl.W) : 0;
-#define T2I_LAUNCH(a, b, c, d) \
-  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_cfg<a, b, c, d>(p, grid, lds, kpw, s);
+#define T2I_LAUNCH(a, b, c, d)                                         \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)             \
+    return norm ? launch_t<a, b, c, d, true>(p, grid, s) : launch_t<a, b, c, d, false>(p, grid, s);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;
@@ -1169,7 +985,6 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   if (!aligned16(x) || !aligned16(y0) || (y1 && !aligned16(y1)) || (residual && !aligned16(residual)))
     return fail(T2I_ERR_ALIGN, "activation pointers must be 16-byte aligned");
   if (gamma) {
-    if (K > NORM_MAX_K) return fail(T2I_ERR_SHAPE, "K=%d exceeds %d for the fused RMSNorm", K, NORM_MAX_K);
     if (!aligned16(gamma)) return fail(T2I_ERR_ALIGN, "norm_weight must be 16-byte aligned");
     if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
   }

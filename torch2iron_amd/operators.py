@@ -161,8 +161,6 @@ class _NormedProjection:
     def __post_init__(self):
         if self.in_features % 128 != 0:
             raise ValueError("in_features must be divisible by 128")
-        if self.in_features > 4096:
-            raise ValueError("in_features must be at most 4096 for the fused RMSNorm")
         if self.out_features % 64 != 0:
             raise ValueError("out_features must be divisible by 64")
         if not 1 <= self.rows <= 64:

@@ -132,7 +132,9 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
 def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: W4A16Weight,
                    out: torch.Tensor | None = None) -> torch.Tensor:
     """``y = rmsnorm(x) @ W^T`` with the RMSNorm done inside the linear kernel
-    (``x`` bf16 ``[M, K]`` is the un-normalised residual stream, 1 <= M <= 64, K <= 4096)."""
+    (``x`` bf16 ``[M, K]`` is the un-normalised residual stream, 1 <= M <= 64): the
+    kernel multiplies ``bf16(x * norm_weight)`` and scales each row's sums by its
+    ``1 / rms``, so it equals the unfused pair up to where products round to bf16."""
     _check_weight(w)
     _check_dev("x", x, BF16)
     _check_dev("norm_weight", norm_weight, BF16)
