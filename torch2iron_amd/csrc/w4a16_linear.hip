@@ -471,13 +471,15 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 // ============================================================================
 // Prompt-sized GEMM (hundreds of rows and more): a 64 x 128 output tile per
 // 256-thread workgroup, 4 waves of 32 x 64 (2 along M x 2 along N), one 128-k
-// tile (= one quantisation group) per step.  76.5 KB of LDS and 184 registers a
-// lane let two workgroups share a CU, so one's barriers, prologue and epilogue
-// overlap the other's k-loop (measured faster than one 128 x 128 workgroup of 8
-// waves a CU: gate_up at 8192 rows 225 -> 209 us).
+// tile (= one quantisation group) per step.  51 KB of LDS and at most 168
+// registers a lane (launch bounds) let three workgroups share a CU, so the
+// others' k-loops cover one's barriers, prologue and epilogue, and the VALU and
+// MFMA work of three waves a SIMD interleave (measured against two workgroups a
+// CU with three stage buffers: gate_up at 8192 rows 208 -> 183 us, qkv 127 ->
+// 113 us; and against one 128 x 128 workgroup of 8 waves a CU before that).
 //   * Every operand of a k-tile (activations, packed weights, the group's scale
 //     and zero words) is loaded straight into LDS (global_load_lds, no
-//     registers); three k-tiles are in flight, in three stage buffers.
+//     registers); two stage buffers: k-tile kt + 1 loads while kt is computed.
 //   * The pipeline's waits are all explicit: a wave waits (vmcnt) until its own
 //     loads of the k-tile it is about to compute have landed, the workgroup meets
 //     at a barrier (then everyone's have), and LDS is read with ds_read in inline
@@ -504,11 +506,7 @@ constexpr int GM_BROW = GM_BN;                // words per qweight row of the ti
 constexpr int GM_BPAIR_W = 2 * GM_BROW + 32;  // words per padded row pair
 constexpr int GM_BPAIR_PW = GM_BPAIR / GM_WAVES;   // weight row pairs loaded per wave
 static_assert(GM_BPAIR % GM_WAVES == 0 && GM_BN == 128, "whole weight row pairs per wave, 1 KB loads");
-// loads per wave per k-tile: its A fragments and its weight row pairs; wave 0 also
-// loads the scale and zero words
-constexpr int GM_OPS = GM_AF_W + GM_BPAIR_PW;
-constexpr int GM_OPS0 = GM_OPS + 2;
-constexpr int GM_STAGES = 3;
+constexpr int GM_STAGES = 2;
 // epilogue: each wave parks its 32 x 64 results as bf16 in LDS (rows padded to
 // 72 values) and stores them back as 16-byte row pieces
 constexpr int GM_EP_LD = 64 + 8;
@@ -562,7 +560,8 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // k-tile kt into stage st (rows past M reload row M - 1; their outputs are never
-// stored).  Each wave issues GM_OPS loads, wave 0 GM_OPS0.
+// stored).  Each wave loads its A fragments and weight row pairs; wave 0 also the
+// scale and zero words.
 __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0, int kt, int wave, int lane,
                                            GemmStage& st) {
   const int c = lane & 15, r = lane >> 4;
@@ -585,11 +584,6 @@ __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0
   }
 }
 
-// Waits until this wave's loads of the k-tile before the most recent one have landed.
-__device__ __forceinline__ void gemm_wait(int wave) {
-  if (wave == 0) wait_vm<GM_OPS0>();
-  else wait_vm<GM_OPS>();
-}
 
 // Fragments of k-step ks: A of this wave's rows, B of its columns.
 struct GemmFrags {
@@ -693,7 +687,7 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn
   }
 }
 
-__global__ __launch_bounds__(GM_THREADS) void w4a16_gemm_kernel(const LinearParams p) {
+__global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearParams p) {
   __shared__ GemmStage stg[GM_STAGES];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -714,32 +708,22 @@ __global__ __launch_bounds__(GM_THREADS) void w4a16_gemm_kernel(const LinearPara
 #pragma unroll
     for (int j = 0; j < 4; ++j) total[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Step kt: load k-tile kt + 2, compute k-tile kt, then wait until this wave's
-  // loads of k-tile kt + 1 have landed and meet the other waves (their loads have
-  // landed, and the stage of k-tile kt is free).  The last two steps issue no
-  // loads (peeled), so nothing is in flight when the epilogue starts.
+  // Step kt: load k-tile kt + 1 into the other stage (its last reader, k-tile
+  // kt - 1, is done: every wave met the barrier after it), compute k-tile kt, then
+  // wait until this wave's loads of kt + 1 have landed and meet the other waves
+  // (then everyone's have).  The last step issues no loads, so nothing is in
+  // flight when the epilogue starts.
   gemm_issue(p, m0, n0, 0, wave, lane, stg[0]);
-  if (KT > 1) {
-    gemm_issue(p, m0, n0, 1, wave, lane, stg[1]);
-    gemm_wait(wave);
-  } else {
-    wait_vm<0>();
-  }
+  wait_vm<0>();
   lds_barrier();
   int kt = 0;
-  for (; kt + 2 < KT; ++kt) {
-    gemm_issue(p, m0, n0, kt + 2, wave, lane, stg[(kt + 2) % GM_STAGES]);
-    gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
-    gemm_wait(wave);
-    lds_barrier();
-  }
-  if (kt + 1 < KT) {
-    gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
+  for (; kt + 1 < KT; ++kt) {
+    gemm_issue(p, m0, n0, kt + 1, wave, lane, stg[(kt + 1) & 1]);
+    gemm_compute(stg[kt & 1], wm, wn, lane, ncol0, total);
     wait_vm<0>();
     lds_barrier();
-    ++kt;
   }
-  gemm_compute(stg[kt % GM_STAGES], wm, wn, lane, ncol0, total);
+  gemm_compute(stg[kt & 1], wm, wn, lane, ncol0, total);
   lds_barrier();   // every wave is done reading the stages: they become the epilogue's tiles
 
   // ---- epilogue: total[mi][j][i] is row 16 (GM_MF wm + mi) + 4 r + i, column
