@@ -37,13 +37,54 @@ struct PrefillPrepParams {
   float eps;
 };
 
-// One workgroup (4 waves) per prompt row; wave w takes vectors w, w + 4, ...
-// of the row's Hq + 2 Hkv heads; a lane holds the rotation pair (i0, i1).
-// The vectors go in batches of PREP_BATCH a wave: every load of a batch (and the
-// norm weights) is issued before the first vector is normalised, so a batch
-// costs one memory round trip, not one per vector.  The loads are unconditional
-// (a wave past its last vector reloads it and drops it).
-constexpr int PREP_BATCH = 8;
+// One workgroup (4 waves) per prompt row.  A head vector (D = 128) is held by a
+// 16-lane row of a wave: lane c holds the 4 rotation pairs p = 4c .. 4c + 3,
+// elements (i0, i1) = (p, p + 64) (two halves) or (2p, 2p + 1) (interleaved),
+// that is two 8-byte pieces or one 16-byte piece of the vector, and the 4
+// (cos, sin) pairs of the RoPE row as one 16-byte piece.  A wave covers 4
+// vectors, the workgroup 16 at a time; every load of PREP_NB such batches (and
+// the norm weights and the RoPE row) is issued before the first vector is
+// normalised.  Loads are unconditional (vectors past the last reload it; nothing
+// is stored for them).  The sum of squares of a vector is a 16-lane DPP sum.
+constexpr int PREP_NB = 2;
+
+// Lane c's piece of a head vector: style 0 the i0 values of pairs 4c .. 4c + 3
+// then their i1 values (two 8-byte pieces), style 1 the four pairs interleaved.
+__device__ __forceinline__ u32x4 prep_load(const uint16_t* vec, int c, int style) {
+  if (style == 0) {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(vec + 4 * c);
+    const u32x2 b = *reinterpret_cast<const u32x2*>(vec + 64 + 4 * c);
+    return u32x4{a.x, a.y, b.x, b.y};
+  }
+  return *reinterpret_cast<const u32x4*>(vec + 8 * c);
+}
+
+__device__ __forceinline__ void prep_unpack(u32x4 v, int style, float (&x0)[4], float (&x1)[4]) {
+  if (style == 0) {
+    x0[0] = bf16_lo(v.x); x0[1] = bf16_hi(v.x); x0[2] = bf16_lo(v.y); x0[3] = bf16_hi(v.y);
+    x1[0] = bf16_lo(v.z); x1[1] = bf16_hi(v.z); x1[2] = bf16_lo(v.w); x1[3] = bf16_hi(v.w);
+  } else {
+    x0[0] = bf16_lo(v.x); x1[0] = bf16_hi(v.x); x0[1] = bf16_lo(v.y); x1[1] = bf16_hi(v.y);
+    x0[2] = bf16_lo(v.z); x1[2] = bf16_hi(v.z); x0[3] = bf16_lo(v.w); x1[3] = bf16_hi(v.w);
+  }
+}
+
+__device__ __forceinline__ u32x4 prep_pack(const float (&y0)[4], const float (&y1)[4], int style) {
+  if (style == 0)
+    return u32x4{pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]), pack_bf16x2(y1[0], y1[1]),
+                 pack_bf16x2(y1[2], y1[3])};
+  return u32x4{pack_bf16x2(y0[0], y1[0]), pack_bf16x2(y0[1], y1[1]), pack_bf16x2(y0[2], y1[2]),
+               pack_bf16x2(y0[3], y1[3])};
+}
+
+__device__ __forceinline__ void prep_store(uint16_t* vec, int c, int style, u32x4 v) {
+  if (style == 0) {
+    *reinterpret_cast<u32x2*>(vec + 4 * c) = u32x2{v.x, v.y};
+    *reinterpret_cast<u32x2*>(vec + 64 + 4 * c) = u32x2{v.z, v.w};
+  } else {
+    *reinterpret_cast<u32x4*>(vec + 8 * c) = v;
+  }
+}
 
 __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepParams p) {
   constexpr int D = PF_D;
@@ -52,49 +93,54 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepPara
   const int t = row - b * p.T;
   const int pos = p.p0 + t;
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = lane & 15;
+  const int slot = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * 4 + (lane >> 4);   // 0 .. 15
   const int nvec = p.Hq + 2 * p.Hkv;
-  const int i0 = p.style == 0 ? lane : 2 * lane;
-  const int i1 = p.style == 0 ? lane + D / 2 : 2 * lane + 1;
   const uint16_t* src_row = p.qkv + (size_t)row * nvec * D;
-  const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
-  const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
-  const float gq0 = bf16_to_f32(p.qn[i0]), gq1 = bf16_to_f32(p.qn[i1]);
-  const float gk0 = bf16_to_f32(p.kn[i0]), gk1 = bf16_to_f32(p.kn[i1]);
-  for (int base = wave; base < nvec; base += 4 * PREP_BATCH) {
-    float x0[PREP_BATCH], x1[PREP_BATCH];
+  for (int base = 0; base < nvec; base += 16 * PREP_NB) {
+    u32x4 raw[PREP_NB];
 #pragma unroll
-    for (int j = 0; j < PREP_BATCH; ++j) {
-      const uint16_t* src = src_row + (size_t)min(base + 4 * j, nvec - 1) * D;
-      x0[j] = bf16_to_f32(src[i0]);
-      x1[j] = bf16_to_f32(src[i1]);
-    }
-    // all of the batch's loads before its first use (the compiler would sink a
+    for (int j = 0; j < PREP_NB; ++j)
+      raw[j] = prep_load(src_row + (size_t)min(base + 16 * j + slot, nvec - 1) * D, c, p.style);
+    const u32x4 rp = *reinterpret_cast<const u32x4*>(p.rope + (size_t)pos * D + 8 * c);   // (cos, sin) x 4
+    const u32x4 gqv = prep_load(p.qn, c, p.style);
+    const u32x4 gkv = prep_load(p.kn, c, p.style);
+    // all of the batch's loads before the first use (the compiler would sink a
     // vector's loads behind the previous vector's normalisation)
 #pragma unroll
-    for (int j = 0; j < PREP_BATCH; ++j) asm volatile("" : "+v"(x0[j]), "+v"(x1[j]));
+    for (int j = 0; j < PREP_NB; ++j) asm volatile("" : "+v"(raw[j]));
     __builtin_amdgcn_sched_barrier(0);
+    const float cs[4] = {bf16_lo(rp.x), bf16_lo(rp.y), bf16_lo(rp.z), bf16_lo(rp.w)};
+    const float sn[4] = {bf16_hi(rp.x), bf16_hi(rp.y), bf16_hi(rp.z), bf16_hi(rp.w)};
+    float gq0[4], gq1[4], gk0[4], gk1[4];
+    prep_unpack(gqv, p.style, gq0, gq1);
+    prep_unpack(gkv, p.style, gk0, gk1);
 #pragma unroll
-    for (int j = 0; j < PREP_BATCH; ++j) {
-      const int vi = base + 4 * j;   // wave-uniform
-      if (vi >= nvec) break;
-      float y0 = x0[j], y1 = x1[j];
-      uint16_t* dst;
-      if (vi < p.Hq + p.Hkv) {
-        const bool isq = vi < p.Hq;
-        const float ss = wave_sum(y0 * y0 + y1 * y1);
-        const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-        const float n0 = round_bf16(round_bf16(y0 * inv) * (isq ? gq0 : gk0));
-        const float n1 = round_bf16(round_bf16(y1 * inv) * (isq ? gq1 : gk1));
-        y0 = round_bf16(round_bf16(n0 * cs) + round_bf16(-n1 * sn));
-        y1 = round_bf16(round_bf16(n1 * cs) + round_bf16(n0 * sn));
-        if (isq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
-        else dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
-      } else {
-        dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
+    for (int j = 0; j < PREP_NB; ++j) {
+      const int vi = base + 16 * j + slot;   // uniform over the 16-lane row
+      float x0[4], x1[4];
+      prep_unpack(raw[j], p.style, x0, x1);
+      const bool isq = vi < p.Hq;
+      const bool normed = vi < p.Hq + p.Hkv;   // q and k: RMSNorm + RoPE; v as is
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
+      ss = row_sum16(ss);
+      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+      float y0[4], y1[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float n0 = round_bf16(round_bf16(x0[e] * inv) * (isq ? gq0[e] : gk0[e]));
+        const float n1 = round_bf16(round_bf16(x1[e] * inv) * (isq ? gq1[e] : gk1[e]));
+        y0[e] = normed ? round_bf16(round_bf16(n0 * cs[e]) + round_bf16(-n1 * sn[e])) : x0[e];
+        y1[e] = normed ? round_bf16(round_bf16(n1 * cs[e]) + round_bf16(n0 * sn[e])) : x1[e];
       }
-      dst[i0] = (uint16_t)f32_to_bf16(y0);
-      dst[i1] = (uint16_t)f32_to_bf16(y1);
+      if (vi >= nvec) continue;
+      uint16_t* dst;
+      if (isq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
+      else if (normed) dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
+      else dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
+      prep_store(dst, c, p.style, prep_pack(y0, y1, p.style));
     }
   }
 }
