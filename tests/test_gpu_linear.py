@@ -193,7 +193,8 @@ def test_golden_fixture_on_gpu(gpu):
 
 
 NORM_CASES = [(1, 1024, 4096), (8, 1024, 4096), (16, 1024, 6144), (33, 2048, 4096), (64, 1024, 1024),
-              (5, 4096, 512), (16, 2048, 12288), (16, 1024, 1024), (7, 1024, 2048)]
+              (5, 4096, 512), (16, 2048, 12288), (16, 1024, 1024), (7, 1024, 2048),
+              (3, 128, 256), (2, 8192, 256)]   # one group (most waves idle); K past the old 4096 limit
 
 
 def check_rounding_of_activations(fused: torch.Tensor, unfused: torch.Tensor, xn: np.ndarray, w_nk: np.ndarray):
