@@ -411,9 +411,9 @@ class Qwen3Model:
         pf = self._prefill_buffers(t)
         toks = prompt.reshape(-1).to(torch.int32).to(self.device)
         ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"])
-        # Over prompt-sized batches the norms run as their own pass: the fused-norm
-        # linear normalises its row tile once per column block, which at thousands of
-        # rows costs more than one extra launch.
+        # Over prompt-sized batches the norms run as their own pass: the prompt GEMM
+        # has no fused-norm form, and the decode kernel's would redo each row's sum
+        # of squares once per column block.
         for i, layer in enumerate(self.layers):
             w = layer.w
             if i > 0:
