@@ -407,10 +407,12 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 // ============================================================================
 // lm_head (bf16 tied embedding) + greedy argmax
 // ============================================================================
-// 4 waves of 32 vocab columns (1188 workgroups for Qwen3's 151936): measured
-// 52.5 us for the 311 MB of the tied embedding, against 59.7 us with 64 columns
-// a wave (594 workgroups: CUs that get 3 of them against 2 set the tail), and
-// slower with 2 or 8 waves a workgroup.
+// 4 waves of up to 2 16-row tiles of the vocabulary each.  The workgroup count
+// is a multiple of 256 (one equal share per CU; Qwen3's 9496 tiles: 1280
+// workgroups of 7 or 8 tiles), each workgroup taking a contiguous range: with
+// 8 tiles a workgroup (1187 workgroups) 163 CUs took a fifth one, ~8 % over an
+// even split.  64-row waves (594 workgroups: CUs with 3 against 2 set the tail)
+// and 2 or 8 waves a workgroup were slower.
 constexpr int LMH_WAVES = 4;
 constexpr int LMH_COLS = 32;                // vocab columns per wave
 constexpr int LMH_TILES = LMH_COLS / 16;    // MFMA n-tiles per wave
@@ -431,6 +433,7 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
 __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
     const uint16_t* __restrict__ hin, int M, const uint16_t* __restrict__ E, int V, int K,
     float* __restrict__ logits, unsigned long long* __restrict__ keys) {
+  // this workgroup's tiles [tb, te) of the V / 16 (contiguous, balanced)
   extern __shared__ uint16_t s_h[];                 // [16][K + 8]
   const int ldh = K + 8;
   const int tid = threadIdx.x;
@@ -438,21 +441,27 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
   const int wave = tid >> 6;
   const int c = lane & 15;
   const int r = lane >> 4;
-  const int n0 = (blockIdx.x * LMH_WAVES + wave) * LMH_COLS;
+  const int T = V / 16;
+  const int tb = (int)((long long)blockIdx.x * T / gridDim.x);
+  const int te = (int)((long long)(blockIdx.x + 1) * T / gridDim.x);
+  const int tile0 = tb + LMH_TILES * wave;
+  const int n0 = tile0 * 16;
   f32x4 acc[LMH_TILES];
 #pragma unroll
   for (int t = 0; t < LMH_TILES; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
   bool tile_ok[LMH_TILES];
 #pragma unroll
-  for (int t = 0; t < LMH_TILES; ++t) tile_ok[t] = (n0 + 16 * t) < V;
+  for (int t = 0; t < LMH_TILES; ++t) tile_ok[t] = tile0 + t < te;
 
   // Double-buffered over 64-deep k slices: the next slice's rows are in flight
-  // while the current one is multiplied.  Rows past V reload row V - 1 (an
-  // unconditional load; their results are dropped).
+  // while the current one is multiplied.  A tile past the workgroup's range
+  // reloads the wave's first tile, or the workgroup's, rows that are loaded
+  // anyway (an unconditional load; its results are dropped).
+  const int nfirst = min(n0, (te - 1) * 16);
   auto load_slice = [&](int k0, u32x4 (&bv)[LMH_TILES][2]) {
 #pragma unroll
     for (int t = 0; t < LMH_TILES; ++t) {
-      const int row = min(n0 + 16 * t + c, V - 1);
+      const int row = (tile_ok[t] ? n0 + 16 * t : nfirst) + c;
       const uint16_t* src = E + (size_t)row * K + k0 + 16 * r;
       bv[t][0] = *reinterpret_cast<const u32x4*>(src);
       bv[t][1] = *reinterpret_cast<const u32x4*>(src + 8);
@@ -719,8 +728,12 @@ extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* 
   if (K < 64 || K % 64 || K > LMH_MAX_K) return fail(T2I_ERR_SHAPE, "K=%d must be a multiple of 64 in [64, %d]", K, LMH_MAX_K);
   if (!aligned16(h) || !aligned16(E) || (logits && !aligned16(logits)))
     return fail(T2I_ERR_ALIGN, "lm_head tensors must be 16-byte aligned");
-  const int cols_per_wg = LMH_WAVES * LMH_COLS;
-  dim3 grid((V + cols_per_wg - 1) / cols_per_wg);
+  // at most LMH_WAVES * LMH_TILES tiles a workgroup; a multiple of 256 workgroups
+  // once there are more than 256
+  const int tiles = V / 16;
+  int wgs = (tiles + LMH_WAVES * LMH_TILES - 1) / (LMH_WAVES * LMH_TILES);
+  if (wgs > 256) wgs = (wgs + 255) / 256 * 256;
+  dim3 grid(wgs);
   const size_t lds = (size_t)16 * (K + 8) * sizeof(uint16_t);
   if (lds > 65536) {
     static thread_local size_t raised = 0;
