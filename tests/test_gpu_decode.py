@@ -134,10 +134,12 @@ def test_decode_attention_out_of_range_position_is_inert(gpu):
 
 
 @pytest.mark.parametrize("m,v,k", [(16, 151936, 1024), (1, 4096, 1024), (5, 1040, 1024), (20, 2048, 1024),
-                                   (3, 1040, 64), (7, 528, 128), (16, 2064, 192), (2, 4096, 2048)])
+                                   (3, 1040, 64), (7, 528, 128), (16, 2064, 192), (2, 4096, 2048),
+                                   (3, 1040, 4096)])
 def test_lm_head_argmax(gpu, m, v, k):
-    """Slices of 64 k: one (peeled), two, an odd count after the loop, and K = 2048
-    (the staged tile spans two load batches)."""
+    """Slices of 64 k: one (peeled), two, an odd count after the loop, K = 2048 (the
+    staged tile spans two load batches and needs more than 64 KB of LDS) and the
+    largest K, 4096."""
     g = torch.Generator().manual_seed(v + k)
     h = torch.randn(m, k, generator=g).to(BF16)
     e = torch.randn(v, k, generator=g).to(BF16)

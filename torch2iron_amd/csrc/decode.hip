@@ -14,6 +14,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "t2i_common.h"
 
 namespace t2i {
@@ -736,14 +738,24 @@ extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* 
   dim3 grid(wgs);
   const size_t lds = (size_t)16 * (K + 8) * sizeof(uint16_t);
   if (lds > 65536) {
-    static thread_local size_t raised = 0;
-    if (lds > raised) {
-      int rc = t2i_host::hip_status(
+    // the attribute belongs to the function on the current device: remember the
+    // raised limit per device (a larger K raises it again)
+    constexpr int kMaxDevices = 64;
+    static std::atomic<size_t> raised[kMaxDevices];
+    int dev = 0;
+    int rc = t2i_host::hip_status(hipGetDevice(&dev), "lm_head device query");
+    if (rc) return rc;
+    if (dev < 0 || dev >= kMaxDevices || lds > raised[dev].load(std::memory_order_relaxed)) {
+      rc = t2i_host::hip_status(
           hipFuncSetAttribute(reinterpret_cast<const void*>(t2i::lm_head_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "lm_head LDS attribute");
       if (rc) return rc;
-      raised = lds;
+      if (dev >= 0 && dev < kMaxDevices) {
+        size_t cur = raised[dev].load(std::memory_order_relaxed);
+        while (cur < lds && !raised[dev].compare_exchange_weak(cur, lds, std::memory_order_relaxed)) {
+        }
+      }
     }
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
