@@ -3,6 +3,13 @@
 ``python -m torch2iron_amd.build`` compiles every ``csrc/*.hip`` into one shared
 library next to this file.  The library exports the C ABI of
 ``include/t2i_hip.h`` and is loaded with ctypes by ``torch2iron_amd._lib``.
+
+``python -m torch2iron_amd.build --tuning PATH`` writes a second library to PATH
+with ``T2I_TUNING`` defined: its plan functions then honour the environment
+overrides ``T2I_PLAN`` and ``T2I_RT`` (decode linear tile plan and row-tile
+height), ``T2I_GEMM_MIN_M`` (smallest M routed to the prompt GEMM) and
+``T2I_ATTN_ROWS`` (decode attention rows per chunk), for sweeps of the launch
+shapes.  Swap it in place of ``libt2i_hip.so`` to use it.
 """
 
 from __future__ import annotations
@@ -32,9 +39,10 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile all HIP sources into ``LIB_PATH`` and return its path."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def build(verbose: bool = False, out: Path | None = None, tuning: bool = False) -> Path:
+    """Compile all HIP sources into ``out`` (default ``LIB_PATH``) and return its path."""
+    out = Path(out) if out is not None else LIB_PATH
+    tmp = out.with_suffix(".so.tmp")
     cmd = [
         hipcc(),
         f"--offload-arch={ARCH}",
@@ -51,6 +59,7 @@ def build(verbose: bool = False) -> Path:
         # scale step then reads them without a v_accvgpr_read each (qkv GEMM at
         # 8192 rows 132 -> 127 us, down 99 -> 94 us)
         "-mllvm", "-amdgpu-mfma-vgpr-form",
+        *(["-DT2I_TUNING"] if tuning else []),
         f"-I{INCLUDE}",
         f"-I{CSRC}",
         *[str(s) for s in sources()],
@@ -62,9 +71,14 @@ def build(verbose: bool = False) -> Path:
     if proc.returncode != 0:
         sys.stderr.write(proc.stdout + proc.stderr)
         raise RuntimeError(f"hipcc failed with exit code {proc.returncode}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    if len(sys.argv) == 3 and sys.argv[1] == "--tuning":
+        print(build(verbose=True, out=Path(sys.argv[2]).resolve(), tuning=True))
+    elif len(sys.argv) == 1:
+        print(build(verbose=True))
+    else:
+        sys.exit("usage: python -m torch2iron_amd.build [--tuning PATH]")
