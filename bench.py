@@ -1,20 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X W4A16 hot path (one GPU).
 
-Workload (one "step"): the W4A16 group-128 linear over every Qwen3-0.6B linear
-shape -- fused qkv K=1024 N=4096, o_proj K=2048 N=1024, fused gate_up K=1024
-N=6144, down K=3072 N=1024 -- at M in {1, 8, 16, 32, 64} (batched decode), each
-(M, shape) pair launched once per weight copy of a pool larger than the
-256 MB MALL, so weights stream from HBM (HBM-cold).  The launches are
-captured in HIP graphs; inputs are resident in HBM before the timed region.
+Workload of the headline (one "step"): the W4A16 group-128 linear over every
+Qwen3-0.6B linear shape -- fused qkv K=1024 N=4096, o_proj K=2048 N=1024, fused
+gate_up K=1024 N=6144, down K=3072 N=1024 -- at M in {1, 8, 16, 32, 64}
+(batched decode).  Each (M, shape) group is one HIP graph that launches the
+linear once per weight copy of a pool of more than twice the 256 MB MALL, and
+the groups run in the order M, then shape, so a weight copy is used again only
+after the whole pool has streamed past: the weights come from HBM (HBM-cold).
+Inputs are resident in HBM before the timed region.
 
 ``value`` = algorithmic bytes of all launches / wall time of the timed steps
 (TB/s).  Algorithmic bytes per launch: K*N/2 (int4) + (K/128)*N*2 (fp16
 scales) + (K/128)*(N/8)*4 (int32 zeros) + M*K*2 + M*N*2 (bf16 in/out).
 
-Extra fields: the MALL-warm rate (one weight copy reused), the per-(M, shape)
-breakdown, the Qwen3-1.7B sweep, a roofline entry for the linear kernel and
-the CPU baseline (the oracle's dequant + fp32 matmul on the host cores).
+Extra fields: the per-(M, shape) breakdown, the MALL-warm rate (one weight copy
+reused), the single GEMV of Qwen3-0.6B's up_proj shape (M=1, K=1024, N=3072;
+HBM-cold and MALL-warm), the Qwen3-1.7B sweep, one fused decode layer (batch 8,
+context 1024), batch-16 greedy decode of the full random-init Qwen3-0.6B, the
+roofline entry for the linear kernel, and the CPU baselines (the oracle on the
+host cores, for each configuration).
 """
 
 from __future__ import annotations
@@ -22,6 +27,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -34,16 +40,16 @@ METRIC = "W4A16 linear achieved HBM TB/s (% of peak); batch-decode tokens/s"
 PEAK_GBPS = 8000.0
 QWEN3_06B = [("qkv", 1024, 4096), ("o_proj", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)]
 QWEN3_17B = [("qkv", 2048, 4096), ("o_proj", 2048, 2048), ("gate_up", 2048, 12288), ("down", 6144, 2048)]
+GEMV_06B = [("up_proj", 1024, 3072)]
 MALL_BYTES = 256 << 20
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = ROOT / "profiles" / "w4a16_linear_qwen3_0.6b_sweep_traffic.json"
+KERNELS_FILE = ROOT / "profiles" / "w4a16_linear_qwen3_0.6b_sweep_kernels.json"
 
 
-def measured_traffic():
-    """HBM bytes per launch of the sweep's linear kernel, from the FETCH_SIZE /
-    WRITE_SIZE counter runs summarised in ``TRAFFIC_FILE`` (None if absent)."""
+def _load_json(path: Path):
     try:
-        return json.loads(TRAFFIC_FILE.read_text())
+        return json.loads(path.read_text())
     except (OSError, ValueError):
         return None
 
@@ -57,8 +63,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--pool-mb", type=int, default=320, help="weight pool per sweep (> 256 MB MALL)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pool-mb", type=int, default=544, help="weight pool per sweep (> 2 x the 256 MB MALL)")
+    ap.add_argument("--cpu-seconds", type=float, default=5.0, help="CPU budget per baseline leg")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true", help="only the headline sweep")
     ap.add_argument("--skip-decode", action="store_true", help="skip the decode layer / greedy decode runs")
@@ -73,7 +79,11 @@ def parse():
 
 
 class Sweep:
-    """Graph-captured launches of one (M, shape) grid over a weight pool."""
+    """Graph-captured launches of one (M, shape) grid over a weight pool.
+
+    Group (M, shape) launches the linear once per copy of that shape's weights;
+    the groups run M-major, so between two uses of one copy the whole pool is
+    read (the reuse distance is the pool size)."""
 
     def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None, eager=False):
         import torch
@@ -89,7 +99,6 @@ class Sweep:
                         for name, k, n in shapes}
         # launches per graph: one per weight copy (HBM-cold), or ``reps`` of the one copy (MALL-warm)
         self.reps = reps or self.copies
-        self.eager = eager
         self.groups = []   # (label, M, K, N, graph, bytes, launches)
         for m in ms:
             for name, k, n in shapes:
@@ -115,6 +124,10 @@ class Sweep:
         self.bytes_per_step = sum(gr["bytes"] for gr in self.groups)
         self.launches_per_step = sum(gr["launches"] for gr in self.groups)
 
+    @property
+    def pool_mb(self) -> float:
+        return self.copies * self.per_copy / 1e6
+
     def run(self, steps, warmup):
         torch = self.torch
         for _ in range(warmup):
@@ -139,11 +152,48 @@ class Sweep:
         per_group = [t / steps for t in per_group]
         return total_ms, per_group
 
+    def breakdown(self, per_group):
+        return {gr["label"]: {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
+                              "us_per_launch": round(t * 1e3 / gr["launches"], 3)}
+                for gr, t in zip(self.groups, per_group)}
+
+
+def rate(sweep: Sweep, steps: int, warmup: int):
+    total_ms, per_group = sweep.run(steps, warmup)
+    ms_step = total_ms / steps
+    return sweep.bytes_per_step / (ms_step * 1e-3) / 1e12, ms_step, per_group
+
+
+def launch_floor(dev, launches: int, steps: int, warmup: int) -> float:
+    """The same number of back-to-back graph launches of a one-element fill: what a
+    dependent launch costs on this stream before any kernel does work (us)."""
+    import torch
+    tiny = torch.zeros(1, device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(launches):
+            tiny.fill_(0.0)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (steps * launches)
+
+
+# ---------------------------------------------------------------------------
+# decode: config 3 (one fused layer) and config 4 (full model, greedy)
+# ---------------------------------------------------------------------------
 
 def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int, batch: int,
-                 streams=(1, 2, 4)):
+                 streams=(1, 2)):
     """Config 3 (one fused decode layer, batch 8, 1024 cached tokens) and config 4
     (full Qwen3-0.6B, batch 16 greedy decode) on random-init weights."""
+    import numpy as np
     import torch
     from torch2iron_amd import model as gm
 
@@ -233,6 +283,17 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                       "first_token_equal_to_prefill": bool(torch.equal(tf[:, 0], toks[:, 0])),
                       "tokens_equal_to_prefill_run": bool(torch.equal(tf, toks))}
     log(f"teacher-forced prompt: {tm['prompt_ms']:.1f} ms")
+    # the fp32 oracle's first 32 tokens for this exact model and prompt (written offline by
+    # tests/golden/make_qwen3_greedy_golden.py from the same seeds)
+    oracle = {}
+    fixture = ROOT / "tests" / "golden" / "qwen3_0.6b_greedy.npz"
+    if fixture.exists() and batch == 16 and prompt_len == 512 and new_tokens >= 32:
+        with np.load(fixture) as f:
+            if np.array_equal(f["prompt"], prompt.numpy()):
+                ref = f["uniform_tokens"]
+                got32 = toks[:, :ref.shape[1]].numpy()
+                oracle = {"sequences_matching_fp32_oracle_32_steps": int((got32 == ref).all(axis=1).sum()),
+                          "of": int(ref.shape[0])}
     best = max(runs.values(), key=lambda r: r["decode_tokens_per_s"])
     out["batch_decode"] = {
         "workload": f"random-init Qwen3-0.6B (28 layers, W4A16 g128, bf16 tied lm_head), batch {batch}, "
@@ -240,82 +301,124 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         **best,
         "by_streams": {str(k): v for k, v in runs.items()},
         "teacher_forced_prompt": teacher_forced,
+        "greedy_parity": oracle,
         "first_tokens": toks[:2, :8].tolist(),
     }
     del model
     torch.cuda.empty_cache()
-    return out, tensors, prompt, toks
+    return out, tensors, prompt
 
 
-def cpu_decode_baseline(tensors, seconds: float, batch: int):
-    """The oracle (torch fp32 on the host cores) decoding a batch: a bounded sample."""
+# ---------------------------------------------------------------------------
+# CPU baselines: the oracle on the host cores (bounded samples)
+# ---------------------------------------------------------------------------
+
+def cpu_info() -> dict:
+    import torch
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads()}
+
+
+def _timed_runs(fn, seconds: float, min_runs: int = 20, max_runs: int = 200):
+    """Median wall time (s) of ``fn()`` over at least ``min_runs`` runs, more while
+    the budget lasts; one untimed warm-up run first."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while len(times) < max_runs and (len(times) < min_runs or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_linear_baselines(seconds: float) -> dict:
+    """Configs 0-2 on the host: per call, the oracle's dequant + fp32 group-loop
+    matmul (the reference runtime's arithmetic, ``model.py:133-146``), and the
+    matmul alone with the dense fp32 weight cached (the reference caches its
+    unpacked weight, ``model.py:122-131``)."""
+    import numpy as np
+    from oracle import w4a16 as ow
+    from torch2iron_amd.formats import algorithmic_bytes
+
+    out = {}
+    cases = [("config0_gemv", "up_proj", 1, 1024, 3072)]
+    cases += [(f"config1_M16_{n}", n, 16, k, nn) for n, k, nn in QWEN3_06B]
+    cases += [(f"config2_M16_{n}", n, 16, k, nn) for n, k, nn in QWEN3_17B]
+    for i, (label, _, m, k, n) in enumerate(cases):
+        qw, qz, sc = ow.synthetic_tensors(k, n, seed=100 + i)
+        x = np.random.default_rng(i).standard_normal((m, k)).astype(np.float32)
+        b = algorithmic_bytes(m, k, n)
+        t_call, n_call = _timed_runs(lambda: ow.linear(x, qw, qz, sc, accumulate="fp32"), seconds / 2)
+        w = ow.dequantize(qw, qz, sc)
+        t_mm, n_mm = _timed_runs(lambda: x @ w.T, seconds / 2)
+        out[label] = {"M": m, "K": k, "N": n,
+                      "dequant_matmul_us": round(t_call * 1e6, 1), "dequant_matmul_GBps": round(b / t_call / 1e9, 3),
+                      "cached_matmul_us": round(t_mm * 1e6, 1), "cached_matmul_GBps": round(b / t_mm / 1e9, 3),
+                      "runs": [n_call, n_mm]}
+    return out
+
+
+def cpu_decode_baselines(tensors, prompt, seconds: float, new_tokens: int) -> dict:
+    """Configs 3 and 4 on the host with the fp32 oracle (dense fp32 weights cached):
+    one decode layer at batch 8, context 1024; the batch-16 prompt pass over the
+    same 512-token prompt as the GPU run, then greedy decode steps from it."""
     import torch
     from oracle import qwen3 as oq
     from torch2iron_amd import model as gm
 
     cfg = gm.QWEN3_0_6B
     ocfg = oq.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__})
-    torch.set_num_threads(os.cpu_count() or 1)
-    m = oq.DenseQwen3(tensors, ocfg, mode="fp32", ctx_cap=640)
-    prompt = torch.randint(0, cfg.vocab, (batch, 16), generator=torch.Generator().manual_seed(7))
+    out = {}
+    # config 3: layer 0 of the same weights, B = 8, 1024 cached positions, write at 1024
+    layer = oq.DenseLayer(tensors, "model.layers.0", ocfg)
+    g = torch.Generator().manual_seed(5)
+    kc = torch.randn(8, cfg.n_kv_heads, 1088, cfg.head_dim, generator=g)
+    vc = torch.randn(8, cfg.n_kv_heads, 1088, cfg.head_dim, generator=g)
+    x = torch.randn(8, cfg.hidden, generator=g)
+    angles = oq.rope_angles(cfg.head_dim, 1088, cfg.rope_theta)
+    pos = torch.full((8,), 1024, dtype=torch.long)
+    rnd = oq._Round("fp32")
+    with torch.no_grad():
+        t_layer, n_layer = _timed_runs(lambda: layer.decode(x, kc, vc, pos, angles, rnd), seconds, min_runs=20)
+    out["config3_decode_layer"] = {"us": round(t_layer * 1e6, 1), "runs": n_layer,
+                                   "sample": "fp32 oracle decode layer, batch 8, context 1024, median"}
+    del layer, kc, vc
+    # config 4: the whole model
+    b, plen = prompt.shape
+    m = oq.DenseQwen3(tensors, ocfg, mode="fp32", ctx_cap=plen + new_tokens)
+    t0 = time.perf_counter()
     logits = m.prefill(prompt)
-    pos = torch.full((batch,), 16, dtype=torch.long)
-    steps = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    t_prompt = time.perf_counter() - t0
+    pos = torch.full((b,), plen, dtype=torch.long)
+    step_times = []
+    t_end = time.perf_counter() + seconds
+    while len(step_times) < 3 or (time.perf_counter() < t_end and len(step_times) < new_tokens - 1):
         nxt = torch.argmax(logits, dim=-1)
+        t1 = time.perf_counter()
         logits = m.decode_step(nxt, pos)
+        step_times.append(time.perf_counter() - t1)
         pos = pos + 1
-        steps += 1
-    dt = time.perf_counter() - t0
-    return {"value": round(batch * steps / dt, 2), "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{steps} batch-{batch} fp32 decode steps of the oracle after a 16-token prompt, {dt:.1f} s"}
-
-
-def cpu_baseline(seconds: float):
-    """The oracle (numpy) on the host: per-call dequant + fp32 matmul, M=16,
-    over the four Qwen3-0.6B shapes in turn, for about ``seconds``."""
-    import numpy as np
-    from oracle import w4a16 as ow
-    from torch2iron_amd.formats import algorithmic_bytes
-
-    try:
-        from threadpoolctl import threadpool_info
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # noqa: BLE001
-        cores = os.cpu_count() or 1
-    m = 16
-    data = []
-    for i, (_, k, n) in enumerate(QWEN3_06B):
-        qw, qz, sc = ow.synthetic_tensors(k, n, seed=100 + i)
-        x = np.random.default_rng(i).standard_normal((m, k)).astype(np.float32)
-        data.append((x, qw, qz, sc, algorithmic_bytes(m, k, n)))
-    calls, nbytes = 0, 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        x, qw, qz, sc, b = data[calls % len(data)]
-        ow.linear(x, qw, qz, sc, accumulate="fp32")
-        calls += 1
-        nbytes += b
-    dt = time.perf_counter() - t0
-    # cached dense weights (the reference caches its unpacked weight)
-    dense = [(x, ow.dequantize(qw, qz, sc), b) for x, qw, qz, sc, b in data]
-    ccalls, cbytes = 0, 0
-    t1 = time.perf_counter()
-    while time.perf_counter() - t1 < min(seconds, 5.0):
-        x, w, b = dense[ccalls % len(dense)]
-        _ = x @ w.T
-        ccalls += 1
-        cbytes += b
-    cdt = time.perf_counter() - t1
-    return {
-        "value": nbytes / dt / 1e12, "unit": "TB/s", "cores": int(cores), "kind": "port",
-        "sample": f"{calls} calls of oracle dequant+fp32 matmul (M=16, Qwen3-0.6B shapes in turn) in {dt:.1f} s",
-        "cached_weights_value": cbytes / cdt / 1e12,
-        "cached_weights_sample": f"{ccalls} fp32 matmuls with cached dense weights in {cdt:.1f} s",
-        "cpu_count": os.cpu_count(),
+    t_step = statistics.median(step_times)
+    t_decode = t_step * (new_tokens - 1)
+    out["config4_batch_decode"] = {
+        "prompt_s": round(t_prompt, 2),
+        "prompt_tokens_per_s": round(b * plen / t_prompt, 1),
+        "ms_per_decode_step": round(t_step * 1e3, 2),
+        "decode_tokens_per_s": round(b / t_step, 2),
+        "end_to_end_tokens_per_s": round(b * new_tokens / (t_prompt + t_decode), 2),
+        "sample": (f"fp32 oracle: one batch-{b} prompt pass over {plen} tokens (timed), then {len(step_times)} "
+                   f"decode steps from position {plen} (median); end to end = prompt + {new_tokens - 1} x the "
+                   f"median step"),
     }
+    return out
 
 
 def main():
@@ -334,40 +437,18 @@ def main():
     ms = [1, 8, 16, 32, 64]
     log(f"building HBM-cold sweep (pool {args.pool_mb} MB)")
     cold = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1, eager=args.eager)
-    log(f"{cold.copies} weight copies, {cold.launches_per_step} launches/step, "
+    log(f"{cold.copies} weight copies ({cold.pool_mb:.0f} MB), {cold.launches_per_step} launches/step, "
         f"{cold.bytes_per_step / 1e6:.1f} MB/step")
-    total_ms, per_group = cold.run(args.steps, args.warmup)
-    torch.cuda.synchronize()
-    # barrier-equivalent for one process: synchronised on both sides of the timed region
-    ms_per_step = total_ms / args.steps
-    value = cold.bytes_per_step / (ms_per_step * 1e-3) / 1e12
+    value, ms_per_step, per_group = rate(cold, args.steps, args.warmup)
     avg_launch_us = ms_per_step * 1e3 / cold.launches_per_step
     log(f"HBM-cold sweep: {value:.3f} TB/s, {ms_per_step:.3f} ms/step, avg launch {avg_launch_us:.2f} us")
-    floor_us = None
-    if not args.eager:
-        # the same number of back-to-back graph launches of a one-element fill: what a
-        # dependent launch costs on this stream before any kernel does work
-        tiny = torch.zeros(1, device=dev)
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for _ in range(cold.launches_per_step):
-                tiny.fill_(0.0)
-        for _ in range(args.warmup):
-            g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        floor_us = e0.elapsed_time(e1) * 1e3 / (args.steps * cold.launches_per_step)
+    floor_us = None if args.eager else launch_floor(dev, cold.launches_per_step, args.steps, args.warmup)
+    if floor_us is not None:
         log(f"launch floor (one-element fill, graph): {floor_us:.2f} us per launch")
-        del g, tiny
-    breakdown = {}
-    for gr, t in zip(cold.groups, per_group):
-        breakdown[gr["label"]] = {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
-                                  "us_per_launch": round(t * 1e3 / gr["launches"], 3)}
+    breakdown = cold.breakdown(per_group)
+    cold_pool_mb = cold.pool_mb
+    cold_copies = cold.copies
+    cold_bytes = cold.bytes_per_step
 
     if args.calibrate_copy:
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
@@ -376,40 +457,68 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    del cold
+    torch.cuda.empty_cache()
 
     extra = {}
     if not args.skip_extra:
         log("MALL-warm sweep (one weight copy)")
-        warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2, reps=cold.copies)
-        w_ms, _ = warm.run(args.steps, args.warmup)
-        extra["mall_warm_TBps"] = round(warm.bytes_per_step / (w_ms / args.steps * 1e-3) / 1e12, 4)
+        warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2, reps=cold_copies)
+        extra["mall_warm_TBps"] = round(rate(warm, args.steps, args.warmup)[0], 4)
         del warm
+        log("single GEMV, M=1 K=1024 N=3072 (HBM-cold and MALL-warm)")
+        gv = Sweep(GEMV_06B, [1], args.pool_mb << 20, dev, seed=4)
+        gv_rate, gv_ms, _ = rate(gv, args.steps, args.warmup)
+        gvw = Sweep(GEMV_06B, [1], 0, dev, seed=5, reps=gv.copies)
+        gvw_rate, gvw_ms, _ = rate(gvw, args.steps, args.warmup)
+        extra["gemv_m1_k1024_n3072"] = {
+            "workload": f"W4A16 GEMV M=1 K=1024 N=3072 (Qwen3-0.6B up_proj), {gv.copies} launches per step",
+            "hbm_cold_TBps": round(gv_rate, 4), "hbm_cold_us_per_launch": round(gv_ms * 1e3 / gv.launches_per_step, 3),
+            "mall_warm_TBps": round(gvw_rate, 4), "mall_warm_us_per_launch": round(gvw_ms * 1e3 / gvw.launches_per_step, 3),
+            "pool_mb": round(gv.pool_mb, 1)}
+        del gv, gvw
         log("Qwen3-1.7B sweep (HBM-cold)")
         big = Sweep(QWEN3_17B, [1, 16, 64], args.pool_mb << 20, dev, seed=3)
-        b_ms, b_groups = big.run(max(2, args.steps // 2), 1)
-        extra["qwen3_1_7b_sweep_TBps"] = round(big.bytes_per_step / (b_ms / max(2, args.steps // 2) * 1e-3) / 1e12, 4)
-        extra["qwen3_1_7b_breakdown"] = {gr["label"]: round(gr["bytes"] / (t * 1e-3) / 1e12, 4)
-                                         for gr, t in zip(big.groups, b_groups)}
+        b_steps = max(2, args.steps // 2)
+        b_rate, _, b_groups = rate(big, b_steps, 1)
+        extra["qwen3_1_7b_sweep_TBps"] = round(b_rate, 4)
+        extra["qwen3_1_7b_breakdown"] = big.breakdown(b_groups)
+        extra["qwen3_1_7b_pool_mb"] = round(big.pool_mb, 1)
         del big
+        torch.cuda.empty_cache()
     torch.cuda.synchronize()
 
     decode = None
-    tensors = None
+    tensors = prompt = None
     if not args.skip_decode:
-        decode, tensors, _, _ = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens,
-                                             args.batch, [int(v) for v in args.streams.split(",")])
+        decode, tensors, prompt = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens,
+                                               args.batch, [int(v) for v in args.streams.split(",")])
         torch.cuda.synchronize()
 
     cpu = None
     if not args.skip_cpu:
-        log(f"CPU baseline ({args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline(args.cpu_seconds)
+        log(f"CPU baselines (about {args.cpu_seconds:.0f} s per leg)")
+        info = cpu_info()
+        lin = cpu_linear_baselines(args.cpu_seconds)
+        # the headline's CPU figure: the per-call form over the config-1 shapes at M=16
+        c1 = [v for k, v in lin.items() if k.startswith("config1_")]
+        c1_bytes = sum(v["dequant_matmul_GBps"] * v["dequant_matmul_us"] for v in c1)   # GB/s * us = kB
+        c1_us = sum(v["dequant_matmul_us"] for v in c1)
+        c1_cached = sum(v["cached_matmul_GBps"] * v["cached_matmul_us"] for v in c1)
+        c1_cached_us = sum(v["cached_matmul_us"] for v in c1)
+        cpu = {"value": round(c1_bytes / c1_us / 1e3, 6), "unit": "TB/s", "cores": info["torch_threads"],
+               "kind": "port",
+               "sample": "oracle dequant + fp32 matmul per call, M=16, the four Qwen3-0.6B shapes, median of >= 20 "
+                         "calls each (algorithmic bytes over time)",
+               "cached_weights_value": round(c1_cached / c1_cached_us / 1e3, 6),
+               **info, "linear": lin}
         if tensors is not None:
-            log(f"CPU decode baseline ({args.cpu_seconds:.0f} s)")
-            cpu["decode"] = cpu_decode_baseline(tensors, args.cpu_seconds, args.batch)
+            log("CPU decode baselines (config 3 layer, config 4 prompt pass + decode steps)")
+            cpu.update(cpu_decode_baselines(tensors, prompt, args.cpu_seconds, args.new_tokens))
 
     achieved_gbps = value * 1e3
-    traffic = measured_traffic()
+    traffic = _load_json(TRAFFIC_FILE)
+    kernels = _load_json(KERNELS_FILE)
     line = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -425,11 +534,11 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "W4A16 group-128 linear sweep, Qwen3-0.6B qkv/o_proj/gate_up/down x M in {1,8,16,32,64}, "
-                        f"HBM-cold ({cold.copies}-copy weight pool, {cold.copies * cold.per_copy / 1e6:.0f} MB)",
+                        f"HBM-cold ({cold_copies}-copy weight pool, {cold_pool_mb:.0f} MB)",
             "weights": "int4 AutoGPTQ (uniform nibbles, fp16 scales U[0.005,0.02])",
             "activations": "bf16 N(0,1)",
-            "launches_per_step": cold.launches_per_step,
-            "bytes_per_step": cold.bytes_per_step,
+            "launches_per_step": len(ms) * len(QWEN3_06B) * cold_copies,
+            "bytes_per_step": cold_bytes,
         },
         "roofline": {
             "bound": "hbm",
@@ -442,6 +551,11 @@ def main():
             "kernel": "w4a16_mfma_kernel",
             "avg_launch_us": round(avg_launch_us, 3),
             "launch_floor_us": None if floor_us is None else round(floor_us, 3),
+            "kernel_time": None if not kernels else {
+                "avg_kernel_us": kernels.get("avg_kernel_us"),
+                "algorithmic_bytes_per_launch": kernels.get("algorithmic_bytes_per_launch"),
+                "frac": kernels.get("frac"),
+                "source": kernels.get("source")},
         },
         "cpu_baseline": cpu,
         "breakdown": breakdown,

@@ -39,7 +39,7 @@ extern "C" {
 
 #define T2I_OK 0
 #define T2I_ERR_NULL (-1)      /* a required pointer is NULL */
-#define T2I_ERR_SHAPE (-2)     /* a size is not supported (K % 128, N % 64, M range, ...) */
+#define T2I_ERR_SHAPE (-2)     /* a size is not supported (K % 128, N % 16, M range, ...) */
 #define T2I_ERR_ALIGN (-3)     /* a pointer is not 16-byte aligned */
 #define T2I_ERR_GROUP (-4)     /* group size other than 128 */
 #define T2I_ERR_WORKSPACE (-5) /* workspace missing or too small */
@@ -61,7 +61,7 @@ int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,
 
 /* ---------------------------------------------------------------------------
  * W4A16 linear: y[M, N] = x[M, K] . W^T, fp32 accumulation, bf16 output.
- * 1 <= M <= T2I_MAX_ROWS; K % 128 == 0; N % 64 == 0.  M = 1 is the GEMV case,
+ * 1 <= M <= T2I_MAX_ROWS; K % 128 == 0; N % 16 == 0.  M = 1 is the GEMV case,
  * M up to 64 the batched decode, larger M a prompt (prefill) batch.
  * residual (nullable, may alias y): y = bf16(bf16(x.W^T) + residual).
  * Replaces: quantized_qwen3/operators/w4a16_gemv/op.py:22-126 (W4A16GEMV, M = 1)
@@ -77,7 +77,7 @@ int t2i_w4a16_linear(const uint16_t* x, int32_t M,
 
 /* ---------------------------------------------------------------------------
  * Paired gate/up linear over one weight whose columns alternate gate and up
- * (fused column 2i = gate i, 2i+1 = up i; N = 2*I, N % 64 == 0).  swiglu != 0: h[M, I] = bf16(bf16(silu(bf16 gate)) * bf16 up) into y0,
+ * (fused column 2i = gate i, 2i+1 = up i; N = 2*I, N % 32 == 0).  swiglu != 0: h[M, I] = bf16(bf16(silu(bf16 gate)) * bf16 up) into y0,
  * y1 unused.  swiglu == 0: y0 = gate [M, I], y1 = up [M, I].
  * Replaces: quantized_qwen3/operators/w4a16_gemm/op.py:178-263 (W4A16PairedKGroupGEMM,
  *           gate = pair 0, up = pair 1) + torch2iron/operators/silu_mul (SiLUMul).

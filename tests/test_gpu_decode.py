@@ -13,6 +13,7 @@ import torch
 from oracle import qwen3 as oq
 from torch2iron_amd import model as gm
 from torch2iron_amd import ops
+from torch2iron_amd.formats import W4A16Weight, interleave_gate_up, random_tensors
 
 pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
@@ -313,3 +314,63 @@ def test_decode_attention_repeat_calls_reset_arrivals(gpu, hq, hkv, cap):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     for buf in ws._bufs.values():
         assert torch.count_nonzero(buf[:b * hkv * 4]).item() == 0, "arrival counters not reset"
+
+
+def test_decode_mode_generate_with_new_prompts_and_lengths(gpu):
+    """The captured prompt-bookkeeping graph reads the model's prompt buffer: a new
+    prompt of the same length is seen by the replays, and a new length re-captures.
+    Every run equals eager launches on the same prompt."""
+    cfg = gm.Qwen3Config(n_layers=2, vocab=2048)
+    t = gm.random_qwen3_tensors(cfg, seed=51, weights="centered")
+    model = gm.Qwen3Model(t, cfg, batch=4, ctx_cap=48, device=gpu)
+    runs = []
+    for plen, seed in ((10, 52), (10, 53), (7, 54), (10, 52)):
+        prompt = torch.randint(0, cfg.vocab, (4, plen), generator=torch.Generator().manual_seed(seed))
+        got = model.generate(prompt, 8, prompt_mode="decode")
+        eager = model.generate(prompt, 8, prompt_mode="decode", use_graph=False)
+        assert torch.equal(got, eager), f"prompt length {plen}, seed {seed}: graph replay differs from eager"
+        runs.append(got)
+    assert torch.equal(runs[0], runs[3]) and not torch.equal(runs[0], runs[1])
+
+
+def test_wrappers_reject_undersized_outputs(gpu):
+    """Output and auxiliary buffers are size-checked before any launch (ValueError)."""
+    d, b, hq, hkv, cap = 128, 2, 4, 2, 32
+    qkv = torch.zeros(b, (hq + 2 * hkv) * d, dtype=BF16, device=gpu)
+    pos = torch.zeros(b, dtype=torch.int32, device=gpu)
+    ones = torch.ones(d, dtype=BF16, device=gpu)
+    rope = gm.rope_table(d, cap, 1e6, gpu)
+    kc = torch.zeros(b, hkv, cap, d, dtype=BF16, device=gpu)
+    small = torch.zeros(8, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.decode_attention(qkv, pos, hq, hkv, ones, ones, 1e-6, rope, kc, kc.clone(), out=small)
+    with pytest.raises(ValueError):
+        ops.decode_attention(qkv, pos, hq, hkv, ones, ones[:64], 1e-6, rope, kc, kc.clone())
+    x = torch.zeros(3, 256, dtype=BF16, device=gpu)
+    w = torch.ones(256, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.rmsnorm(x, w, 1e-6, out=small)
+    with pytest.raises(ValueError):
+        ops.rmsnorm(x, w, 1e-6, argmax_keys=torch.zeros(2, dtype=torch.int64, device=gpu))
+    table = torch.zeros(10, 256, dtype=BF16, device=gpu)
+    tok = torch.zeros(3, dtype=torch.int32, device=gpu)
+    with pytest.raises(ValueError):
+        ops.rmsnorm(table, w, 1e-6, tokens=tok, x_out=small)
+    emb = torch.zeros(64, 256, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.lm_head_argmax(x, emb, torch.zeros(2, dtype=torch.int64, device=gpu))
+    with pytest.raises(ValueError):
+        ops.lm_head_argmax(x.view(-1), emb, torch.zeros(3, dtype=torch.int64, device=gpu))
+    wp = W4A16Weight.from_numpy(*interleave_gate_up(random_tensors(256, 64, 1), random_tensors(256, 64, 2)),
+                                device=gpu)
+    with pytest.raises(ValueError):
+        ops.gate_up(x, wp, swiglu=False, out_up=small)
+    q = torch.zeros(b, hq, 4, d, dtype=BF16, device=gpu)
+    kc64 = torch.zeros(b, hkv, cap, 64, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError):
+        ops.prefill_attention(q, 0, hkv, kc64, kc64.clone())
+    keys = torch.zeros(b, dtype=torch.int64, device=gpu)
+    with pytest.raises(ValueError):
+        ops.greedy_advance(keys, pos.float(), pos, None, torch.zeros(1, dtype=torch.int32, device=gpu))
+    with pytest.raises(ValueError):
+        ops.prompt_advance(torch.zeros(3, 5, dtype=torch.int32, device=gpu), pos, pos)

@@ -1,25 +1,107 @@
-"""The reference operator surface: constructor checks and argument order (CPU),
-and on the GPU that each operator gives the same bits as the functional layer."""
+"""The reference operator surface: construction with the reference's own call-site
+arguments and constructor checks (CPU), and on the GPU that each operator gives
+the same bits as the functional layer, and that a decode layer written as a
+runlist of ``(op, *buffer_names)`` entries gives the same bits as the layer."""
 
+import numpy as np
 import pytest
 import torch
 
 from oracle import w4a16 as ow
 from torch2iron_amd import formats, model as gm, operators as O, ops
+from torch2iron_amd import runlist as R
 
 BF16 = torch.bfloat16
 
+# quantized_qwen3/batch_decode_fused.py:46-52, 74-77 (NPU tiling constants of the batch decoder)
+COLUMNS, TILE_M, TILE_K, TILE_N, LM_TILE_N = 8, 8, 128, 64, 64
+
+
+def _gemm_tile_m(rows):
+    return 4 if rows <= 8 else TILE_M
+
+
+def _n_shard_rows(n, tile_n):
+    groups = n // (tile_n * COLUMNS)
+    return next(r for r in (4, 3, 2, 1) if groups % r == 0)
+
+
+@pytest.mark.parametrize("rows", [4, 8, 16, 32])
+def test_batch_decode_builder_call_sites_construct(rows):
+    """Every W4A16 operator exactly as ``batch_decode_fused.py:170-266`` builds it
+    for Qwen3-0.6B (emb 1024, attn 2048, kv 1024, ffn 3072, padded lm_head 152064)."""
+    tm = _gemm_tile_m(rows)
+    common = dict(num_aie_columns=COLUMNS, num_aie_rows=rows // tm, tile_m=tm, tile_k=TILE_K, tile_n=TILE_N,
+                  context=object())
+    ops_ = [
+        O.W4A16GEMM(M=rows, K=1024, N=2048, **common),
+        O.W4A16KGroupGEMM(M=rows, K=1024, N=2048, k_group=4, **common),          # queries
+        O.W4A16PairedKGroupGEMM(M=rows, K=1024, N=1024, k_group=2, **common),    # keys / values
+        O.W4A16KGroupGEMM(M=rows, K=2048, N=1024, k_group=2, **common),          # attention output
+        O.W4A16PairedKGroupGEMM(M=rows, K=1024, N=3072, k_group=2, **common),    # gate / up
+        O.W4A16KGroupGEMM(M=rows, K=3072, N=1024, k_group=2, **common),          # down
+        O.W4A16NShardGEMM(M=rows, K=1024, N=152064, num_aie_columns=COLUMNS,
+                          num_aie_rows=_n_shard_rows(152064, LM_TILE_N), tile_m=tm, tile_k=TILE_K,
+                          tile_n=LM_TILE_N, context=object()),
+    ]
+    for op in ops_:
+        specs = op.get_arg_spec()
+        assert specs[0].shape == (rows, op.K) and specs[0].direction == "in"       # (A, W, C[, C1])
+        assert all(s.direction == "out" for s in specs[2:])
+
+
+def test_codegen_gemv_call_sites_construct():
+    """``W4A16GEMV`` exactly as the codegen factory ``_gemv`` builds it
+    (``export/templates/decode_fused.py.j2:93-110``, values of
+    ``generated/decode_fused.py:157-333`` for Qwen3-0.6B)."""
+    for m, k, tsi, tso in [(2048, 1024, 4, 64), (1024, 1024, 8, 128), (1024, 2048, 2, 128),
+                           (3072, 1024, 2, 384), (1024, 3072, 1, 128), (151936, 1024, 8, 128)]:
+        op = O.W4A16GEMV(M=m, K=k, num_aie_columns=8, tile_size_input=tsi, tile_size_output=tso,
+                         group_size=128, context=object())
+        w, x, y = op.get_arg_spec()
+        assert (w.direction, x.shape, y.shape) == ("in", (k,), (m,))               # (W, x, y)
+
+
+def test_q4nx_call_sites_construct():
+    """The Q4NX callables with the fields their smokes pass
+    (``fast_qwen3/qkv_operator_smoke.py:208``, ``up_gate_operator_smoke.py:178``,
+    ``o_projection_operator_smoke.py:127``, ``o_projection_residual_operator_smoke.py:139``)."""
+    qkv = O.Q4NXFusedQKVProjection(in_features=1024, output_patches=8, rms_norm_epsilon=1e-6, context=object())
+    assert [s.shape for s in qkv.get_arg_spec()] == [(1024,), (1024,), ("W4A16Weight", 1024, 1536), (1536,)]
+    ug = O.Q4NXFusedUpGateProjection(in_features=1024, output_patches=4, rms_norm_epsilon=1e-6)
+    assert ug.get_arg_spec()[3].shape == (4 * 2 * 64,)
+    lin = O.Q4NXFusedLinearProjection(in_features=2048, output_patches=8, context=object())
+    assert [s.direction for s in lin.get_arg_spec()] == ["in", "in", "out"]
+    res = O.Q4NXFusedLinearResidualProjection(in_features=2048, output_patches=8)
+    assert [s.shape for s in res.get_arg_spec()] == [(2048,), (512,), ("W4A16Weight", 2048, 512), (8, 64)]
+
 
 @pytest.mark.parametrize("ctor", [
+    # the reference's own checks
     lambda: O.W4A16GEMV(M=3072, K=1000),
+    lambda: O.W4A16GEMV(M=3072, K=1024, kernel_vector_size=16),
+    lambda: O.W4A16GEMV(M=3072, K=1024, tile_size_input=4, tile_size_output=6),
+    lambda: O.W4A16GEMM(M=12, K=1024, N=4096),                                    # M % (tile_m * rows)
+    lambda: O.W4A16GEMM(M=32, K=1024, N=4000),                                    # N % (tile_n * cols)
+    lambda: O.W4A16GEMM(M=32, K=1024, N=4096, tile_k=64),                         # tile_k != group_size
+    lambda: O.W4A16GEMM(M=36, K=1024, N=4096, tile_m=6, num_aie_rows=1),
+    lambda: O.W4A16GEMM(M=32, K=1024, N=4096, tile_n=24),
+    lambda: O.W4A16KGroupGEMM(M=32, K=1024, N=4096, k_group=3),
+    lambda: O.W4A16PairedKGroupGEMM(M=32, K=640, N=3072),
+    lambda: O.W4A16NShardGEMM(M=8, K=1024, N=151936, num_aie_rows=3),
+    lambda: O.Q4NXFusedQKVProjection(in_features=1152),
+    lambda: O.Q4NXFusedQKVProjection(in_features=1024, out_rows=32),
+    lambda: O.Q4NXFusedUpGateProjection(in_features=1024, output_patches=9),
+    lambda: O.Q4NXFusedUpGateProjection(in_features=1024, rms_norm_epsilon=0.0),
+    lambda: O.Q4NXFusedLinearProjection(in_features=3072),                        # at most 2048 K
+    lambda: O.Q4NXFusedLinearResidualProjection(in_features=2048, output_patches=0),
+    # the GPU kernels' limits
+    lambda: O.W4A16GEMV(M=3000, K=1024),
     lambda: O.W4A16GEMV(M=3072, K=1024, group_size=64),
-    lambda: O.W4A16GEMM(M=0, K=1024, N=4096),
-    lambda: O.W4A16GEMM(M=16, K=1024, N=4000),
-    lambda: O.W4A16KGroupGEMM(M=16, K=1024, N=4096, k_group=3),
-    lambda: O.W4A16PairedKGroupGEMM(M=16, K=640, N=3072),
     lambda: O.Qwen3FusedQKVProjection(in_features=1000, out_features=4096),
     lambda: O.Qwen3FusedUpGateProjection(in_features=1024, out_features=3072, rms_norm_epsilon=0.0),
     lambda: O.Qwen3FusedLinearResidualProjection(in_features=2048, out_features=1000),
+    lambda: O.Qwen3DecodeAttention(n_heads=16, n_kv_heads=6),
 ])
 def test_constructor_checks_raise_value_error(ctor):
     with pytest.raises(ValueError):
@@ -29,19 +111,49 @@ def test_constructor_checks_raise_value_error(ctor):
 def test_argument_order_matches_the_reference():
     gemv = O.W4A16GEMV(M=3072, K=1024).get_arg_spec()
     assert [a.direction for a in gemv] == ["in", "in", "out"] and gemv[1].shape == (1024,)   # (W, x, y)
-    gemm = O.W4A16GEMM(M=16, K=1024, N=4096).get_arg_spec()
-    assert gemm[0].shape == (16, 1024) and gemm[2].shape == (16, 4096)                       # (A, W, C)
-    paired = O.W4A16PairedKGroupGEMM(M=8, K=1024, N=3072).get_arg_spec()
+    batched = O.W4A16GEMV(M=3072, K=1024, num_batches=4, shared_qparam=True).get_arg_spec()
+    assert batched[1].shape == (4, 1024) and batched[2].shape == (4, 3072)
+    gemm = O.W4A16GEMM(M=32, K=1024, N=4096).get_arg_spec()
+    assert gemm[0].shape == (32, 1024) and gemm[2].shape == (32, 4096)                       # (A, W, C)
+    paired = O.W4A16PairedKGroupGEMM(M=8, K=1024, N=3072, tile_m=4, num_aie_rows=2).get_arg_spec()
     assert [a.direction for a in paired] == ["in", "in", "out", "out"]                        # (A, W, C0, C1)
     res = O.Qwen3FusedLinearResidualProjection(2048, 1024, rows=8).get_arg_spec()
     assert res[0].shape == (8, 2048) and res[1].shape == (8, 1024)                            # (ctx, residual, W, out)
 
 
 def test_weight_buffer_is_checked():
-    op = O.W4A16GEMM(M=4, K=256, N=64)
+    op = O.W4A16GEMM(M=4, K=256, N=512, tile_m=4, num_aie_rows=1)
     w = formats.W4A16Weight.from_numpy(*ow.synthetic_tensors(256, 128, seed=1))
     with pytest.raises(ValueError):
-        op(torch.zeros(4, 256, dtype=BF16), w, torch.zeros(4, 64, dtype=BF16))
+        op(torch.zeros(4, 256, dtype=BF16), w, torch.zeros(4, 512, dtype=BF16))
+
+
+def test_q4nx_patch_weight_is_a_column_permutation():
+    """Column (p * 3 + j) * 64 + r of the patch weight is row (first + p) * 64 + r of
+    projection j, exactly (the dequantised columns are equal)."""
+    parts = [ow.synthetic_tensors(256, n, seed=s) for s, n in ((1, 512), (2, 256), (3, 256))]
+    w = formats.q4nx_patch_weight(*parts, output_patches=2, first_patch=1)
+    dense = ow.dequantize(*w)
+    ref = [ow.dequantize(*p) for p in parts]
+    for p in range(2):
+        for j in range(3):
+            got = dense[(p * 3 + j) * 64:(p * 3 + j + 1) * 64]
+            assert np.array_equal(got, ref[j][(1 + p) * 64:(2 + p) * 64])
+    with pytest.raises(ValueError):
+        formats.q4nx_patch_weight(*parts, output_patches=5)
+
+
+def test_runlist_checks_entries_against_arg_specs():
+    cfg = gm.Qwen3Config(n_layers=1)
+    rl = R.qwen3_decode_runlist(cfg, rows=4, ctx_cap=64)
+    assert len(rl) == 5 and all(len(bufs) == len(op.get_arg_spec()) for op, *bufs in rl)
+    op, *bufs = rl[2]
+    with pytest.raises(ValueError, match="Number of buffers"):
+        R.FusedRunlist("bad", [(op, *bufs[:-1])], [], [], {}, "cpu")
+    with pytest.raises(TypeError):
+        R.FusedRunlist("bad", [(op, 1, 2, 3, 4)], [], [], {}, "cpu")
+    with pytest.raises(ValueError, match="weight buffer"):
+        R.FusedRunlist("bad", [rl[2]], [], [], {}, "cpu")
 
 
 @pytest.mark.gpu
@@ -50,16 +162,16 @@ def test_operators_match_functional_layer(gpu):
     w = formats.W4A16Weight.from_numpy(*ow.synthetic_tensors(1024, 3072, seed=2), device=gpu)
     x = torch.randn(1024, generator=g).to(BF16).to(gpu)
     y = torch.empty(3072, dtype=BF16, device=gpu)
-    O.W4A16GEMV(M=3072, K=1024)(w, x, y)
+    O.W4A16GEMV(M=3072, K=1024, num_aie_columns=8, tile_size_input=2, tile_size_output=384)(w, x, y)
     assert torch.equal(y, ops.linear(x, w))
     a = torch.randn(16, 1024, generator=g).to(BF16).to(gpu)
     c = torch.empty(16, 3072, dtype=BF16, device=gpu)
-    O.W4A16KGroupGEMM(M=16, K=1024, N=3072, k_group=4)(a, w, c)
+    O.W4A16KGroupGEMM(M=16, K=1024, N=3072, num_aie_rows=2, k_group=4)(a, w, c)
     assert torch.equal(c, ops.linear(a, w))
     gate, up = ow.synthetic_tensors(1024, 3072, seed=3), ow.synthetic_tensors(1024, 3072, seed=4)
     wp = formats.W4A16Weight.from_numpy(*formats.interleave_gate_up(gate, up), device=gpu)
     c0, c1 = torch.empty_like(c), torch.empty_like(c)
-    O.W4A16PairedKGroupGEMM(M=16, K=1024, N=3072)(a, wp, c0, c1)
+    O.W4A16PairedKGroupGEMM(M=16, K=1024, N=3072, num_aie_rows=2)(a, wp, c0, c1)
     r0, r1 = ops.gate_up(a, wp, swiglu=False)
     assert torch.equal(c0, r0) and torch.equal(c1, r1)
     nw = torch.ones(1024, dtype=BF16, device=gpu)
@@ -71,3 +183,78 @@ def test_operators_match_functional_layer(gpu):
     out = torch.empty_like(res)
     O.Qwen3FusedLinearResidualProjection(3072, 1024, rows=16)(h, res, wo, out)
     assert torch.equal(out, ops.linear(h, wo, residual=res))
+    # several vectors, one weight each (num_batches, not shared)
+    ws = [formats.W4A16Weight.from_numpy(*ow.synthetic_tensors(1024, 3072, seed=10 + i), device=gpu) for i in range(3)]
+    xb = torch.randn(3, 1024, generator=g).to(BF16).to(gpu)
+    yb = torch.empty(3, 3072, dtype=BF16, device=gpu)
+    O.W4A16GEMV(M=3072, K=1024, num_batches=3)(ws, xb, yb)
+    for i in range(3):
+        assert torch.equal(yb[i], ops.linear(xb[i], ws[i]))
+
+
+@pytest.mark.gpu
+def test_q4nx_operators_match_the_patch_reference(gpu):
+    """The Q4NX callables against the oracle: out[p][j][r] = projection j row 64 (first + p) + r
+    of the RMSNorm'd hidden vector (qkv: q, k, v; up/gate: up, gate), and the plain and
+    residual o-projections, with patch-ordered AutoGPTQ weights."""
+    g = torch.Generator().manual_seed(5)
+    k = 1024
+    parts = [ow.synthetic_tensors(k, 1024, seed=20 + j) for j in range(3)]
+    hidden = torch.randn(k, generator=g).to(BF16)
+    nw = (torch.rand(k, generator=g) * 0.2 + 0.9).to(BF16)
+    from oracle import qwen3 as oq
+    xn = oq.rmsnorm(hidden.float(), nw.float(), 1e-6, oq._Round("bf16"))
+    for cls, nproj in ((O.Q4NXFusedQKVProjection, 3), (O.Q4NXFusedUpGateProjection, 2)):
+        op = cls(in_features=k, output_patches=4, rms_norm_epsilon=1e-6)
+        wt = formats.q4nx_patch_weight(*parts[:nproj], output_patches=4, first_patch=2)
+        out = torch.empty(op.get_arg_spec()[3].shape, dtype=BF16, device=gpu)
+        op(hidden.to(gpu), nw.to(gpu), formats.W4A16Weight.from_numpy(*wt, device=gpu), out)
+        got = out.float().cpu().view(4, nproj, 64)
+        ref = torch.from_numpy(ow.linear(xn.numpy()[None], *wt)).view(4, nproj, 64)
+        err = (got - ref).abs().max() / ref.abs().max()
+        assert err < 1e-2, (cls.__name__, float(err))
+    wo = ow.synthetic_tensors(2048, 512, seed=30)
+    ctx = torch.randn(2048, generator=g).to(BF16)
+    resid = torch.randn(512, generator=g).to(BF16)
+    ref = torch.from_numpy(ow.linear(ctx.float().numpy()[None], *wo)).view(-1)
+    lin = O.Q4NXFusedLinearProjection(in_features=2048, output_patches=8)
+    out = torch.empty(512, dtype=BF16, device=gpu)
+    lin(ctx.to(gpu), formats.W4A16Weight.from_numpy(*wo, device=gpu), out)
+    assert ((out.float().cpu() - ref).abs().max() / ref.abs().max()) < 1e-2
+    rop = O.Q4NXFusedLinearResidualProjection(in_features=2048, output_patches=8)
+    out2 = torch.empty(8, 64, dtype=BF16, device=gpu)
+    rop(ctx.to(gpu), resid.to(gpu), formats.W4A16Weight.from_numpy(*wo, device=gpu), out2)
+    assert torch.equal(out2.view(-1), (out.float() + resid.to(gpu).float()).to(BF16))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("layers", [1, 2])
+def test_runlist_layer_matches_decode_layer(gpu, layers):
+    """A decode step's layers written as the reference's ``(op, *buffer_names)``
+    runlist (``batch_decode_fused.py:426-539`` form) give the same bits as
+    ``Qwen3DecodeLayer``: residual stream and both KV caches."""
+    cfg = gm.Qwen3Config(n_layers=layers, vocab=512)
+    t = gm.random_qwen3_tensors(cfg, seed=41, weights="centered")
+    b, cap = 6, 96
+    m1 = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu)
+    m2 = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu)
+    g = torch.Generator().manual_seed(42)
+    x0 = torch.randn(b, cfg.hidden, generator=g).to(BF16).to(gpu)
+    kc = torch.randn(m1.k_cache.shape, generator=g).to(BF16).to(gpu)
+    vc = torch.randn(m1.v_cache.shape, generator=g).to(BF16).to(gpu)
+    pos = torch.tensor([0, 5, 17, 40, 90, 95], dtype=torch.int32, device=gpu)
+    for m in (m1, m2):
+        m.x.copy_(x0)
+        m.k_cache.copy_(kc)
+        m.v_cache.copy_(vc)
+        m.positions.copy_(pos)
+    buf = m1.micro[0].buf
+    for i, layer in enumerate(m1.layers):
+        layer(buf, m1.positions, m1.k_cache[i], m1.v_cache[i])
+    fused = R.FusedRunlist("qwen3_decode_layers", R.qwen3_decode_runlist(cfg, rows=b, ctx_cap=cap),
+                           ["x", "positions"], ["x"], R.qwen3_decode_buffers(m2), gpu)
+    fused()
+    torch.cuda.synchronize()
+    assert torch.equal(m2.x, m1.x)
+    assert torch.equal(m2.k_cache, m1.k_cache) and torch.equal(m2.v_cache, m1.v_cache)
+    assert torch.equal(fused.get_buffer("x"), m1.x)

@@ -896,7 +896,8 @@ Plan plan_linear(int M, int K, int N, bool paired) {
   pl.MT = 1;
   pl.CK = 4;
   const int mz = (M + 15) / 16;
-  if ((N / 16) * mz <= 256 && !paired) {
+  if (((N / 16) * mz <= 256 || N % 32) && !paired) {
+    // (N not a multiple of 32: 16-column blocks are the only whole ones)
     pl.LW = 1; pl.W = 16; pl.CK = 2;
   } else if ((N / 32) * mz <= 256 || N % 64) {
     pl.LW = 2; pl.W = 8;
@@ -950,7 +951,7 @@ int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
   if (!qweight || !qzeros || !scales) return fail(T2I_ERR_NULL, "qweight/qzeros/scales must not be NULL");
   if (group_size != GS) return fail(T2I_ERR_GROUP, "group_size %d unsupported (only 128)", group_size);
   if (K <= 0 || K % GS) return fail(T2I_ERR_SHAPE, "K=%d must be a positive multiple of 128", K);
-  if (N <= 0 || N % 64) return fail(T2I_ERR_SHAPE, "N=%d must be a positive multiple of 64", N);
+  if (N <= 0 || N % 16) return fail(T2I_ERR_SHAPE, "N=%d must be a positive multiple of 16", N);
   if (!aligned16(qweight) || !aligned16(scales)) return fail(T2I_ERR_ALIGN, "qweight/scales must be 16-byte aligned");
   if (((uintptr_t)qzeros & 3u) != 0) return fail(T2I_ERR_ALIGN, "qzeros must be 4-byte aligned");
   return T2I_OK;
@@ -973,6 +974,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
   }
   const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
+  if (paired && N % 32) return fail(T2I_ERR_SHAPE, "paired N=%d must be a multiple of 32", N);
   if (!gamma && M >= gemm_min_rows() && N % GM_BN == 0) {
     // prompt-sized: the LDS-tiled GEMM
     LinearParams p{};

@@ -131,6 +131,27 @@ def interleave_gate_up(gate, up):
     return _permute_columns(*cat, gate_up_permutation(inter))
 
 
+def q4nx_patch_weight(*parts, output_patches: int, first_patch: int = 0, patch_rows: int = 64):
+    """The columns a Q4NX fused projection reads, as one AutoGPTQ linear (numpy triple).
+
+    ``parts`` are the projections whose patches the operator interleaves (q, k, v
+    for the fused qkv, up, gate for the up/gate projection).  New column
+    ``(p * len(parts) + j) * patch_rows + r`` is row ``(first_patch + p) * patch_rows + r``
+    of projection ``j``: the ``[patch][projection][row]`` output order of the
+    Q4NX operators (``q4nx_fused_qkv_projection/op.py:128-136``).  Exact (a
+    column permutation at the nibble level).
+    """
+    if output_patches < 1 or not parts:
+        raise ValueError("need at least one projection and one patch")
+    widths = [int(np.asarray(p[0]).shape[1]) for p in parts]
+    if any(w < (first_patch + output_patches) * patch_rows for w in widths):
+        raise ValueError("a projection has fewer rows than the requested patches")
+    offsets = np.cumsum([0] + widths[:-1])
+    perm = [offsets[j] + (first_patch + p) * patch_rows + r
+            for p in range(output_patches) for j in range(len(parts)) for r in range(patch_rows)]
+    return _permute_columns(*concat_columns(*parts), np.asarray(perm, dtype=np.int64))
+
+
 def random_weight_on_device(K: int, N: int, generator: torch.Generator, device) -> W4A16Weight:
     """Seeded random AutoGPTQ weight drawn directly on the device (benchmarks).
 

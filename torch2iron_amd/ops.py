@@ -117,10 +117,14 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
     if out is None:
         out = torch.empty(m, inter, dtype=BF16, device=x.device)
     _check_dev("out", out, BF16)
+    if out.numel() != m * inter:
+        raise ValueError(f"out must hold {m}x{inter} elements")
     if not swiglu:
         if out_up is None:
             out_up = torch.empty(m, inter, dtype=BF16, device=x.device)
         _check_dev("out_up", out_up, BF16)
+        if out_up.numel() != m * inter:
+            raise ValueError(f"out_up must hold {m}x{inter} elements")
     lib = _lib.load()
     rc = lib.t2i_w4a16_gate_up(x2.data_ptr(), m, w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
                                w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)),
@@ -174,6 +178,8 @@ def rmsnorm_gate_up(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_pa
         if out_up is None:
             out_up = torch.empty(m, inter, dtype=BF16, device=x.device)
         _check_dev("out_up", out_up, BF16)
+        if out_up.numel() != m * inter:
+            raise ValueError(f"out_up must hold {m}x{inter} elements")
     lib = _lib.load()
     rc = lib.t2i_w4a16_rmsnorm_gate_up(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps),
                                        w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(), w_pair.scales.data_ptr(),
@@ -199,16 +205,25 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor
     if tokens is not None:
         _check_dev("tokens", tokens, torch.int32)
         m = tokens.numel()
+        if x.dim() != 2:
+            raise ValueError("with tokens, x must be a [V, H] table")
         if x_out is None:
             raise ValueError("x_out is required with tokens")
-        _check_dev("x_out", x_out, BF16)
     else:
         m = x.numel() // h
+    if x_out is not None:
+        _check_dev("x_out", x_out, BF16)
+        if x_out.numel() != m * h:
+            raise ValueError(f"x_out must hold {m}x{h} elements")
     if out is None:
         out = torch.empty(m, h, dtype=BF16, device=x.device)
     _check_dev("out", out, BF16)
+    if out.numel() != m * h:
+        raise ValueError(f"out must hold {m}x{h} elements")
     if argmax_keys is not None:
         _check_dev("argmax_keys", argmax_keys, torch.int64)
+        if argmax_keys.numel() < m:
+            raise ValueError(f"argmax_keys must hold at least {m} entries")
     lib = _lib.load()
     rc = lib.t2i_rmsnorm(x.data_ptr(), _lib.ptr(tokens), x.shape[0] if tokens is not None else 0, m, h,
                          weight.data_ptr(), float(eps), _lib.ptr(x_out),
@@ -233,6 +248,8 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n
         _check_dev(n, t, BF16)
     b = positions.numel()
     d = q_norm.numel()
+    if k_norm.numel() != d:
+        raise ValueError("q_norm and k_norm must both hold head_dim values")
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise ValueError("k_cache and v_cache must be [B, Hkv, ctx_cap, D] of equal shape")
     if tuple(k_cache.shape[:2]) != (b, n_kv_heads) or k_cache.shape[3] != d:
@@ -245,6 +262,8 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n
     if out is None:
         out = torch.empty(b, n_heads * d, dtype=BF16, device=qkv.device)
     _check_dev("out", out, BF16)
+    if out.numel() != b * n_heads * d:
+        raise ValueError(f"out must hold {b}x{n_heads * d} elements")
     lib = _lib.load()
     nbytes = lib.t2i_decode_attention_workspace_bytes(b, n_heads, n_kv_heads, ctx_cap)
     ws = (workspace or DEFAULT_WORKSPACE).get(("attn", b, n_kv_heads, ctx_cap), nbytes, qkv.device)
@@ -269,11 +288,16 @@ def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_k
     for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
         _check_dev(n, t, BF16)
     d = q_norm.numel()
+    if k_norm.numel() != d:
+        raise ValueError("q_norm and k_norm must both hold head_dim values")
+    if batch < 1:
+        raise ValueError("batch must be positive")
     rows = qkv.numel() // ((n_heads + 2 * n_kv_heads) * d)
     if rows % batch or rows * (n_heads + 2 * n_kv_heads) * d != qkv.numel():
         raise ValueError("qkv must be [B * T, (Hq + 2 Hkv) * D]")
     t = rows // batch
-    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (batch, n_kv_heads):
+    if (k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (batch, n_kv_heads)
+            or k_cache.shape[3] != d):
         raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
     ctx_cap = k_cache.shape[2]
     if rope.shape[0] < p0 + t:
@@ -299,8 +323,11 @@ def prefill_attention(q: torch.Tensor, p0: int, n_kv_heads: int, k_cache: torch.
     _check_dev("q", q, BF16)
     _check_dev("k_cache", k_cache, BF16)
     _check_dev("v_cache", v_cache, BF16)
+    if q.dim() != 4:
+        raise ValueError("q must be [B, Hq, T, D]")
     b, hq, t, d = q.shape
-    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (b, n_kv_heads):
+    if (k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (b, n_kv_heads)
+            or k_cache.shape[3] != d):
         raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
     if out is None:
         out = torch.empty(b * t, hq * d, dtype=BF16, device=q.device)
@@ -321,10 +348,14 @@ def lm_head_argmax(h: torch.Tensor, embed: torch.Tensor, keys: torch.Tensor,
     _check_dev("h", h, BF16)
     _check_dev("embed", embed, BF16)
     _check_dev("keys", keys, torch.int64)
+    if h.dim() != 2 or embed.dim() != 2:
+        raise ValueError("h must be [M, K] and embed [V, K]")
     m, k = h.shape
     v = embed.shape[0]
     if embed.shape[1] != k:
         raise ValueError("embed must be [V, K] with K = h.shape[1]")
+    if keys.numel() < m:
+        raise ValueError(f"keys must hold at least {m} entries")
     if logits is not None:
         _check_dev("logits", logits, torch.float32)
         if logits.numel() != m * v:
@@ -345,8 +376,18 @@ def keys_to_tokens(keys: torch.Tensor) -> torch.Tensor:
 def greedy_advance(keys, tokens, positions, history, step):
     """Device-side greedy bookkeeping between captured decode steps (``history`` may
     be None: no token record)."""
-    lib = _lib.load()
+    _check_dev("keys", keys, torch.int64)
+    _check_dev("tokens", tokens, torch.int32)
+    _check_dev("positions", positions, torch.int32)
+    _check_dev("step", step, torch.int32)
     b = tokens.numel()
+    if keys.numel() < b or positions.numel() != b or step.numel() < 1:
+        raise ValueError("keys, tokens and positions must hold one entry per sequence; step one")
+    if history is not None:
+        _check_dev("history", history, torch.int32)
+        if history.dim() != 2 or history.shape[0] != b:
+            raise ValueError("history must be [B, hist_cap]")
+    lib = _lib.load()
     rc = lib.t2i_greedy_advance(keys.data_ptr(), b, tokens.data_ptr(), positions.data_ptr(),
                                 history.data_ptr() if history is not None else None,
                                 history.shape[1] if history is not None else 0, step.data_ptr(),
@@ -356,6 +397,11 @@ def greedy_advance(keys, tokens, positions, history, step):
 
 def prompt_advance(prompt, tokens, positions):
     """Teacher-forced prompt bookkeeping (``prompt`` int32 ``[B, P]``)."""
+    _check_dev("prompt", prompt, torch.int32)
+    _check_dev("tokens", tokens, torch.int32)
+    _check_dev("positions", positions, torch.int32)
+    if prompt.dim() != 2 or tokens.numel() != prompt.shape[0] or positions.numel() != prompt.shape[0]:
+        raise ValueError("prompt must be [B, P] with one token and position per sequence")
     lib = _lib.load()
     b, plen = prompt.shape
     rc = lib.t2i_prompt_advance(prompt.data_ptr(), b, plen, tokens.data_ptr(), positions.data_ptr(),
