@@ -145,6 +145,23 @@ int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t 
                          uint16_t* ctx, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Allocation-free variant of t2i_decode_attention.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The chunk states live in a library-held scratch array of
+ * T2I_DECODE_ATTENTION_SCRATCH_BYTES per device (held until the process ends):
+ * at most 8192 (sequence, kv head) pairs and 16 MiB minus 32 KiB of chunk
+ * states, else T2I_ERR_WORKSPACE.  Arguments and results as
+ * t2i_decode_attention.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap in time on one GPU (different streams) race. */
+#define T2I_DECODE_ATTENTION_SCRATCH_BYTES ((size_t)16 << 20)
+int t2i_decode_attention_noalloc(const uint16_t* qkv, const int32_t* positions, int32_t B,
+                                 int32_t Hq, int32_t Hkv, int32_t D,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                 const uint16_t* rope, int32_t rope_style,
+                                 uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
+                                 uint16_t* ctx, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Prompt (prefill) attention, every prompt row of B sequences at once.  Rows of
  * qkv are b * T + t for prompt token t of sequence b at position p0 + t.

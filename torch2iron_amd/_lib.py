@@ -43,6 +43,9 @@ SIGNATURES = {
     "t2i_decode_attention": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                        c_float, c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p,
                                        c_size_t, c_void_p]),
+    "t2i_decode_attention_noalloc": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
+                                               c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p, c_int32,
+                                               c_void_p, c_void_p]),
     "t2i_prefill_qk_rope_kv": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                                          c_void_p, c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p,
                                          c_void_p, c_int32, c_void_p]),

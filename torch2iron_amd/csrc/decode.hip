@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
 
 #include "t2i_common.h"
 
@@ -95,6 +96,11 @@ constexpr int ATT_THREADS = 256;
 // lanes, one slot per group and pass).  Fewer rows for more q heads per kv
 // head keeps the per-lane score and accumulator registers bounded.
 constexpr int att_rows(int q) { return q <= 2 ? 8 : (q == 4 ? 4 : 2); }
+
+// Chunk-state scratch of t2i_decode_attention_noalloc: one copy per device,
+// zero-initialised at load (16 MiB).  Host code never passes this name to a
+// kernel; it takes the copy's device address from hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[(size_t)16 << 20] = {};
 
 struct AttnParams {
   const uint16_t* qkv;
@@ -741,6 +747,40 @@ int run_attention(const AttnPlan& pl, const uint16_t* qkv, const int32_t* positi
   return t2i_host::hip_status(e, "attention launch");
 }
 
+// ---- library-held chunk-state scratch (the allocation-free entry point) ----
+// Fixed layout, whatever the call's shape: the arrival counters of up to
+// ATT_SCRATCH_UNITS (sequence, kv head) pairs first, then the chunk states.  The
+// array is zero-initialised when the code object is loaded, and every call
+// leaves the counters it used at zero again, so the counters start at zero for
+// every call; a counter word never holds anything else.
+constexpr int ATT_SCRATCH_UNITS = 8192;
+constexpr size_t ATT_SCRATCH_COUNTERS = ATT_SCRATCH_UNITS * sizeof(unsigned);
+constexpr size_t ATT_SCRATCH_BYTES = (size_t)16 << 20;   // T2I_DECODE_ATTENTION_SCRATCH_BYTES
+constexpr int ATT_MAX_DEVICES = 64;
+static_assert(ATT_SCRATCH_BYTES == T2I_DECODE_ATTENTION_SCRATCH_BYTES, "header and library agree");
+
+std::mutex g_scratch_mu;
+char* g_scratch_ptr[ATT_MAX_DEVICES];   // device address of `scratch` on each device, once known
+
+// The device address of the current device's copy of `scratch` (set up on the
+// first call on that device).  Host code uses only this address: the array's
+// own name on the host is a stand-in, not a device address.
+int scratch_for_current_device(char** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return t2i_host::hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= ATT_MAX_DEVICES) return fail(T2I_ERR_VALUE, "device %d beyond %d", dev, ATT_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(t2i::scratch));
+    if (e != hipSuccess) return t2i_host::hip_status(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(T2I_ERR_NULL, "scratch has no device address");
+    g_scratch_ptr[dev] = static_cast<char*>(ptr);
+  }
+  *out = g_scratch_ptr[dev];
+  return T2I_OK;
+}
 }  // namespace
 
 extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t B, int32_t Hq,
@@ -762,6 +802,31 @@ extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* position
                        ctx_cap, ctx, ws ? reinterpret_cast<unsigned*>(ws) : nullptr,
                        ws ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr,
                        ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr, stream);
+}
+
+extern "C" int t2i_decode_attention_noalloc(const uint16_t* qkv, const int32_t* positions, int32_t B, int32_t Hq,
+                                            int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
+                                            float eps, const uint16_t* rope, int32_t rope_style, uint16_t* k_cache,
+                                            uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx, void* stream) {
+  int rc = check_attention(qkv, positions, B, Hq, Hkv, D, q_norm, k_norm, eps, rope, rope_style, k_cache, v_cache,
+                           ctx_cap, ctx);
+  if (rc) return rc;
+  const AttnPlan pl = plan_attention(B, Hq, Hkv, ctx_cap);
+  const size_t units = (size_t)B * Hkv;
+  const size_t states = pl.bytes ? pl.bytes - pl.off_ml : 0;   // chunk states after the counters
+  if (pl.bytes && (units > ATT_SCRATCH_UNITS || states > ATT_SCRATCH_BYTES - ATT_SCRATCH_COUNTERS))
+    return fail(T2I_ERR_WORKSPACE, "B*Hkv=%zu (max %d) or %zu bytes of chunk states (max %zu) exceed the "
+                "library's scratch", units, ATT_SCRATCH_UNITS, states, ATT_SCRATCH_BYTES - ATT_SCRATCH_COUNTERS);
+  char* base = nullptr;
+  if (pl.bytes) {
+    rc = scratch_for_current_device(&base);
+    if (rc) return rc;
+  }
+  return run_attention(pl, qkv, positions, B, Hq, Hkv, D, q_norm, k_norm, eps, rope, rope_style, k_cache, v_cache,
+                       ctx_cap, ctx, base ? reinterpret_cast<unsigned*>(base) : nullptr,
+                       base ? reinterpret_cast<float*>(base + ATT_SCRATCH_COUNTERS) : nullptr,
+                       base ? reinterpret_cast<float*>(base + ATT_SCRATCH_COUNTERS + (pl.off_o - pl.off_ml)) : nullptr,
+                       stream);
 }
 
 extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,
