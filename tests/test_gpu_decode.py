@@ -103,6 +103,10 @@ def _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed):
     # batch 16: 5 chunks of 128 slots would give 640 workgroups, so 6 chunks of 107
     # (768 = 3 x 256); positions at and around the chunk boundaries
     (16, 16, 8, 640, [0, 105, 106, 107, 108, 213, 214, 320, 321, 427, 428, 533, 534, 535, 600, 639]),
+    # many (sequence, kv head) pairs; positions at 128-slot boundaries
+    (16, 16, 8, 1088, [1024] * 8 + [0, 127, 128, 255, 256, 383, 384, 1087]),
+    (128, 8, 8, 300, [(37 * i) % 300 for i in range(128)]),
+    (64, 4, 2, 520, [511, 512, 255, 256, 0, 519] + list(range(100, 158))),
 ])
 def test_decode_attention_matches_oracle(gpu, b, hq, hkv, ctx_cap, positions, style):
     out, ref, kd, vd, kref, vref, pos = _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed=b + hq)
@@ -121,14 +125,15 @@ def test_decode_attention_matches_oracle(gpu, b, hq, hkv, ctx_cap, positions, st
     assert torch.equal(kd.float().permute(0, 2, 1, 3)[mask], kref.permute(0, 2, 1, 3)[mask])
 
 
-def test_decode_attention_out_of_range_position_is_inert(gpu):
-    d, b, hq, hkv, cap = 128, 2, 16, 8, 128
+@pytest.mark.parametrize("b", [2, 16])
+def test_decode_attention_out_of_range_position_is_inert(gpu, b):
+    d, hq, hkv, cap = 128, 16, 8, 128
     qkv = torch.randn(b, (hq + 2 * hkv) * d).to(BF16).to(gpu)
     kc = torch.randn(b, hkv, cap, d).to(BF16).to(gpu)
     kc0 = kc.clone()
     vc = torch.randn(b, hkv, cap, d).to(BF16).to(gpu)
     ones = torch.ones(d, dtype=BF16, device=gpu)
-    pos = torch.tensor([cap, -1], dtype=torch.int32, device=gpu)
+    pos = torch.tensor([cap, -1] * (b // 2), dtype=torch.int32, device=gpu)
     out = ops.decode_attention(qkv, pos, hq, hkv, ones, ones, 1e-6, gm.rope_table(d, cap, 1e6, gpu), kc, vc)
     assert torch.count_nonzero(out).item() == 0
     assert torch.equal(kc, kc0)

@@ -221,14 +221,16 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
     const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
     const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
     __builtin_amdgcn_sched_barrier(0);   // the RoPE row ahead of the K / V rows
-    // slots past the chunk's end reload its first slot; masked when scored
+    // slots past the chunk's end reload its first slot; masked when scored.  The
+    // K/V stream is read once per step: non-temporal loads (measured 12.8 -> 12.1 us
+    // per call at batch 16, context 577, decode step 889 -> 870 us with the lm_head's)
     u32x4 kreg[ROWS], vreg[ROWS];
 #pragma unroll
     for (int it = 0; it < ROWS; ++it) {
       const int t = t0 + it * 16 + grp;
       const int tl = t < t1 ? t : t0;
-      kreg[it] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)tl * D + 8 * c);
-      vreg[it] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)tl * D + 8 * c);
+      kreg[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)tl * D + 8 * c));
+      vreg[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)tl * D + 8 * c));
     }
 
     // ---- q heads and the current k: per-head RMSNorm then RoPE; v as is ----
@@ -479,15 +481,16 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
   // Double-buffered over 64-deep k slices: the next slice's rows are in flight
   // while the current one is multiplied.  A tile past the workgroup's range
   // reloads the wave's first tile, or the workgroup's, rows that are loaded
-  // anyway (an unconditional load; its results are dropped).
+  // anyway (an unconditional load; its results are dropped).  The table is read
+  // once per step: non-temporal loads.
   const int nfirst = min(n0, (te - 1) * 16);
   auto load_slice = [&](int k0, u32x4 (&bv)[LMH_TILES][2]) {
 #pragma unroll
     for (int t = 0; t < LMH_TILES; ++t) {
       const int row = (tile_ok[t] ? n0 + 16 * t : nfirst) + c;
       const uint16_t* src = E + (size_t)row * K + k0 + 16 * r;
-      bv[t][0] = *reinterpret_cast<const u32x4*>(src);
-      bv[t][1] = *reinterpret_cast<const u32x4*>(src + 8);
+      bv[t][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
+      bv[t][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 8));
     }
   };
   auto mul_slice = [&](int k0, const u32x4 (&bv)[LMH_TILES][2]) {
@@ -732,8 +735,8 @@ int run_attention(const AttnPlan& pl, const uint16_t* qkv, const int32_t* positi
   p.eps = eps;
   p.scale = (float)(1.0 / sqrt((double)D));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(B * Hkv, pl.splits);
   hipError_t e;
+  const dim3 grid(B * Hkv, pl.splits);
   switch (Q * 100 + pl.rows) {
     case 104: e = launch_attention<1, 4>(p, grid, s); break;
     case 108: e = launch_attention<1, 8>(p, grid, s); break;

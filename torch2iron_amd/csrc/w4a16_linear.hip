@@ -260,6 +260,27 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
   }
 }
 
+// NC chunks of a wave in a straight line: every chunk's loads are in flight
+// before the first is computed (the first, A, was issued by the caller), and
+// each computation waits for its own chunk only: one memory round trip for the
+// whole K slice of the wave.  Up to 6 chunks of 2 k-steps without the fused
+// norm (12 registers a chunk at one word per lane), 3 otherwise.
+template <int MT, int LW, int CK, bool NORM, int NC>
+__device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_begin, int ncol, int c, int r, int mbase,
+                                                Chunk<MT, LW, CK>& A, float (&total)[MT][LW][4], float& ss,
+                                                int zshift) {
+  if constexpr (NC == 1) {
+    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+  } else {
+    Chunk<MT, LW, CK> rest[NC - 1];
+#pragma unroll
+    for (int i = 1; i < NC; ++i) load_chunk<MT, LW, CK, NORM>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
+    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+#pragma unroll
+    for (int i = 1; i < NC; ++i) compute_chunk<MT, LW, CK, NORM>(rest[i - 1], total, ss, zshift);
+  }
+}
+
 // Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32
 // sums v; res holds the row's residual values (bf16 pairs), fetched at the start.
 template <int LW>
@@ -374,7 +395,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   float ss = 0.0f;   // fused norm: this lane's share of its A row's sum of squares
 
   // every wave loads a first chunk (a wave without chunks reloads the last and computes nothing)
-  Chunk<MT, LW, CK> A, B, C;
+  Chunk<MT, LW, CK> A, B;
   load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
   // The residual values this wave stores (residual epilogue) are fetched now, so
   // the epilogue waits for nothing.  The load is unconditional: waves that store
@@ -387,27 +408,27 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   load_scales<LW>(!NORM && p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
                   ncol & 1);
   __builtin_amdgcn_sched_barrier(0);
-  // One word per lane: straight-line schedules for 1, 2 and 3 chunks per wave
-  // (every chunk of the wave in flight before the first is computed, each
-  // computation waiting for its own chunk only), else a double-buffered loop.
+  // One word per lane: straight-line schedules for up to 6 chunks per wave (3
+  // with the fused norm), else a double-buffered loop.
   // Wider tiles use the loop alone, which keeps their registers (occupancy) as
   // they were; their decode plans have one chunk per wave.
   const int n = c_end - c_begin;   // wave-uniform
   bool looped = true;
   if constexpr (LW == 1) {
+    constexpr bool DEEP = !NORM && CK == 2;   // 4..6 chunks in registers: 12 a chunk
     looped = false;
     if (n == 1) {
-      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
     } else if (n == 2) {
-      load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
-      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
     } else if (n == 3) {
-      load_chunk<MT, LW, CK, NORM>(p, c_begin + 1, ncol, c, r, mbase, B);
-      load_chunk<MT, LW, CK, NORM>(p, c_begin + 2, ncol, c, r, mbase, C);
-      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
-      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
-      compute_chunk<MT, LW, CK, NORM>(C, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 4) {
+      straight_chunks<MT, LW, CK, NORM, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 5) {
+      straight_chunks<MT, LW, CK, NORM, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 6) {
+      straight_chunks<MT, LW, CK, NORM, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
     } else {
       looped = true;
     }
