@@ -68,6 +68,8 @@ def parse():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true", help="only the headline sweep")
     ap.add_argument("--skip-decode", action="store_true", help="skip the decode layer / greedy decode runs")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the decode layer and greedy decode (for a kernel trace of the decode step; no headline)")
     ap.add_argument("--prompt", type=int, default=512)
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--batch", type=int, default=16)
@@ -190,7 +192,7 @@ def launch_floor(dev, launches: int, steps: int, warmup: int) -> float:
 # ---------------------------------------------------------------------------
 
 def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int, batch: int,
-                 streams=(1, 2)):
+                 streams=(1, 2), teacher_forced_leg: bool = True):
     """Config 3 (one fused decode layer, batch 8, 1024 cached tokens) and config 4
     (full Qwen3-0.6B, batch 16 greedy decode) on random-init weights."""
     import numpy as np
@@ -275,14 +277,17 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         log(f"decode ({model.n_streams} streams): {runs[s]['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step; "
             f"prefill {tm['prompt_ms']:.2f} ms; end to end {runs[s]['end_to_end_tokens_per_s']} tok/s")
     # the prompt consumed one position at a time through the decode step (the NPU runner's way)
-    model.set_streams(1)
-    tm = {}
-    tf = model.generate(prompt, new_tokens, timings=tm, prompt_mode="decode")
-    teacher_forced = {"prompt_ms": round(tm["prompt_ms"], 2),
-                      "end_to_end_tokens_per_s": round(batch * new_tokens / ((tm["prompt_ms"] + tm["decode_ms"]) * 1e-3), 1),
-                      "first_token_equal_to_prefill": bool(torch.equal(tf[:, 0], toks[:, 0])),
-                      "tokens_equal_to_prefill_run": bool(torch.equal(tf, toks))}
-    log(f"teacher-forced prompt: {tm['prompt_ms']:.1f} ms")
+    teacher_forced = None
+    if teacher_forced_leg:
+        model.set_streams(1)
+        tm = {}
+        tf = model.generate(prompt, new_tokens, timings=tm, prompt_mode="decode")
+        teacher_forced = {
+            "prompt_ms": round(tm["prompt_ms"], 2),
+            "end_to_end_tokens_per_s": round(batch * new_tokens / ((tm["prompt_ms"] + tm["decode_ms"]) * 1e-3), 1),
+            "first_token_equal_to_prefill": bool(torch.equal(tf[:, 0], toks[:, 0])),
+            "tokens_equal_to_prefill_run": bool(torch.equal(tf, toks))}
+        log(f"teacher-forced prompt: {tm['prompt_ms']:.1f} ms")
     # the fp32 oracle's first 32 tokens for this exact model and prompt (written offline by
     # tests/golden/make_qwen3_greedy_golden.py from the same seeds)
     oracle = {}
@@ -434,6 +439,12 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.decode_only:
+        decode, _, _ = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens, args.batch,
+                                    [int(v) for v in args.streams.split(",")], teacher_forced_leg=False)
+        print(json.dumps({"metric": METRIC, "value": None, "unit": "TB/s", "n_gpus": 1, "note": "decode only",
+                          **decode}), flush=True)
+        return
     ms = [1, 8, 16, 32, 64]
     log(f"building HBM-cold sweep (pool {args.pool_mb} MB)")
     cold = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1, eager=args.eager)

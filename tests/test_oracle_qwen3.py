@@ -143,3 +143,121 @@ def test_decoder_matches_transformers_qwen3(tied):
     ours = oq.DenseQwen3(t, ocfg, mode="fp32", ctx_cap=32).prefill(prompt)
     assert torch.allclose(ours, ref, rtol=1e-4, atol=1e-3 * ref.abs().max()), (ours - ref).abs().max()
     assert torch.equal(torch.argmax(ours, -1), torch.argmax(ref, -1))
+
+
+# ---- the bf16 mode against the same formulas run natively in torch.bfloat16 ----
+# ``quantized_qwen3/model.py`` with ``compute_dtype=torch.bfloat16`` keeps every
+# activation as a bf16 tensor; each torch op then rounds its result to bf16.  The
+# oracle's bf16 mode holds bf16 values in fp32 tensors and rounds explicitly; these
+# tests run the reference's formulas on bf16 tensors and require the same bits.
+
+BF = torch.bfloat16
+
+
+def _bf16_randn(*shape, seed=0, scale=1.0):
+    return (torch.randn(*shape, generator=torch.Generator().manual_seed(seed)) * scale).to(BF)
+
+
+@pytest.mark.parametrize("shape", [(4, 1024), (3, 16, 128), (2, 8, 128), (1, 2048)])
+def test_bf16_rmsnorm_matches_native_bfloat16(shape):
+    """``model.py:176-179``: variance in fp32, rsqrt cast to bf16, two bf16 products."""
+    x = _bf16_randn(*shape, seed=shape[-1], scale=3.0)
+    w = (torch.rand(shape[-1], generator=torch.Generator().manual_seed(7)) * 0.2 + 0.9).to(BF)
+    variance = x.to(torch.float32).pow(2).mean(dim=-1, keepdim=True)
+    native = (x * torch.rsqrt(variance + 1e-6).to(x.dtype)) * w
+    got = oq.rmsnorm(x.float(), w.float(), 1e-6, B16)
+    assert torch.equal(got.to(BF), native)
+
+
+def test_bf16_rope_interleaved_matches_native_bfloat16():
+    """``model.py:184-196``: x * cos + rotate_half(x) * sin, each product and the sum in bf16."""
+    d, n = 128, 40
+    ang = oq.rope_angles(d, 600, 1e6)
+    pos = torch.arange(0, 600, 15)[:n]
+    x = _bf16_randn(n, 16, d, seed=3)
+    a = ang[pos].to(BF)[:, None, :]                  # the bf16 table (model.py:421-425)
+    cos = a[..., ::2].repeat_interleave(2, dim=-1)
+    sin = a[..., 1::2].repeat_interleave(2, dim=-1)
+    rot = torch.stack((-x[..., 1::2], x[..., ::2]), dim=-1).flatten(-2)
+    native = x * cos + rot * sin
+    got = oq.apply_rope(x.float(), a.float(), "interleaved", B16)
+    assert torch.equal(got.to(BF), native)
+
+
+def test_bf16_rope_halves_matches_native_bfloat16():
+    """The (i, i + d/2) pairing of ``rms_norm_rope/kernel.cc:39-67``, written as the
+    same bf16 products and sum."""
+    d, n = 128, 40
+    ang = oq.rope_angles(d, 600, 1e6)
+    pos = torch.arange(0, 600, 15)[:n]
+    x = _bf16_randn(n, 8, d, seed=4)
+    a = ang[pos].to(BF)[:, None, :]
+    cos = torch.cat((a[..., ::2], a[..., ::2]), dim=-1)
+    sin = torch.cat((a[..., 1::2], a[..., 1::2]), dim=-1)
+    rot = torch.cat((-x[..., d // 2:], x[..., :d // 2]), dim=-1)
+    native = x * cos + rot * sin
+    got = oq.apply_rope(x.float(), a.float(), "halves", B16)
+    assert torch.equal(got.to(BF), native)
+
+
+def test_bf16_swiglu_and_residual_match_native_bfloat16():
+    """``model.py:215-216, 322-327``: silu(gate) * up and the residual adds, each op in bf16."""
+    g = _bf16_randn(6, 3072, seed=5, scale=4.0)
+    u = _bf16_randn(6, 3072, seed=6, scale=2.0)
+    native = torch.nn.functional.silu(g) * u
+    got = oq._bf(oq._bf(oq.silu(g.float())) * u.float())
+    assert torch.equal(got.to(BF), native)
+    r = _bf16_randn(6, 1024, seed=8, scale=30.0)
+    o = _bf16_randn(6, 1024, seed=9, scale=0.5)
+    assert torch.equal(oq._bf(r.float() + o.float()).to(BF), r + o)
+
+
+def test_bf16_layer_matches_native_bfloat16_layer():
+    """One decode-free layer pass (RMSNorm, projections, q/k-norm, RoPE, causal
+    attention, o_proj + residual, RMSNorm, SwiGLU MLP + residual) of the oracle's
+    bf16 mode against the same layer written natively in bf16 torch ops, with the
+    linears as fp32 matmuls of the exact weights cast back to bf16
+    (``model.py:133-146``) and fp32 softmax weights (the oracle's stated departure
+    from ``model.py:277``)."""
+    cfg = oq.Qwen3Config(hidden=256, n_heads=4, n_kv_heads=2, head_dim=128, intermediate=512, n_layers=1,
+                         vocab=64, rope_style="interleaved")
+    gcfg = gm.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__})
+    t = gm.random_qwen3_tensors(gcfg, seed=12, weights="centered")
+    layer = oq.DenseLayer(t, "model.layers.0", cfg)
+    b, n = 2, 9
+    x = _bf16_randn(b, n, cfg.hidden, seed=13)
+    ang = oq.rope_angles(cfg.head_dim, 64, cfg.rope_theta)
+    kc = torch.zeros(b, cfg.n_kv_heads, 64, cfg.head_dim)
+    vc = torch.zeros_like(kc)
+    got = layer.prefill(x.float(), kc, vc, ang, B16)
+
+    def lin(name, h):
+        return (h.float() @ layer.w[name].T).to(BF)
+
+    def norm(h, w):
+        var = h.float().pow(2).mean(dim=-1, keepdim=True)
+        return (h * torch.rsqrt(var + cfg.eps).to(BF)) * w.to(BF)
+
+    def rope(h):
+        a = ang[:n].to(BF)[None, None]
+        cos = a[..., ::2].repeat_interleave(2, dim=-1)
+        sin = a[..., 1::2].repeat_interleave(2, dim=-1)
+        rot = torch.stack((-h[..., 1::2], h[..., ::2]), dim=-1).flatten(-2)
+        return h * cos + rot * sin
+
+    xn = norm(x, layer.ln1)
+    q = lin("q_proj", xn).view(b, n, cfg.n_heads, cfg.head_dim).transpose(1, 2)
+    k = lin("k_proj", xn).view(b, n, cfg.n_kv_heads, cfg.head_dim).transpose(1, 2)
+    v = lin("v_proj", xn).view(b, n, cfg.n_kv_heads, cfg.head_dim).transpose(1, 2)
+    q = rope(norm(q, layer.q_norm))
+    k = rope(norm(k, layer.k_norm))
+    kk = k.float().repeat_interleave(2, dim=1)
+    vv = v.float().repeat_interleave(2, dim=1)
+    s = (q.float() @ kk.transpose(-2, -1)) * cfg.head_dim ** -0.5
+    s = s.masked_fill(~torch.ones(n, n, dtype=torch.bool).tril(), torch.finfo(torch.float32).min)
+    ctx = (torch.softmax(s, dim=-1) @ vv).to(BF).transpose(1, 2).reshape(b, n, -1)
+    h = x + lin("o_proj", ctx)
+    hn = norm(h, layer.ln2)
+    mlp = torch.nn.functional.silu(lin("gate_proj", hn)) * lin("up_proj", hn)
+    native = h + lin("down_proj", mlp)
+    assert torch.equal(got.to(BF), native)
