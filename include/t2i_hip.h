@@ -145,6 +145,35 @@ int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t 
                          uint16_t* ctx, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* ---------------------------------------------------------------------------
+ * The front of the decode layer in one cooperative launch: the input RMSNorm +
+ * fused q|k|v projection of t2i_w4a16_rmsnorm_linear (norm_weight != NULL; with
+ * NULL, x is taken as already normalised, as t2i_w4a16_linear), then the
+ * attention of t2i_decode_attention on those q, k, v rows (q/k RMSNorm, RoPE,
+ * KV-cache write at positions[b], GQA attention), ctx bf16 [B, Hq * D].  The
+ * projection's weight holds q, k, v columns (N = (Hq + 2 Hkv) * D); K is the
+ * hidden size.  The projection is bit-identical to the standalone call; the
+ * attention splits the context differently, so ctx may differ from
+ * t2i_decode_attention's by rounding.  1 <= B <= 16, Hq / Hkv in {1, 2}, D = 128,
+ * B * Hkv no more than the device's CUs.  One 16-wave workgroup per CU, all
+ * resident at once: launches of this call must not run concurrently with other
+ * work on the device.  The workspace (t2i_qkv_attention_workspace_bytes) must be
+ * zero-filled before its first use and not shared by calls that overlap in
+ * time; a wait inside the launch that times out sets the 32-bit word at
+ * t2i_qkv_attention_error_offset() of the workspace (zero otherwise).
+ * Replaces: the per-layer front of quantized_qwen3/batch_decode_fused.py:426-479
+ *           (RMSNorm, query and key/value GEMMs, RMSNormRoPE, CopyPresentPacketKV,
+ *           LlamaChunkedAttention), fast_qwen3/operators/qwen3_layer_fused/op.py:18-50.
+ */
+size_t t2i_qkv_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv);
+size_t t2i_qkv_attention_error_offset(int32_t B, int32_t Hq, int32_t Hkv);
+int t2i_qkv_attention(const uint16_t* x, int32_t B, const uint16_t* norm_weight, float eps,
+                      const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales, int32_t K,
+                      int32_t group_size, const int32_t* positions, int32_t Hq, int32_t Hkv, int32_t D,
+                      const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope, int32_t rope_style,
+                      uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free variant of t2i_decode_attention.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -89,7 +89,6 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
 // ============================================================================
 // GQA decode attention
 // ============================================================================
-constexpr int ATT_D = 128;
 constexpr int ATT_THREADS = 256;
 
 // Context slots per lane: a workgroup covers 16 * rows slots (16 groups of 16
@@ -119,16 +118,6 @@ struct AttnParams {
   float eps, scale;
 };
 
-__device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
-  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
-  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
-}
-
-// Scores are kept in log2 units (scaled by log2 e), so every exponential is a
-// single v_exp_f32.  2^(m - M) is the weight of a softmax state with running max m
-// under a new max M; an empty state (m = -inf) weighs nothing.
-__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-__device__ __forceinline__ float state_weight(float m, float M) { return m > -INFINITY ? exp2_fast(m - M) : 0.0f; }
 
 // One workgroup per (sequence b, kv head h, chunk of 16 * ROWS context slots).
 // A single workgroup per (b, h) streaming the whole context was measured 2-4x

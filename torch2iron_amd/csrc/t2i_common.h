@@ -38,6 +38,20 @@ __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }
 
+// ---- attention helpers ----
+constexpr int ATT_D = 128;   // head dimension of the attention kernels
+
+__device__ __forceinline__ void unpack8(u32x4 v, float (&f)[8]) {
+  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x); f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z); f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+}
+
+// Scores are kept in log2 units (scaled by log2 e), so every exponential is a
+// single v_exp_f32.  2^(m - M) is the weight of a softmax state with running max m
+// under a new max M; an empty state (m = -inf) weighs nothing.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float state_weight(float m, float M) { return m > -INFINITY ? exp2_fast(m - M) : 0.0f; }
+
 // ---- 16-lane row reductions with DPP (a wave64 is four rows of 16 lanes) ----
 
 template <int CTRL>

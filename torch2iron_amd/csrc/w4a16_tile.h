@@ -1,0 +1,484 @@
+// Device-side building blocks of the W4A16 decode linear (gfx950), shared by
+// the standalone linear kernel and the fused kernels that run a linear phase.
+#pragma once
+
+#include "t2i_common.h"
+
+namespace t2i {
+
+constexpr int GS = 128;             // quantisation group along K
+constexpr int KSG = GS / 32;        // MFMA k-steps per group
+constexpr uint32_t MAGIC = 0x43004300u;  // two bf16 128.0
+constexpr uint32_t NIB2 = 0x000F000Fu;
+
+// EPI_LL: each output value goes out as one 64-bit word, the bf16 bits in the
+// low half and the launch's tag in the high half, stored agent-coherently
+// (written through to the device-coherent level), so a consumer in the same
+// launch on any XCD can poll the word itself until the tag shows it is this
+// launch's value (one word per lane and column: one-word-per-lane tiles only).
+enum : int { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_PAIRED = 3, EPI_LL = 4 };
+
+struct LinearParams {
+  const uint16_t* x;
+  const uint32_t* qw;
+  const uint32_t* qz;
+  const uint16_t* sc;
+  const uint16_t* residual;
+  uint16_t* y0;
+  uint16_t* y1;
+  const uint16_t* gamma;   // RMSNorm weight [K] of the fused-norm variant
+  float eps;
+  int M, K, N;
+  int ldx, ldy;
+  int chunks;           // K / (32 * CK)
+  int epi;
+  int rt;               // rows per row tile: 16, or fewer to give a narrow output more workgroups
+  unsigned long long* ll;   // EPI_LL: [M][ldy] tagged words
+  uint32_t tag;             // EPI_LL: this launch's tag
+};
+
+// MAGIC in a VGPR.  A VALU instruction reads at most one scalar operand (SGPR or
+// literal) on gfx9, so with the nibble mask as that operand the AND-OR takes
+// MAGIC from a VGPR and stays one v_and_or_b32; with both as constants the
+// compiler splits it into an AND and an OR.
+__device__ __forceinline__ uint32_t magic_vgpr() {
+  uint32_t m = MAGIC;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
+// magic: MAGIC, held in a VGPR (magic_vgpr).
+__device__ __forceinline__ bf16x8 b_operand(uint32_t w, uint32_t magic) {
+  u32x4 d;
+  d.x = (w & NIB2) | magic;           // (k0, k4)
+  d.y = ((w >> 4) & NIB2) | magic;    // (k1, k5)
+  d.z = ((w >> 8) & NIB2) | magic;    // (k2, k6)
+  d.w = ((w >> 12) & NIB2) | magic;   // (k3, k7)
+  return __builtin_bit_cast(bf16x8, d);
+}
+
+// v holds bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7); reorder to match b_operand,
+// one byte permute (v_perm_b32) per output word.
+__device__ __forceinline__ bf16x8 a_operand(u32x4 v) {
+  u32x4 d;
+  d.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);   // (lo x, lo z)
+  d.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);   // (hi x, hi z)
+  d.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  d.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  return __builtin_bit_cast(bf16x8, d);
+}
+
+__device__ __forceinline__ bf16x8 ones_operand() {
+  u32x4 d = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};
+  return __builtin_bit_cast(bf16x8, d);
+}
+
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+// g * sigmoid(g) on v_exp_f32 and v_rcp_f32: a few ulp of fp32 from silu_f32 (the
+// result is rounded to bf16 right after).  For the prompt GEMM's epilogue, where
+// the libm exponential and the IEEE division cost more than its k-loop's last steps.
+__device__ __forceinline__ float silu_fast(float g) {
+  return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g * 1.4426950408889634f));
+}
+
+template <int LW>
+__device__ __forceinline__ void load_words(const uint32_t* src, uint32_t (&w)[LW]) {
+  if constexpr (LW == 8) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(src + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+    w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+  } else if constexpr (LW == 4) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+  } else if constexpr (LW == 2) {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(src);
+    w[0] = a.x; w[1] = a.y;
+  } else {
+    w[0] = *src;
+  }
+}
+
+// Raw fp16 scales of LW consecutive columns, two per word (converted only when
+// the chunk is computed, so issuing a chunk's loads never waits for them).
+// LW 16-bit values from src (fp16 scales or bf16 residuals) as 32-bit words.  One
+// value (odd: at an odd index) comes as the aligned word holding it (half_of picks
+// it): a 16-bit load would be widened right after the load, which makes the
+// compiler wait for it there.
+template <int LW>
+__device__ __forceinline__ void load_scales(const uint16_t* src, uint32_t (&s)[(LW + 1) / 2], int odd = 0) {
+  if constexpr (LW == 8) {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(src);
+    s[0] = a.x; s[1] = a.y; s[2] = a.z; s[3] = a.w;
+  } else if constexpr (LW == 4) {
+    const u32x2 a = *reinterpret_cast<const u32x2*>(src);
+    s[0] = a.x; s[1] = a.y;
+  } else if constexpr (LW == 2) {
+    s[0] = *reinterpret_cast<const uint32_t*>(src);
+  } else {
+    s[0] = *reinterpret_cast<const uint32_t*>(src - odd);
+  }
+}
+
+// Bits of value t of this lane's columns; odd: the lane's first column is odd (LW == 1).
+template <int LW>
+__device__ __forceinline__ uint32_t half_of(const uint32_t (&s)[(LW + 1) / 2], int t, bool odd) {
+  const bool hi = LW == 1 ? odd : (t & 1) != 0;
+  return hi ? (s[t >> 1] >> 16) : (s[t >> 1] & 0xFFFFu);
+}
+
+// Operands of one chunk (CK k-steps, all inside one quantisation group), as loaded.
+template <int MT, int LW, int CK>
+struct Chunk {
+  uint32_t w[CK][LW];
+  u32x4 x[MT][CK];
+  u32x4 g[CK];                // fused-norm variant: norm weight of k 8 r .. 8 r + 7 of each k-step
+  uint32_t s[(LW + 1) / 2];   // fp16 scales of this lane's LW columns
+  uint32_t zw;                // qzeros word holding this lane's columns
+};
+
+// Activation row held by A-operand row `local` of the row tile at mbase.  A tile
+// of p.rt rows repeats its last row in the MFMA rows past p.rt, and rows past M
+// repeat row M - 1: the loads stay unconditional, an MFMA output row depends on
+// its own A row only, and the repeats are never stored.
+__device__ __forceinline__ int tile_row(const LinearParams& p, int mbase, int local) {
+  return min(mbase + min(local, p.rt - 1), p.M - 1);
+}
+
+template <int MT, int LW, int CK, bool NORM>
+__device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
+                                           Chunk<MT, LW, CK>& b) {
+  const int ks0 = ch * CK;
+#pragma unroll
+  for (int j = 0; j < CK; ++j)
+    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    const int m = tile_row(p, mbase, mi * 16 + c);
+#pragma unroll
+    for (int j = 0; j < CK; ++j)
+      b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < CK; ++j) b.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
+  }
+  const int g = ks0 / KSG;
+  load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
+  b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
+}
+
+// Pins a loaded value at this point: code that uses it cannot be moved above the
+// pin (say, to a point shared by the chunk schedules, where it would wait for the
+// chunk's loads before the other chunks' loads are issued).
+__device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
+
+// NORM (fused-norm variant, MT = 1): the A operand is bf16(x * gamma), and the
+// lane's share of its row's sum of squares accumulates in ss; the row's 1 / rms
+// multiplies the finished sums (see the kernel).
+template <int MT, int LW, int CK, bool NORM>
+__device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4], float& ss,
+                                              int zshift) {
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+#pragma unroll
+    for (int t = 0; t < LW; ++t) pin(b.w[j][t]);
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) pin(b.x[mi][j]);
+    if constexpr (NORM) pin(b.g[j]);
+  }
+#pragma unroll
+  for (int i = 0; i < (LW + 1) / 2; ++i) pin(b.s[i]);
+  pin(b.zw);
+  const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
+  const bf16x8 ones = ones_operand();
+  const uint32_t magic = magic_vgpr();
+  f32x4 acc[MT][LW];
+  f32x4 xs[MT];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < LW; ++t) acc[mi][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int j = 0; j < CK; ++j) {
+    bf16x8 bop[LW];
+#pragma unroll
+    for (int t = 0; t < LW; ++t) bop[t] = b_operand(b.w[j][t], magic);
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi) {
+      u32x4 xv = b.x[mi][j];
+      if constexpr (NORM) {
+        const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+        const uint32_t ga[4] = {b.g[j].x, b.g[j].y, b.g[j].z, b.g[j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16_lo(xa[e]), hi = bf16_hi(xa[e]);
+          ss = fmaf(lo, lo, ss);
+          ss = fmaf(hi, hi, ss);
+          o[e] = pack_bf16x2(lo * bf16_lo(ga[e]), hi * bf16_hi(ga[e]));
+        }
+        xv = u32x4{o[0], o[1], o[2], o[3]};
+      }
+      const bf16x8 a = a_operand(xv);
+      xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
+#pragma unroll
+      for (int t = 0; t < LW; ++t)
+        acc[mi][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop[t], acc[mi][t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < LW; ++t) {
+    const float zb = -(float)(128 + 1 + ((zw >> (4 * t)) & 0xFu));
+    const float sc = f16_to_f32(half_of<LW>(b.s, t, (zshift & 4) != 0));
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        total[mi][t][i] = fmaf(sc, fmaf(zb, xs[mi][i], acc[mi][t][i]), total[mi][t][i]);
+  }
+}
+
+// NC chunks of a wave in a straight line: every chunk's loads are in flight
+// before the first is computed (the first, A, was issued by the caller), and
+// each computation waits for its own chunk only: one memory round trip for the
+// whole K slice of the wave.  Up to 6 chunks of 2 k-steps without the fused
+// norm (12 registers a chunk at one word per lane), 3 otherwise.
+template <int MT, int LW, int CK, bool NORM, int NC>
+__device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_begin, int ncol, int c, int r, int mbase,
+                                                Chunk<MT, LW, CK>& A, float (&total)[MT][LW][4], float& ss,
+                                                int zshift) {
+  if constexpr (NC == 1) {
+    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+  } else {
+    Chunk<MT, LW, CK> rest[NC - 1];
+#pragma unroll
+    for (int i = 1; i < NC; ++i) load_chunk<MT, LW, CK, NORM>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
+    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+#pragma unroll
+    for (int i = 1; i < NC; ++i) compute_chunk<MT, LW, CK, NORM>(rest[i - 1], total, ss, zshift);
+  }
+}
+
+// Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32
+// sums v; res holds the row's residual values (bf16 pairs), fetched at the start.
+template <int LW>
+__device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW],
+                                          const uint32_t (&res)[(LW + 1) / 2]) {
+  if (m >= p.M) return;
+  if constexpr (LW == 1) {
+    if (p.epi == EPI_LL) {
+      const unsigned long long w = (unsigned long long)f32_to_bf16(v_in[0]) | ((unsigned long long)p.tag << 32);
+      __hip_atomic_store(p.ll + (size_t)m * p.ldy + ncol, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+  }
+  if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
+    float v[LW];
+#pragma unroll
+    for (int t = 0; t < LW; ++t) v[t] = v_in[t];
+    if (p.epi == EPI_RESIDUAL) {
+#pragma unroll
+      for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32((uint16_t)half_of<LW>(res, t, ncol & 1));
+    }
+    uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
+    if constexpr (LW == 1) {
+      dst[0] = (uint16_t)f32_to_bf16(v[0]);
+    } else {
+      uint32_t packed[LW / 2];
+#pragma unroll
+      for (int j = 0; j < LW / 2; ++j) packed[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
+      if constexpr (LW == 8) *reinterpret_cast<u32x4*>(dst) = u32x4{packed[0], packed[1], packed[2], packed[3]};
+      else if constexpr (LW == 4) *reinterpret_cast<u32x2*>(dst) = u32x2{packed[0], packed[1]};
+      else *reinterpret_cast<uint32_t*>(dst) = packed[0];
+    }
+  } else if constexpr (LW >= 2) {
+    // fused column 2q = gate q, 2q + 1 = up q
+    float o0[LW / 2], o1[LW / 2];
+#pragma unroll
+    for (int q = 0; q < LW / 2; ++q) {
+      const float g = round_bf16(v_in[2 * q]);
+      const float u = round_bf16(v_in[2 * q + 1]);
+      if (p.epi == EPI_SWIGLU) {
+        o0[q] = round_bf16(silu_f32(g)) * u;
+        o1[q] = 0.0f;
+      } else {
+        o0[q] = g;
+        o1[q] = u;
+      }
+    }
+    const size_t off = (size_t)m * p.ldy + (ncol >> 1);
+    if constexpr (LW == 8) {
+      *reinterpret_cast<u32x2*>(p.y0 + off) = u32x2{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3])};
+      if (p.epi == EPI_PAIRED)
+        *reinterpret_cast<u32x2*>(p.y1 + off) = u32x2{pack_bf16x2(o1[0], o1[1]), pack_bf16x2(o1[2], o1[3])};
+    } else if constexpr (LW == 4) {
+      *reinterpret_cast<uint32_t*>(p.y0 + off) = pack_bf16x2(o0[0], o0[1]);
+      if (p.epi == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = pack_bf16x2(o1[0], o1[1]);
+    } else {
+      p.y0[off] = (uint16_t)f32_to_bf16(o0[0]);
+      if (p.epi == EPI_PAIRED) p.y1[off] = (uint16_t)f32_to_bf16(o1[0]);
+    }
+  }
+}
+
+// Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
+// its own L2.  Neighbouring column blocks share 128-byte lines of qweight,
+// scales and qzeros, so the blocks are renumbered to give each XCD one
+// contiguous range of them: a shared line is then fetched from HBM once, not
+// once per XCD.  (With G a multiple of 8 the row-tile index in grid.z keeps
+// the XCD, so the row tiles of a column block share its weights in one L2.)
+__device__ __forceinline__ int xcd_block(int b, int G) {
+  return (G & 7) ? b : (b & 7) * (G >> 3) + (b >> 3);
+}
+
+// NORM: the fused-RMSNorm variant.  RMSNorm(x) W = (1 / rms) (x * gamma) W for
+// each row, so the waves multiply bf16(x * gamma) by the weights as soon as
+// their own loads land, summing each row's squares alongside, and the row's
+// 1 / rms, bf16(1 / sqrt(mean(x^2) + eps)) as the standalone RMSNorm rounds it,
+// multiplies the finished sums.  Normalising before the product needs every
+// row's full sum of squares first, that is two workgroup barriers ahead of the
+// MFMAs (measured 0.92 against 0.86 ms per decode step); the only change is
+// where the products are rounded to bf16.
+// Everything the first loads' addresses need comes as leading scalar arguments
+// (x, qweight, scales, qzeros, the residual or norm weight, N, M, K and the
+// column-block count G = gridDim.x), which the library is built to preload into
+// SGPRs at wave launch: the first loads are issued without waiting for a load of
+// the kernel arguments (measured 4.8 -> 4.4 us per launch over the decode shapes).
+// The other fields come from p_ (the epilogue's, needed once the data is in).
+// M_ carries log2 of the row-tile height in bits 24 and up (M < 2^24).
+// One workgroup's tile of the decode linear: column block bx (of G) and row tile bz.
+// after_loads() runs once the first chunk's loads are issued and before any of
+// them is waited for (a fused kernel issues its own loads there).
+struct NoHook {
+  __device__ __forceinline__ void operator()() const {}
+};
+template <int MT, int LW, int W, int CK, bool NORM, class Hook = NoHook>
+__device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx, int bz,
+                                            const Hook& after_loads = Hook()) {
+  static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
+  constexpr int E = MT * LW * 4;      // fp32 results per lane
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar control flow
+  const int c = lane & 15;
+  const int r = lane >> 4;
+  const int ncol = xcd_block(bx, G) * (16 * LW) + LW * c;
+  const int zshift = (ncol & 7) * 4;
+  const int mbase = bz * p.rt;   // row tile of this workgroup
+
+  // this wave's chunks: a contiguous slice of K
+  const int per_wave = (p.chunks + W - 1) / W;
+  const int c_begin = wave * per_wave;
+  const int c_end = min(c_begin + per_wave, p.chunks);
+
+  float total[MT][LW][4];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int t = 0; t < LW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
+  float ss = 0.0f;   // fused norm: this lane's share of its A row's sum of squares
+
+  // every wave loads a first chunk (a wave without chunks reloads the last and computes nothing)
+  Chunk<MT, LW, CK> A, B;
+  load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
+  // The residual values this wave stores (residual epilogue) are fetched now, so
+  // the epilogue waits for nothing.  The load is unconditional: waves that store
+  // nothing fetch a clamped row and drop it, and without a residual the first
+  // scales row stands in (in bounds, unused).
+  const int st_mi = min(wave >> 2, MT - 1), st_i = wave & 3;
+  const int st_local = st_mi * 16 + r * 4 + st_i;
+  const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // the row this lane stores (M: none)
+  uint32_t resv[(LW + 1) / 2];
+  load_scales<LW>(!NORM && p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
+                  ncol & 1);
+  __builtin_amdgcn_sched_barrier(0);
+  after_loads();
+  __builtin_amdgcn_sched_barrier(0);
+  // One word per lane: straight-line schedules for up to 6 chunks per wave (3
+  // with the fused norm), else a double-buffered loop.
+  // Wider tiles use the loop alone, which keeps their registers (occupancy) as
+  // they were; their decode plans have one chunk per wave.
+  const int n = c_end - c_begin;   // wave-uniform
+  bool looped = true;
+  if constexpr (LW == 1) {
+    constexpr bool DEEP = !NORM && CK == 2;   // 4..6 chunks in registers: 12 a chunk
+    looped = false;
+    if (n == 1) {
+      straight_chunks<MT, LW, CK, NORM, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (n == 2) {
+      straight_chunks<MT, LW, CK, NORM, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (n == 3) {
+      straight_chunks<MT, LW, CK, NORM, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 4) {
+      straight_chunks<MT, LW, CK, NORM, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 5) {
+      straight_chunks<MT, LW, CK, NORM, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else if (DEEP && n == 6) {
+      straight_chunks<MT, LW, CK, NORM, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+    } else {
+      looped = true;
+    }
+  }
+  if (looped) {
+    for (int ch = c_begin; ch < c_end; ch += 2) {
+      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
+      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+      if (ch + 1 >= c_end) break;
+      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 2, ncol, c, r, mbase, A);
+      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
+    }
+  }
+
+  // ---- reduce the waves of this workgroup in LDS: one barrier, fixed order ----
+  // Every wave that had chunks parks its sums (and, fused norm, its rows' sums of
+  // squares); then wave 4 mi + i adds row i of m-tile mi over the waves in wave
+  // order and stores it.
+  const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
+  static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
+  {
+    __shared__ float red[W * E * 64];
+    __shared__ float s_ss[NORM ? W : 1][16];
+    if constexpr (NORM) {
+      ss += __shfl_xor(ss, 16, 64);   // the four k sub-blocks of A row c
+      ss += __shfl_xor(ss, 32, 64);
+    }
+    if (wave < nw) {
+      float* dst = red + wave * E * 64 + lane;
+#pragma unroll
+      for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+        for (int t = 0; t < LW; ++t)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
+      if constexpr (NORM) {
+        if (lane < 16) s_ss[wave][lane] = ss;
+      }
+    }
+    __syncthreads();
+    if (wave >= 4 * MT) return;
+    float v[LW];
+#pragma unroll
+    for (int t = 0; t < LW; ++t) v[t] = 0.0f;
+    float t_ss = 0.0f;   // fused norm: output row st_local of the tile is A row st_local (MT = 1)
+    for (int w = 0; w < nw; ++w) {
+      const float* src = red + w * E * 64 + lane;
+#pragma unroll
+      for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
+      if constexpr (NORM) t_ss += s_ss[w][st_local];
+    }
+    if constexpr (NORM) {
+      const float inv = round_bf16(1.0f / sqrtf(t_ss / (float)p.K + p.eps));
+#pragma unroll
+      for (int t = 0; t < LW; ++t) v[t] *= inv;
+    }
+    store_row<LW>(p, ncol, st_m, v, resv);
+  }
+}
+
+
+}  // namespace t2i

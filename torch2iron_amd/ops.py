@@ -275,6 +275,67 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n
     return out
 
 
+def qkv_attention(x: torch.Tensor, norm_weight: torch.Tensor | None, eps: float, w_qkv: W4A16Weight,
+                  positions: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
+                  rope: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
+                  out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """The decode layer's front in one cooperative launch: RMSNorm (``norm_weight``,
+    or none when ``x`` is already normalised) + the fused q|k|v projection, then
+    ``decode_attention`` on those rows.  ``x`` bf16 ``[B, hidden]`` (B <= 16); returns
+    the context ``[B, Hq * D]``.  The launch takes one workgroup per CU: it must not
+    run concurrently with other GPU work."""
+    _check_weight(w_qkv)
+    _check_dev("x", x, BF16)
+    _check_dev("positions", positions, torch.int32)
+    for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_dev(n, t, BF16)
+    if norm_weight is not None:
+        _check_dev("norm_weight", norm_weight, BF16)
+        if norm_weight.numel() != w_qkv.K:
+            raise ValueError("norm_weight must hold K values")
+    b = positions.numel()
+    d = q_norm.numel()
+    if k_norm.numel() != d:
+        raise ValueError("q_norm and k_norm must both hold head_dim values")
+    if x.numel() != b * w_qkv.K:
+        raise ValueError(f"x must be [B, {w_qkv.K}] with B = {b}")
+    if w_qkv.N != (n_heads + 2 * n_kv_heads) * d:
+        raise ValueError("the qkv weight must have (Hq + 2 Hkv) * D columns")
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (b, n_kv_heads) \
+            or k_cache.shape[3] != d:
+        raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
+    ctx_cap = k_cache.shape[2]
+    if rope.shape[0] < ctx_cap or rope.shape[1] != d:
+        raise ValueError("rope table must be [>= ctx_cap, D]")
+    if out is None:
+        out = torch.empty(b, n_heads * d, dtype=BF16, device=x.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != b * n_heads * d:
+        raise ValueError(f"out must hold {b}x{n_heads * d} elements")
+    lib = _lib.load()
+    nbytes = lib.t2i_qkv_attention_workspace_bytes(b, n_heads, n_kv_heads)
+    if nbytes == 0:
+        raise ValueError(f"unsupported shape for the fused launch: B={b}, Hq={n_heads}, Hkv={n_kv_heads}")
+    ws = (workspace or DEFAULT_WORKSPACE).get(("qkv_attn", b, n_heads, n_kv_heads), nbytes, x.device)
+    rc = lib.t2i_qkv_attention(x.data_ptr(), b, _lib.ptr(norm_weight), float(eps), w_qkv.qweight.data_ptr(),
+                               w_qkv.qzeros.data_ptr(), w_qkv.scales.data_ptr(), w_qkv.K, w_qkv.group_size,
+                               positions.data_ptr(), n_heads, n_kv_heads, d, q_norm.data_ptr(), k_norm.data_ptr(),
+                               rope.data_ptr(), int(rope_style), k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap,
+                               out.data_ptr(), ws.data_ptr(), nbytes, _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_qkv_attention")
+    return out
+
+
+def qkv_attention_errors(b: int, n_heads: int, n_kv_heads: int, device, workspace: Workspace | None = None) -> int:
+    """The error word of the fused launch's workspace (non-zero: a wait timed out).
+    Synchronises with the device."""
+    lib = _lib.load()
+    off = lib.t2i_qkv_attention_error_offset(b, n_heads, n_kv_heads)
+    nbytes = lib.t2i_qkv_attention_workspace_bytes(b, n_heads, n_kv_heads)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("qkv_attn", b, n_heads, n_kv_heads), nbytes, device)
+    return int(ws[off:off + 4].view(torch.int32).item())
+
+
 def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_kv_heads: int,
                        q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float, rope: torch.Tensor,
                        k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
