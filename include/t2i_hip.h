@@ -174,6 +174,67 @@ int t2i_qkv_attention(const uint16_t* x, int32_t B, const uint16_t* norm_weight,
                       uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Every decoder layer of one decode step in one cooperative launch.
+ * Per layer l (weights and caches from layers[l], a device array of n_layers
+ * entries): RMSNorm + q|k|v projection (layer 0 takes xn0, already normalised),
+ * the attention of t2i_decode_attention (q/k RMSNorm, RoPE, KV write at
+ * positions[b]), o_proj + residual, RMSNorm + paired gate/up + SwiGLU, down +
+ * residual.  x bf16 [B, hidden] is the residual stream: the embedding rows in,
+ * the last layer's output out.  Weights as the t2i_w4a16_* calls take them
+ * (gate_up interleaved as for t2i_w4a16_gate_up, N = 2 * intermediate); norm
+ * weights bf16; caches bf16 [B, Hkv, ctx_cap, D] per layer.
+ * Every linear gives the bits the standalone calls give on the same input; the
+ * attention is t2i_qkv_attention's (the context may differ from
+ * t2i_decode_attention's by rounding).  Supported: 1 <= B <= 16, Hq / Hkv in
+ * {1, 2}, D = 128, group 128, and shapes whose decode-linear plans are the
+ * 16-wave tiles (t2i_decode_step_workspace_bytes returns 0 otherwise; Qwen3-0.6B
+ * fits).  One 16-wave workgroup per CU, all resident: launches must not run
+ * concurrently with other work on the device.  The workspace must be
+ * zero-filled before first use and not shared by calls that overlap in time; a
+ * wait that times out sets the error word (t2i_decode_step_offset, region 4).
+ * Replaces: the whole-step runlist of quantized_qwen3/batch_decode_fused.py:426-539
+ *           compiled into one ELF (batch_decode_fused.py:556-588) and run as one
+ *           dispatch (FusedFullELFCallable.__call__, fusion.py:821-840), lm_head
+ *           excepted.
+ */
+typedef struct {
+  const int32_t* qkv_qweight;
+  const int32_t* qkv_qzeros;
+  const uint16_t* qkv_scales;
+  const int32_t* o_qweight;
+  const int32_t* o_qzeros;
+  const uint16_t* o_scales;
+  const int32_t* gate_up_qweight;
+  const int32_t* gate_up_qzeros;
+  const uint16_t* gate_up_scales;
+  const int32_t* down_qweight;
+  const int32_t* down_qzeros;
+  const uint16_t* down_scales;
+  const uint16_t* input_norm;
+  const uint16_t* post_attention_norm;
+  const uint16_t* q_norm;
+  const uint16_t* k_norm;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+} t2i_decode_layer;
+
+size_t t2i_decode_step_workspace_bytes(int32_t B, int32_t n_layers, int32_t hidden, int32_t intermediate,
+                                       int32_t Hq, int32_t Hkv);
+/* Byte offset in the workspace of (after a launch, as 32-bit words with the bf16
+ * bits in the low half): 0 the per-layer contexts [L, B, Hq * D], 1 the residual
+ * stream after each layer's attention [L, B, hidden], 2 the SwiGLU outputs
+ * [L, B, intermediate], 3 the residual stream between layers [L - 1, B, hidden];
+ * 4 the 32-bit error word; 0 for an unsupported shape or region.  (The first
+ * B * (Hq + 2 Hkv) * D 64-bit words hold the last layer's q|k|v projection, bf16
+ * bits in the low 16 bits.) */
+size_t t2i_decode_step_offset(int32_t B, int32_t n_layers, int32_t hidden, int32_t intermediate,
+                              int32_t Hq, int32_t Hkv, int32_t region);
+int t2i_decode_step(const t2i_decode_layer* layers, int32_t n_layers, const uint16_t* xn0, uint16_t* x,
+                    int32_t B, int32_t hidden, int32_t intermediate, int32_t Hq, int32_t Hkv, int32_t D,
+                    int32_t group_size, const int32_t* positions, const uint16_t* rope, int32_t rope_style,
+                    int32_t ctx_cap, float eps, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Allocation-free variant of t2i_decode_attention.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).

@@ -288,9 +288,9 @@ def test_greedy_decode_micro_batch_streams_agree(gpu):
     t = gm.random_qwen3_tensors(cfg, seed=31, weights="centered")
     b, plen, new = 8, 12, 16
     prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(32))
-    # the one-launch qkv + attention front needs the whole GPU (one stream): off here,
-    # so every split runs the same kernels
-    model = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=48, device=gpu, streams=1, fused=False)
+    # the one-launch paths need the whole GPU (one stream): off here, so every
+    # split runs the same kernels
+    model = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=48, device=gpu, streams=1, fused=False, persistent=False)
     ref = model.generate(prompt, new)
     for s in (2, 3, 4):
         model.set_streams(s)

@@ -142,8 +142,8 @@ def test_model_decode_with_fused_front_matches_unfused(gpu):
     t = gm.random_qwen3_tensors(cfg, seed=61, weights="centered")
     b, plen, new = 16, 40, 16
     prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(62))
-    fused = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu, fused=True)
-    plain = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu, fused=False)
+    fused = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu, fused=True, persistent=False)
+    plain = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu, fused=False, persistent=False)
     assert fused.layers[0].fused and not plain.layers[0].fused
     tf = fused.generate(prompt, new)
     tp = plain.generate(prompt, new)

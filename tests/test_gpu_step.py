@@ -1,0 +1,145 @@
+"""Every layer of a decode step in one cooperative launch (``t2i_decode_step``).
+
+Each linear phase must give the bits of the standalone kernel on the same input
+(read back from the launch's per-layer activations), the attention must match
+``t2i_decode_attention`` on the same q/k/v rows within one bf16 rounding with
+identical KV-cache writes, and greedy decode through the one-launch step must
+agree with the separate-kernel path (tokens, logits) and with itself across
+graph replays."""
+
+import pytest
+import torch
+
+from torch2iron_amd import model as gm
+from torch2iron_amd import ops
+
+pytestmark = pytest.mark.gpu
+BF16 = torch.bfloat16
+
+
+def _model(gpu, cfg, b, cap, seed, persistent=True, weights="centered"):
+    t = gm.random_qwen3_tensors(cfg, seed=seed, weights=weights)
+    return gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, persistent=persistent)
+
+
+@pytest.mark.parametrize("b,cap,positions", [
+    (16, 640, [576] * 8 + [0, 95, 96, 191, 192, 300, 383, 639]),
+    (8, 1100, [1024] * 4 + [0, 191, 192, 1099]),
+    (3, 300, [0, 150, 299]),
+    (1, 2100, [2050]),
+])
+def test_step_phases_match_standalone_kernels(gpu, b, cap, positions):
+    print(f"step phases B={b} cap={cap}", flush=True)
+    cfg = gm.Qwen3Config(n_layers=3, vocab=512)
+    m = _model(gpu, cfg, b, cap, seed=b + cap)
+    assert m.step_table is not None
+    g = torch.Generator().manual_seed(b)
+    m.k_cache.copy_(torch.randn(m.k_cache.shape, generator=g).to(BF16))
+    m.v_cache.copy_(torch.randn(m.v_cache.shape, generator=g).to(BF16))
+    kc0, vc0 = m.k_cache.clone(), m.v_cache.clone()
+    m.tokens.copy_(torch.randint(0, cfg.vocab, (b,), generator=g, dtype=torch.int32).to(gpu))
+    m.positions.copy_(torch.tensor(positions, dtype=torch.int32))
+    buf = m.micro[0].buf
+    m.forward_step(with_head=False)
+    torch.cuda.synchronize()
+    assert ops.decode_step_errors(m.step_table, gpu, workspace=buf.workspace) == 0
+    mid = ops.decode_step_intermediates(m.step_table, gpu, workspace=buf.workspace)
+    x0 = m.embed[m.tokens.long()]
+    xn0 = buf.xn   # layer 0's input, from the embedding gather + RMSNorm launch
+    c = cfg
+    kc_ref, vc_ref = kc0.clone(), vc0.clone()
+    for li, layer in enumerate(m.layers):
+        w = layer.w
+        x_in = x0 if li == 0 else mid["x"][li - 1]
+        x_out = m.x if li == cfg.n_layers - 1 else mid["x"][li]
+        qkv = ops.linear(xn0, w.qkv) if li == 0 else ops.rmsnorm_linear(x_in, w.ln1, c.eps, w.qkv)
+        if li == cfg.n_layers - 1:
+            assert torch.equal(mid["qkv"], qkv), "qkv projection bits"
+        ref = ops.decode_attention(qkv, m.positions, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, m.rope,
+                                   kc_ref[li], vc_ref[li], rope_style=layer.rope_style)
+        got = mid["ctx"][li]
+        diff = (got.float() - ref.float()).abs()
+        assert (diff <= 2.0 ** -7 * ref.float().abs() + 1e-3 * ref.float().abs().max()).all(), f"layer {li} context"
+        assert torch.equal(m.k_cache[li], kc_ref[li]) and torch.equal(m.v_cache[li], vc_ref[li]), f"layer {li} KV"
+        # the linear phases, bit for bit, each on the launch's own input rows
+        assert torch.equal(mid["xmid"][li], ops.linear(got, w.o, residual=x_in)), f"layer {li} o_proj"
+        assert torch.equal(mid["h"][li], ops.rmsnorm_gate_up(mid["xmid"][li], w.ln2, c.eps, w.gate_up)), \
+            f"layer {li} gate_up"
+        assert torch.equal(x_out, ops.linear(mid["h"][li], w.down, residual=mid["xmid"][li])), f"layer {li} down"
+
+
+def test_step_greedy_decode_matches_separate_kernels(gpu):
+    """4 layers, batch 16: the one-launch step against the separate-kernel path,
+    prefill then 24 greedy steps; graph replays equal eager launches."""
+    cfg = gm.Qwen3Config(n_layers=4, vocab=4096)
+    t = gm.random_qwen3_tensors(cfg, seed=71, weights="centered")
+    b, plen, new = 16, 40, 24
+    prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(72))
+    one = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=80, device=gpu, persistent=True)
+    sep = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=80, device=gpu)
+    assert one.step_table is not None and sep.step_table is None
+    t1 = one.generate(prompt, new)
+    t1e = one.generate(prompt, new, use_graph=False)
+    assert torch.equal(t1, t1e), "graph replays differ from eager launches"
+    t1b = one.generate(prompt, new)
+    assert torch.equal(t1, t1b), "second graph run differs"
+    ts = sep.generate(prompt, new)
+    same = (t1 == ts).all(dim=1).float().mean().item()
+    print(f"one-launch vs separate kernels: {same:.2f} of sequences identical over {new} tokens", flush=True)
+    assert same >= 0.75
+    # teacher-forced logits along the separate path's tokens
+    one.reset()
+    sep.reset()
+    l1 = one.prefill(prompt, want_logits=True)
+    ls = sep.prefill(prompt, want_logits=True)
+    assert torch.equal(l1, ls)   # the prompt pass is the same code on both
+    worst = 0.0
+    for s in range(4):
+        pos = torch.full((b,), plen + s)
+        _, a = one.decode_step(ts[:, s], pos, want_logits=True)
+        _, r = sep.decode_step(ts[:, s], pos, want_logits=True)
+        worst = max(worst, ((a - r).pow(2).mean().sqrt() / r.std()).item())
+    print(f"teacher-forced logit RMS difference / logit std: {worst:.2e}", flush=True)
+    assert worst < 2e-2
+
+
+def test_step_decode_mode_prompt_and_replays(gpu):
+    """The prompt consumed one position at a time through captured one-launch
+    steps equals eager launches, and a second prompt of the same length too."""
+    cfg = gm.Qwen3Config(n_layers=2, vocab=2048)
+    m = _model(gpu, cfg, 4, 48, seed=81)
+    runs = []
+    for seed in (82, 83, 82):
+        prompt = torch.randint(0, cfg.vocab, (4, 10), generator=torch.Generator().manual_seed(seed))
+        got = m.generate(prompt, 8, prompt_mode="decode")
+        eager = m.generate(prompt, 8, prompt_mode="decode", use_graph=False)
+        assert torch.equal(got, eager)
+        runs.append(got)
+    assert torch.equal(runs[0], runs[2]) and not torch.equal(runs[0], runs[1])
+
+
+def test_step_falls_back_where_no_plan(gpu):
+    """More than 16 rows, or several streams: the separate kernels run (no table);
+    the wrapper rejects a table whose shapes have no one-launch plan."""
+    cfg = gm.Qwen3Config(n_layers=1, vocab=256)
+    m = _model(gpu, cfg, 17, 32, seed=91)
+    assert m.step_table is None
+    m2 = _model(gpu, cfg, 8, 32, seed=91)
+    assert m2.step_table is not None
+    m2.set_streams(2)
+    assert m2.step_table is None
+    m2.set_streams(1)
+    assert m2.step_table is not None
+    big = gm.Qwen3Config(n_layers=1, vocab=256, hidden=2048, intermediate=6144)
+    m3 = _model(gpu, big, 16, 32, seed=92)
+    assert m3.step_table is None    # the 1.7B gate/up plan is a 64-column tile
+    layers = [dict(qkv=L.w.qkv, o=L.w.o, gate_up=L.w.gate_up, down=L.w.down, ln1=L.w.ln1, ln2=L.w.ln2,
+                   q_norm=L.w.q_norm, k_norm=L.w.k_norm, k_cache=m3.k_cache[i], v_cache=m3.v_cache[i])
+              for i, L in enumerate(m3.layers)]
+    table = ops.DecodeLayerTable(layers, big.n_heads, big.n_kv_heads, gpu)
+    assert table.workspace_bytes() == 0
+    with pytest.raises(ValueError):
+        ops.decode_step(table, m3.xn, m3.x, m3.positions, big.eps, m3.rope)
+    layers[0]["k_cache"] = m3.k_cache[0, :8]
+    with pytest.raises(ValueError):
+        ops.DecodeLayerTable(layers, big.n_heads, big.n_kv_heads, gpu)

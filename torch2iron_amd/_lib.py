@@ -51,6 +51,11 @@ SIGNATURES = {
     "t2i_qkv_attention": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int32,
                                     c_int32, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                     c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "t2i_decode_step_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "t2i_decode_step_offset": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "t2i_decode_step": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                  c_int32, c_int32, c_void_p, c_void_p, c_int32, c_int32, c_float, c_void_p, c_size_t,
+                                  c_void_p]),
     "t2i_prefill_qk_rope_kv": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                                          c_void_p, c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p,
                                          c_void_p, c_int32, c_void_p]),

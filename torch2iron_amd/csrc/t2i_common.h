@@ -14,6 +14,15 @@ typedef __attribute__((ext_vector_type(4))) float f32x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
+// threadIdx.x behind an empty asm: values derived from it are recomputed where a
+// phase uses them instead of being hoisted out of a persistent kernel's layer
+// loop and held in registers across every other phase.
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // ---- bf16 / fp16 scalar conversions (bit patterns held in uint16/uint32) ----
 
 __device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
@@ -89,6 +98,48 @@ __device__ __forceinline__ float ld_agent(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Agent-coherent activations of a launch that runs several dependent phases:
+// the producer writes with st_coh16, waits for its stores and bumps an arrival
+// counter; a consumer that has seen the counter reads with ld_coh32 / ld_coh128
+// (relaxed agent-scope atomics: never served by a stale copy in its XCD's L2).
+__device__ __forceinline__ void st_coh16(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_coh32(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coh32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned long long ld_coh64(const void* p) {
+  return __hip_atomic_load(reinterpret_cast<const unsigned long long*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u32x4 ld_coh128(const void* p) {
+  const unsigned long long* q = reinterpret_cast<const unsigned long long*>(p);
+  const unsigned long long a = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long b = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+}
+
+// The error word of a launch whose workgroups wait on each other (ctl[2]): a
+// bounded wait that gives up raises it, and every other wait then gives up early.
+constexpr int WAIT_SPIN = 1 << 18;   // polls before a wait gives up
+__device__ __forceinline__ void ctl_fail(unsigned* ctl) {
+  __hip_atomic_store(ctl + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool ctl_failed(const unsigned* ctl) {
+  return __hip_atomic_load(ctl + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+// true when the wait should give up (spin budget spent, or the error word up)
+__device__ __forceinline__ bool wait_gives_up(int& spins, unsigned* ctl) {
+  if (++spins >= WAIT_SPIN || ((spins & 255) == 0 && ctl_failed(ctl))) {
+    ctl_fail(ctl);
+    return true;
+  }
+  __builtin_amdgcn_s_sleep(1);
+  return false;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
   v = row_sum16(v);

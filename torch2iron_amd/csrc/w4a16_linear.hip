@@ -400,11 +400,9 @@ __global__ void dequant_f32_kernel(const uint32_t* __restrict__ qw, const uint32
 // ============================================================================
 // host side
 // ============================================================================
-namespace {
+namespace t2i_host {
 
 using namespace t2i;
-using t2i_host::aligned16;
-using t2i_host::fail;
 
 // Compiled tile configurations: (MT m-tiles, LW words per lane, W waves, CK k-steps per chunk).
 // Row tiles beyond 16 rows go to grid.z (measured faster than multi-tile waves
@@ -413,18 +411,11 @@ using t2i_host::fail;
   X(1, 1, 16, 4)              \
   X(1, 1, 16, 2)              \
   X(1, 2, 16, 4)              \
+  X(1, 2, 16, 2)              \
   X(1, 2, 8, 4)               \
   X(1, 4, 8, 4)               \
   X(1, 4, 4, 4)               \
   X(1, 8, 4, 4)
-
-struct Plan {
-  int MT, LW, W, CK;
-  int rt;       // rows per row tile (16 * MT, or fewer)
-  int mz;       // row tiles (grid.z)
-  int cbs;      // column blocks (grid.x)
-  int chunks;   // K / (32 * CK)
-};
 
 bool config_exists(int MT, int LW, int W, int CK) {
 #define T2I_MATCH(a, b, c, d) if (MT == a && LW == b && W == c && CK == d) return true;
@@ -433,7 +424,7 @@ bool config_exists(int MT, int LW, int W, int CK) {
   return false;
 }
 
-void finish_plan(Plan& pl, int M, int K, int N) {
+void finish_plan(LinearPlan& pl, int M, int K, int N) {
   pl.cbs = N / (16 * pl.LW);
   pl.chunks = K / (32 * pl.CK);
   // Row tiles shorter than 16 rows when the column blocks alone leave CUs idle:
@@ -461,14 +452,14 @@ void finish_plan(Plan& pl, int M, int K, int N) {
 // compiled plans: one 16-row tile per workgroup (more rows go to grid.z and
 // share the weights in their XCD's L2), and the narrowest column block that
 // keeps the column-block x row-tile count at 256 or less: 16 columns (1 word
-// per lane, 16 waves, chunks of 2 k-steps), else 32 (2 words, 8 waves), else
-// 64 (4 words, 8 waves).  The rule picks the measured optimum, or a plan
+// per lane, 16 waves, chunks of 2 k-steps), else 32 (2 words, 8 waves; paired
+// outputs 16 waves, see below), else 64 (4 words, 8 waves).  The rule picks the measured optimum, or a plan
 // within 4 % of it, at 38 of the 40 shape/M points, and is within 9 % at all.  Splitting K across workgroups was measured slower:
 // the fp32 partials and an arrival counter add memory round trips that cost
 // more than the parallelism they add at these sizes, so K is only split
 // between the waves of a workgroup.
-Plan plan_linear(int M, int K, int N, bool paired) {
-  Plan pl{};
+LinearPlan plan_linear(int M, int K, int N, bool paired) {
+  LinearPlan pl{};
   pl.MT = 1;
   pl.CK = 4;
   const int mz = (M + 15) / 16;
@@ -476,14 +467,21 @@ Plan plan_linear(int M, int K, int N, bool paired) {
     // (N not a multiple of 32: 16-column blocks are the only whole ones)
     pl.LW = 1; pl.W = 16; pl.CK = 2;
   } else if ((N / 32) * mz <= 256 || N % 64) {
-    pl.LW = 2; pl.W = 8;
+    // Paired (gate/up) outputs take 16 waves of 2-step chunks, the configuration
+    // the one-launch decode step runs (its workgroups have 16 waves and 128
+    // registers a lane), so both paths give the same bits; 8 waves of 4-step
+    // chunks measured 0.1-0.2 us faster on the Qwen3-0.6B gate_up at M <= 16
+    // (4.62 against 4.73 us at M = 16) but need 148 registers a lane.
+    pl.LW = 2;
+    pl.W = paired ? 16 : 8;
+    pl.CK = paired ? 2 : 4;
   } else {
     pl.LW = 4; pl.W = 8;
   }
 #ifdef T2I_TUNING
   // tuning builds only: T2I_PLAN="MT,LW,W,CK" overrides the choice
   if (const char* env = getenv("T2I_PLAN")) {
-    Plan o = pl;
+    LinearPlan o = pl;
     if (sscanf(env, "%d,%d,%d,%d", &o.MT, &o.LW, &o.W, &o.CK) == 4 && config_exists(o.MT, o.LW, o.W, o.CK) &&
         N % (16 * o.LW) == 0 && (!paired || o.LW >= 2))
       pl = o;
@@ -492,6 +490,16 @@ Plan plan_linear(int M, int K, int N, bool paired) {
   finish_plan(pl, M, K, N);
   return pl;
 }
+
+}  // namespace t2i_host
+
+namespace {
+
+using namespace t2i;
+using t2i_host::aligned16;
+using t2i_host::fail;
+using t2i_host::LinearPlan;
+using t2i_host::plan_linear;
 
 template <int MT, int LW, int W, int CK, bool NORM>
 hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
@@ -504,7 +512,7 @@ hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_plan(const Plan& pl, const LinearParams& p, bool norm, hipStream_t s) {
+hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
 #define T2I_LAUNCH(a, b, c, d)                                         \
   if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)             \
@@ -569,7 +577,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p);
     return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
   }
-  const Plan pl = plan_linear(M, K, N, paired);
+  const LinearPlan pl = plan_linear(M, K, N, paired);
   LinearParams p{};
   p.x = x;
   p.qw = reinterpret_cast<const uint32_t*>(qweight);

@@ -34,7 +34,16 @@ struct LinearParams {
   int epi;
   int rt;               // rows per row tile: 16, or fewer to give a narrow output more workgroups
   unsigned long long* ll;   // EPI_LL: [M][ldy] tagged words
-  uint32_t tag;             // EPI_LL: this launch's tag
+  uint32_t tag;             // EPI_LL: this launch's tag; yll: its low 16 bits
+  // Phases of one launch (linear_phase) hand rows over as tagged 32-bit words,
+  // bf16 bits | tag << 16: input (xll, in place of x), residual (rll, in place of
+  // residual) and output (yll, in place of y0), each used when not NULL; the
+  // input and residual words are awaited until they carry xtag / rtag.
+  const uint32_t* xll;
+  const uint32_t* rll;
+  uint32_t* yll;
+  uint32_t xtag, rtag;
+  unsigned* ctl;            // ctl[2]: the launch's error word (bounded waits)
 };
 
 // MAGIC in a VGPR.  A VALU instruction reads at most one scalar operand (SGPR or
@@ -168,6 +177,75 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
   b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
 }
 
+// The weight half of load_chunk (packed words, norm weight, scales, zeros):
+// nothing here depends on the activations.
+template <int MT, int LW, int CK, bool NORM>
+__device__ __forceinline__ void load_chunk_w(const LinearParams& p, int ch, int ncol, int r, Chunk<MT, LW, CK>& b) {
+  const int ks0 = ch * CK;
+#pragma unroll
+  for (int j = 0; j < CK; ++j)
+    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+  if constexpr (NORM) {
+#pragma unroll
+    for (int j = 0; j < CK; ++j) b.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
+  }
+  const int g = ks0 / KSG;
+  load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
+  b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
+}
+
+// 8 consecutive bf16 values held as tagged 32-bit words (word i = bf16 bits |
+// tag << 16), read as four agent-coherent 64-bit loads.
+struct Tagged8 {
+  unsigned long long w[4];
+};
+__device__ __forceinline__ void tagged_issue(const uint32_t* src, Tagged8& t) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) t.w[q] = ld_coh64(src + 2 * q);
+}
+__device__ __forceinline__ bool tagged_ready(const Tagged8& t, uint32_t tag) {
+  bool ok = true;
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    ok = ok && (uint32_t)((t.w[q] >> 16) & 0xFFFFu) == tag && (uint32_t)(t.w[q] >> 48) == tag;
+  return ok;
+}
+// Wait (bounded) until all 8 words carry tag, then the values as 4 bf16 pairs.
+__device__ __forceinline__ u32x4 tagged_wait8(const uint32_t* src, Tagged8 t, uint32_t tag, unsigned* ctl) {
+  int spins = 0;
+  while (!tagged_ready(t, tag)) {
+    if (wait_gives_up(spins, ctl)) break;
+    tagged_issue(src, t);
+  }
+  uint32_t v[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = (uint32_t)(t.w[q] & 0xFFFFu) | (uint32_t)((t.w[q] >> 16) & 0xFFFF0000u);
+  return u32x4{v[0], v[1], v[2], v[3]};
+}
+// One tagged word, awaited (bounded); its bf16 bits in both halves of the result.
+__device__ __forceinline__ uint32_t tagged_wait1(const uint32_t* src, uint32_t tag, unsigned* ctl) {
+  uint32_t w = ld_coh32(src);
+  int spins = 0;
+  while ((w >> 16) != tag) {
+    if (wait_gives_up(spins, ctl)) break;
+    w = ld_coh32(src);
+  }
+  return (w & 0xFFFFu) | (w << 16);
+}
+
+// The activation half, agent-coherent (the rows were written in the same launch).
+template <int MT, int LW, int CK>
+__device__ __forceinline__ void load_chunk_x_coh(const LinearParams& p, int ch, int c, int r, int mbase,
+                                                 Chunk<MT, LW, CK>& b) {
+  const int ks0 = ch * CK;
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi) {
+    const int m = tile_row(p, mbase, mi * 16 + c);
+#pragma unroll
+    for (int j = 0; j < CK; ++j) b.x[mi][j] = ld_coh128(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+  }
+}
+
 // Pins a loaded value at this point: code that uses it cannot be moved above the
 // pin (say, to a point shared by the chunk schedules, where it would wait for the
 // chunk's loads before the other chunks' loads are issued).
@@ -263,11 +341,20 @@ __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_beg
   }
 }
 
+// One output value of a phase: a tagged word when the phase hands its rows over
+// (yll), else an agent-coherent bf16 store.
+__device__ __forceinline__ void emit_coh(const LinearParams& p, size_t idx, uint16_t v) {
+  if (p.yll) st_coh32(p.yll + idx, (uint32_t)v | (p.tag << 16));
+  else st_coh16(p.y0 + idx, v);
+}
+
 // Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32
 // sums v; res holds the row's residual values (bf16 pairs), fetched at the start.
-template <int LW>
+// COH: agent-coherent stores (one 16-bit store a value; one or two words a lane).
+template <int LW, bool COH = false>
 __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW],
                                           const uint32_t (&res)[(LW + 1) / 2]) {
+  static_assert(!COH || LW <= 2, "coherent stores: one or two words a lane");
   if (m >= p.M) return;
   if constexpr (LW == 1) {
     if (p.epi == EPI_LL) {
@@ -285,7 +372,10 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
       for (int t = 0; t < LW; ++t) v[t] = round_bf16(v[t]) + bf16_to_f32((uint16_t)half_of<LW>(res, t, ncol & 1));
     }
     uint16_t* dst = p.y0 + (size_t)m * p.ldy + ncol;
-    if constexpr (LW == 1) {
+    if constexpr (COH) {
+#pragma unroll
+      for (int t = 0; t < LW; ++t) emit_coh(p, (size_t)m * p.ldy + ncol + t, (uint16_t)f32_to_bf16(v[t]));
+    } else if constexpr (LW == 1) {
       dst[0] = (uint16_t)f32_to_bf16(v[0]);
     } else {
       uint32_t packed[LW / 2];
@@ -318,11 +408,61 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
     } else if constexpr (LW == 4) {
       *reinterpret_cast<uint32_t*>(p.y0 + off) = pack_bf16x2(o0[0], o0[1]);
       if (p.epi == EPI_PAIRED) *reinterpret_cast<uint32_t*>(p.y1 + off) = pack_bf16x2(o1[0], o1[1]);
+    } else if constexpr (COH) {
+      emit_coh(p, off, (uint16_t)f32_to_bf16(o0[0]));   // SwiGLU output (paired outputs are not handed over)
     } else {
       p.y0[off] = (uint16_t)f32_to_bf16(o0[0]);
       if (p.epi == EPI_PAIRED) p.y1[off] = (uint16_t)f32_to_bf16(o1[0]);
     }
   }
+}
+
+// Reduce the waves' sums of one tile in LDS (one barrier, fixed order) and store:
+// every wave that had chunks (wave < nw) parks its sums (and, fused norm, its
+// rows' sums of squares) in red ([W][E][64]) and s_ss ([W][16]); then wave
+// 4 mi + i adds row i of m-tile mi over the waves in wave order and stores it.
+template <int MT, int LW, int W, bool NORM, bool COH>
+__device__ __forceinline__ void reduce_store(const LinearParams& p, int ncol, int nw, int st_mi, int st_i,
+                                             int st_local, int st_m, const float (&total)[MT][LW][4], float ss,
+                                             const uint32_t (&resv)[(LW + 1) / 2], float* red, float* s_ss) {
+  constexpr int E = MT * LW * 4;
+  static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if constexpr (NORM) {
+    ss += __shfl_xor(ss, 16, 64);   // the four k sub-blocks of A row c
+    ss += __shfl_xor(ss, 32, 64);
+  }
+  if (wave < nw) {
+    float* dst = red + wave * E * 64 + lane;
+#pragma unroll
+    for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+      for (int t = 0; t < LW; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
+    if constexpr (NORM) {
+      if (lane < 16) s_ss[wave * 16 + lane] = ss;
+    }
+  }
+  __syncthreads();
+  if (wave >= 4 * MT) return;
+  float v[LW];
+#pragma unroll
+  for (int t = 0; t < LW; ++t) v[t] = 0.0f;
+  float t_ss = 0.0f;   // fused norm: output row st_local of the tile is A row st_local (MT = 1)
+  for (int w = 0; w < nw; ++w) {
+    const float* src = red + w * E * 64 + lane;
+#pragma unroll
+    for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
+    if constexpr (NORM) t_ss += s_ss[w * 16 + st_local];
+  }
+  if constexpr (NORM) {
+    const float inv = round_bf16(1.0f / sqrtf(t_ss / (float)p.K + p.eps));
+#pragma unroll
+    for (int t = 0; t < LW; ++t) v[t] *= inv;
+  }
+  store_row<LW, COH>(p, ncol, st_m, v, resv);
 }
 
 // Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
@@ -435,50 +575,134 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   }
 
   // ---- reduce the waves of this workgroup in LDS: one barrier, fixed order ----
-  // Every wave that had chunks parks its sums (and, fused norm, its rows' sums of
-  // squares); then wave 4 mi + i adds row i of m-tile mi over the waves in wave
-  // order and stores it.
   const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
-  static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
-  {
-    __shared__ float red[W * E * 64];
-    __shared__ float s_ss[NORM ? W : 1][16];
-    if constexpr (NORM) {
-      ss += __shfl_xor(ss, 16, 64);   // the four k sub-blocks of A row c
-      ss += __shfl_xor(ss, 32, 64);
-    }
-    if (wave < nw) {
-      float* dst = red + wave * E * 64 + lane;
+  __shared__ float red[W * E * 64];
+  __shared__ float s_ss[NORM ? W : 1][16];
+  reduce_store<MT, LW, W, NORM, false>(p, ncol, nw, st_mi, st_i, st_local, st_m, total, ss, resv, red, &s_ss[0][0]);
+}
+
+// One workgroup's tile of a linear phase inside a launch that runs dependent
+// phases (the one-launch decode step): each wave requests the weights of all its
+// chunks, then wait() runs (workgroup-uniform; whatever the caller issues
+// there), then the activation rows and the residual come in with agent-coherent
+// loads, as tagged words awaited until they carry this launch's tag (xll / rll)
+// or as bf16 rows a previous launch wrote.  Chunk
+// ranges, arithmetic and reduction order are linear_tile's, so a plan gives the
+// same bits as the standalone kernel.  Straight schedules only, of at most NMAX
+// chunks a wave (3 with the fused norm, 6 without at CK = 2); returns false (and
+// computes nothing) for a plan beyond that, which the host rejects up front.
+// The output goes out as tagged words (yll) or agent-coherent bf16 stores; the
+// stores are not waited for (a consumer awaits the tags, or the launch's end).
+template <int MT, int LW, int CK, bool NORM, int NC, int NMAX>
+__device__ __forceinline__ void phase_weights(const LinearParams& p, int c_begin, int ncol, int r,
+                                              Chunk<MT, LW, CK> (&ch)[NMAX]) {
+#pragma unroll
+  for (int i = 0; i < NC; ++i) load_chunk_w<MT, LW, CK, NORM>(p, c_begin + i, ncol, r, ch[i]);
+}
+template <int MT, int LW, int CK, bool NORM, int NC, int NMAX>
+__device__ __forceinline__ void phase_compute(const LinearParams& p, int c_begin, int c, int r, int mbase,
+                                              Chunk<MT, LW, CK> (&ch)[NMAX], float (&total)[MT][LW][4],
+                                              float& ss, int zshift) {
+  if (p.xll) {
+    // tagged input words: all requested, then each group awaited in order
+    Tagged8 raw[NC][MT][CK];
+#pragma unroll
+    for (int i = 0; i < NC; ++i)
 #pragma unroll
       for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-        for (int t = 0; t < LW; ++t)
+        for (int j = 0; j < CK; ++j)
+          tagged_issue(p.xll + (size_t)tile_row(p, mbase, mi * 16 + c) * p.ldx + ((c_begin + i) * CK + j) * 32 + r * 8,
+                       raw[i][mi][j]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dst[((mi * LW + t) * 4 + i) * 64] = total[mi][t][i];
-      if constexpr (NORM) {
-        if (lane < 16) s_ss[wave][lane] = ss;
-      }
-    }
-    __syncthreads();
-    if (wave >= 4 * MT) return;
-    float v[LW];
+    for (int i = 0; i < NC; ++i)
 #pragma unroll
-    for (int t = 0; t < LW; ++t) v[t] = 0.0f;
-    float t_ss = 0.0f;   // fused norm: output row st_local of the tile is A row st_local (MT = 1)
-    for (int w = 0; w < nw; ++w) {
-      const float* src = red + w * E * 64 + lane;
+      for (int mi = 0; mi < MT; ++mi)
 #pragma unroll
-      for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
-      if constexpr (NORM) t_ss += s_ss[w][st_local];
-    }
-    if constexpr (NORM) {
-      const float inv = round_bf16(1.0f / sqrtf(t_ss / (float)p.K + p.eps));
+        for (int j = 0; j < CK; ++j)
+          ch[i].x[mi][j] = tagged_wait8(
+              p.xll + (size_t)tile_row(p, mbase, mi * 16 + c) * p.ldx + ((c_begin + i) * CK + j) * 32 + r * 8,
+              raw[i][mi][j], p.xtag, p.ctl);
+  } else {
 #pragma unroll
-      for (int t = 0; t < LW; ++t) v[t] *= inv;
-    }
-    store_row<LW>(p, ncol, st_m, v, resv);
+    for (int i = 0; i < NC; ++i) load_chunk_x_coh<MT, LW, CK>(p, c_begin + i, c, r, mbase, ch[i]);
   }
+#pragma unroll
+  for (int i = 0; i < NC; ++i) compute_chunk<MT, LW, CK, NORM>(ch[i], total, ss, zshift);
 }
 
+template <int MT, int LW, int W, int CK, bool NORM, int NMAX, class Wait>
+__device__ __forceinline__ bool linear_phase(const LinearParams& p, int G, int bx, int bz, float* red, float* s_ss,
+                                             const Wait& wait) {
+  static_assert(NMAX >= 1 && NMAX <= (NORM ? 3 : 6), "straight schedules of up to 3 chunks (fused norm) or 6");
+  static_assert(NMAX <= 3 || CK == 2, "more than three chunks in registers only at two k-steps a chunk");
+  const int tid = opaque_tid();
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15;
+  const int r = lane >> 4;
+  const int ncol = xcd_block(bx, G) * (16 * LW) + LW * c;
+  const int zshift = (ncol & 7) * 4;
+  const int mbase = bz * p.rt;
+  const int per_wave = (p.chunks + W - 1) / W;
+  const int c_begin = wave * per_wave;
+  const int n = min(c_begin + per_wave, p.chunks) - c_begin;   // wave-uniform; <= 0: no chunks
+  const bool fits = per_wave <= NMAX;
+
+  float total[MT][LW][4];
+#pragma unroll
+  for (int mi = 0; mi < MT; ++mi)
+#pragma unroll
+    for (int t = 0; t < LW; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) total[mi][t][i] = 0.0f;
+  float ss = 0.0f;
+  Chunk<MT, LW, CK> ch[NMAX];
+  if (fits) {
+    if (n == 1) phase_weights<MT, LW, CK, NORM, 1, NMAX>(p, c_begin, ncol, r, ch);
+    if constexpr (NMAX >= 2) if (n == 2) phase_weights<MT, LW, CK, NORM, 2, NMAX>(p, c_begin, ncol, r, ch);
+    if constexpr (NMAX >= 3) if (n == 3) phase_weights<MT, LW, CK, NORM, 3, NMAX>(p, c_begin, ncol, r, ch);
+    if constexpr (NMAX >= 4) if (n == 4) phase_weights<MT, LW, CK, NORM, 4, NMAX>(p, c_begin, ncol, r, ch);
+    if constexpr (NMAX >= 5) if (n == 5) phase_weights<MT, LW, CK, NORM, 5, NMAX>(p, c_begin, ncol, r, ch);
+    if constexpr (NMAX >= 6) if (n == 6) phase_weights<MT, LW, CK, NORM, 6, NMAX>(p, c_begin, ncol, r, ch);
+  }
+  wait();
+  // the row this lane stores and, with a residual, its values
+  const int st_mi = min(wave >> 2, MT - 1), st_i = wave & 3;
+  const int st_local = st_mi * 16 + r * 4 + st_i;
+  const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // M: none
+  uint32_t resv[(LW + 1) / 2];
+#pragma unroll
+  for (int i = 0; i < (LW + 1) / 2; ++i) resv[i] = 0u;
+  if constexpr (!NORM && LW == 1) {
+    const size_t ridx = (size_t)min(st_m, p.M - 1) * p.ldy + ncol;
+    if (p.rll) resv[0] = tagged_wait1(p.rll + ridx, p.rtag, p.ctl);
+    else if (p.residual) resv[0] = ld_coh32(reinterpret_cast<const uint32_t*>(p.residual + ridx - (ncol & 1)));
+  }
+  if (!fits) return false;
+  if (n == 1) phase_compute<MT, LW, CK, NORM, 1, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  if constexpr (NMAX >= 2) if (n == 2) phase_compute<MT, LW, CK, NORM, 2, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  if constexpr (NMAX >= 3) if (n == 3) phase_compute<MT, LW, CK, NORM, 3, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  if constexpr (NMAX >= 4) if (n == 4) phase_compute<MT, LW, CK, NORM, 4, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  if constexpr (NMAX >= 5) if (n == 5) phase_compute<MT, LW, CK, NORM, 5, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  if constexpr (NMAX >= 6) if (n == 6) phase_compute<MT, LW, CK, NORM, 6, NMAX>(p, c_begin, c, r, mbase, ch, total, ss, zshift);
+  const int nw = (p.chunks + per_wave - 1) / per_wave;
+  reduce_store<MT, LW, W, NORM, true>(p, ncol, nw, st_mi, st_i, st_local, st_m, total, ss, resv, red, s_ss);
+  return true;
+}
 
 }  // namespace t2i
+
+namespace t2i_host {
+// The decode linear's tile plan for an M x K x N product (defined with the
+// standalone kernel, which launches it; the one-launch decode step runs the same
+// plans so that both give the same bits).
+struct LinearPlan {
+  int MT, LW, W, CK;
+  int rt;       // rows per row tile (16 * MT, or fewer)
+  int mz;       // row tiles (grid.z)
+  int cbs;      // column blocks (grid.x)
+  int chunks;   // K / (32 * CK)
+};
+LinearPlan plan_linear(int M, int K, int N, bool paired);
+}  // namespace t2i_host

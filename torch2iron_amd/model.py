@@ -18,7 +18,10 @@ RMSNorms run inside the linears that consume them, and the RoPE, q/k-norm and
 KV write live in the attention prologue.
 
 A whole decode step is captured once into a HIP graph and replayed; token ids,
-positions and the output history stay on the device between steps.
+positions and the output history stay on the device between steps.  The
+layers can instead run as one cooperative launch per step (``t2i_decode_step``,
+``persistent=True``), whose phases give the separate kernels' bits; it measured
+slower (see ``Qwen3Model``) and is off by default.
 """
 
 from __future__ import annotations
@@ -268,17 +271,21 @@ class Qwen3Model:
     the whole batch.  Sequences never interact, so the tokens do not depend on
     the split.
 
-    ``fused=True`` runs each layer's RMSNorm + qkv projection + attention as one
-    cooperative launch (``ops.qkv_attention``, single stream only).  Off by
-    default: at batch 16, context 576 it measured 38.5 us a layer against 16.0 us
-    for the two separate kernels, of which about 18 us is the cooperative launch
-    itself (20.4 us kernel time).
+    Two one-launch alternatives, both off by default because they measured
+    slower than the separate kernels (Qwen3-0.6B, batch 16, context 576):
+    ``persistent=True`` runs every layer of a step in one cooperative launch
+    (``ops.decode_step``, single stream, shapes with a one-launch plan): 1.33
+    against 0.87 ms a step.  ``fused=True`` runs each layer's RMSNorm + qkv
+    projection + attention as one cooperative launch (``ops.qkv_attention``):
+    38.5 us a layer against 16.0 us for the two kernels, of which about 18 us is
+    the cooperative launch itself.
     """
 
     def __init__(self, tensors: dict, cfg: Qwen3Config, batch: int, ctx_cap: int, device, streams: int = 1,
-                 fused: bool = False):
+                 fused: bool = False, persistent: bool = False):
         self.cfg = cfg
         self.fused_front = fused
+        self.persistent = persistent
         self.batch = batch
         self.ctx_cap = ctx_cap
         self.device = torch.device(device)
@@ -334,8 +341,27 @@ class Qwen3Model:
             buf = DecodeBuffers(self.cfg, b1 - b0, self.device, x=self.x[b0:b1], xn=self.xn[b0:b1])
             stream = torch.cuda.Stream(self.device) if streams > 1 else None
             self.micro.append(_Micro(b0, b1, buf, stream))
+        self.step_table = self._step_table() if self.persistent and len(self.micro) == 1 else None
         self._head_graph = None
         self._captured = False
+
+    def _step_table(self):
+        """The one-launch step's layer table, or None when the shapes have no one-launch plan."""
+        c = self.cfg
+        if c.head_dim != 128:
+            return None
+        layers = [dict(qkv=L.w.qkv, o=L.w.o, gate_up=L.w.gate_up, down=L.w.down, ln1=L.w.ln1, ln2=L.w.ln2,
+                       q_norm=L.w.q_norm, k_norm=L.w.k_norm, k_cache=self.k_cache[i], v_cache=self.v_cache[i])
+                  for i, L in enumerate(self.layers)]
+        table = ops.DecodeLayerTable(layers, c.n_heads, c.n_kv_heads, self.device)
+        return table if table.workspace_bytes() > 0 else None
+
+    def check_errors(self) -> None:
+        """Raise if a wait inside the one-launch step timed out (synchronises)."""
+        if self.step_table is not None:
+            err = ops.decode_step_errors(self.step_table, self.device, workspace=self.micro[0].buf.workspace)
+            if err:
+                raise RuntimeError("t2i_decode_step: a wait inside the launch timed out (error word set)")
 
     @property
     def n_streams(self) -> int:
@@ -347,6 +373,10 @@ class Qwen3Model:
         c, b = self.cfg, m.buf
         ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens[m.b0:m.b1], x_out=b.x)
         pos = self.positions[m.b0:m.b1]
+        if self.step_table is not None:
+            ops.decode_step(self.step_table, b.xn, b.x, pos, c.eps, self.rope, rope_style=self.layers[0].rope_style,
+                            workspace=b.workspace)
+            return
         for i, layer in enumerate(self.layers):
             layer(b, pos, self.k_cache[i, m.b0:m.b1], self.v_cache[i, m.b0:m.b1], normed=(i == 0))
 
@@ -403,6 +433,7 @@ class Qwen3Model:
         self.positions.copy_(positions.to(self.device))
         self.forward_step(with_head=True, want_logits=want_logits)
         nxt = ops.keys_to_tokens(self.keys)
+        self.check_errors()
         return nxt.cpu(), (self.logits.clone() if want_logits else None)
 
     # ---- prompt pass (prefill) ----
@@ -579,6 +610,7 @@ class Qwen3Model:
                 ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
         ev[2].record()
         torch.cuda.synchronize(self.device)
+        self.check_errors()
         if timings is not None:
             timings["prompt_ms"] = ev[0].elapsed_time(ev[1])
             timings["decode_ms"] = ev[1].elapsed_time(ev[2])

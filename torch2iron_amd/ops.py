@@ -11,7 +11,7 @@ from __future__ import annotations
 import torch
 
 from torch2iron_amd import _lib
-from torch2iron_amd.formats import W4A16Weight
+from torch2iron_amd.formats import GROUP_SIZE, W4A16Weight
 
 BF16 = torch.bfloat16
 
@@ -334,6 +334,139 @@ def qkv_attention_errors(b: int, n_heads: int, n_kv_heads: int, device, workspac
     nbytes = lib.t2i_qkv_attention_workspace_bytes(b, n_heads, n_kv_heads)
     ws = (workspace or DEFAULT_WORKSPACE).get(("qkv_attn", b, n_heads, n_kv_heads), nbytes, device)
     return int(ws[off:off + 4].view(torch.int32).item())
+
+
+class DecodeLayerTable:
+    """The per-layer weights and caches of ``decode_step``: a device array of
+    ``t2i_decode_layer`` entries (18 pointers a layer, in the header's field
+    order), checked once here and kept alive with the tensors it points into.
+
+    ``layers``: one dict per layer with W4A16Weight ``qkv`` (q|k|v columns),
+    ``o``, ``gate_up`` (``interleave_gate_up`` layout), ``down``; bf16 ``ln1``,
+    ``ln2`` [hidden], ``q_norm``, ``k_norm`` [D]; bf16 caches ``k_cache``,
+    ``v_cache`` [B, Hkv, ctx_cap, D].
+    """
+
+    FIELDS = ("qkv", "o", "gate_up", "down")
+
+    def __init__(self, layers: list, n_heads: int, n_kv_heads: int, device):
+        if not layers:
+            raise ValueError("at least one layer")
+        d = layers[0]["q_norm"].numel()
+        kc0 = layers[0]["k_cache"]
+        if kc0.dim() != 4:
+            raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
+        self.batch, self.ctx_cap = kc0.shape[0], kc0.shape[2]
+        self.hidden = layers[0]["ln1"].numel()
+        self.intermediate = layers[0]["gate_up"].N // 2
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, d
+        self.n_layers = len(layers)
+        h, i = self.hidden, self.intermediate
+        shapes = {"qkv": (h, (n_heads + 2 * n_kv_heads) * d), "o": (n_heads * d, h), "gate_up": (h, 2 * i),
+                  "down": (i, h)}
+        rows = []
+        for li, lay in enumerate(layers):
+            row = []
+            for f in self.FIELDS:
+                w = lay[f]
+                _check_weight(w)
+                if (w.K, w.N) != shapes[f] or w.group_size != GROUP_SIZE:
+                    raise ValueError(f"layer {li}: {f} must be K x N = {shapes[f]}, group {GROUP_SIZE}")
+                row += [w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr()]
+            for f, n in (("ln1", h), ("ln2", h), ("q_norm", d), ("k_norm", d)):
+                _check_dev(f, lay[f], BF16)
+                if lay[f].numel() != n:
+                    raise ValueError(f"layer {li}: {f} must hold {n} values")
+                row.append(lay[f].data_ptr())
+            for f in ("k_cache", "v_cache"):
+                c = lay[f]
+                _check_dev(f, c, BF16)
+                if tuple(c.shape) != (self.batch, n_kv_heads, self.ctx_cap, d):
+                    raise ValueError(f"layer {li}: {f} must be [{self.batch}, {n_kv_heads}, {self.ctx_cap}, {d}]")
+                row.append(c.data_ptr())
+            rows.append(row)
+        self._keep = layers
+        self.table = torch.tensor(rows, dtype=torch.int64).to(device)
+
+    def workspace_bytes(self) -> int:
+        """0 when the library has no one-launch plan for these shapes."""
+        return _lib.load().t2i_decode_step_workspace_bytes(self.batch, self.n_layers, self.hidden, self.intermediate,
+                                                           self.n_heads, self.n_kv_heads)
+
+    def _key(self):
+        return ("decode_step", self.batch, self.n_layers, self.hidden, self.intermediate, self.n_heads,
+                self.n_kv_heads)
+
+
+def decode_step(table: DecodeLayerTable, xn0: torch.Tensor, x: torch.Tensor, positions: torch.Tensor,
+                eps: float, rope: torch.Tensor, rope_style: int = ROPE_HALVES,
+                workspace: Workspace | None = None) -> torch.Tensor:
+    """Every decoder layer of one decode step in one cooperative launch
+    (``t2i_decode_step``).  ``xn0`` bf16 ``[B, hidden]``: layer 0's normalised
+    input; ``x``: the residual stream, the embedding rows in and the last
+    layer's output out (updated in place and returned).  The launch takes one
+    workgroup per CU: it must not run concurrently with other GPU work."""
+    if not isinstance(table, DecodeLayerTable):
+        raise ValueError("table must be a DecodeLayerTable")
+    b, h = table.batch, table.hidden
+    for n, t in (("xn0", xn0), ("x", x), ("rope", rope)):
+        _check_dev(n, t, BF16)
+    _check_dev("positions", positions, torch.int32)
+    if xn0.numel() != b * h or x.numel() != b * h:
+        raise ValueError(f"xn0 and x must be [{b}, {h}]")
+    if positions.numel() != b:
+        raise ValueError(f"positions must hold {b} values")
+    if rope.dim() != 2 or rope.shape[0] < table.ctx_cap or rope.shape[1] != table.head_dim:
+        raise ValueError("rope table must be [>= ctx_cap, D]")
+    nbytes = table.workspace_bytes()
+    if nbytes == 0:
+        raise ValueError("no one-launch decode-step plan for these shapes")
+    ws = (workspace or DEFAULT_WORKSPACE).get(table._key(), nbytes, x.device)
+    lib = _lib.load()
+    rc = lib.t2i_decode_step(table.table.data_ptr(), table.n_layers, xn0.data_ptr(), x.data_ptr(), b, h,
+                             table.intermediate, table.n_heads, table.n_kv_heads, table.head_dim, GROUP_SIZE,
+                             positions.data_ptr(), rope.data_ptr(), int(rope_style), table.ctx_cap, float(eps),
+                             ws.data_ptr(), nbytes, _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_decode_step")
+    return x
+
+
+def _step_region(table: DecodeLayerTable, which: int, device, workspace: Workspace | None):
+    lib = _lib.load()
+    args = (table.batch, table.n_layers, table.hidden, table.intermediate, table.n_heads, table.n_kv_heads)
+    ws = (workspace or DEFAULT_WORKSPACE).get(table._key(), lib.t2i_decode_step_workspace_bytes(*args), device)
+    return ws, lib.t2i_decode_step_offset(*args, which)
+
+
+def decode_step_errors(table: DecodeLayerTable, device, workspace: Workspace | None = None) -> int:
+    """The error word of the one-launch step's workspace (non-zero: a wait timed
+    out).  Synchronises with the device."""
+    ws, off = _step_region(table, 4, device, workspace)
+    return int(ws[off:off + 4].view(torch.int32).item())
+
+
+def decode_step_intermediates(table: DecodeLayerTable, device, workspace: Workspace | None = None) -> dict:
+    """Copies of the last one-launch step's per-layer activations from its
+    workspace's tagged words (for checks): ``ctx`` [L, B, Hq*D], ``xmid``
+    [L, B, hidden] (after attention), ``h`` [L, B, intermediate] (SwiGLU), ``x``
+    [L-1, B, hidden] (between layers), ``qkv`` [B, (Hq+2Hkv)*D] (the last layer's
+    projection)."""
+    b, L, h, i, d = table.batch, table.n_layers, table.hidden, table.intermediate, table.head_dim
+    hq, hkv = table.n_heads, table.n_kv_heads
+    def low16(words):
+        v = words.to(torch.int64) & 0xFFFF
+        return torch.where(v >= 32768, v - 65536, v).to(torch.int16).view(BF16)
+
+    views = {}
+    for which, name, shape in ((0, "ctx", (L, b, hq * d)), (1, "xmid", (L, b, h)), (2, "h", (L, b, i)),
+                               (3, "x", (max(L - 1, 1), b, h))):
+        ws, off = _step_region(table, which, device, workspace)
+        n = shape[0] * shape[1] * shape[2]
+        views[name] = low16(ws[off:off + 4 * n].view(torch.int32)).view(shape)
+    nq = (hq + 2 * hkv) * d
+    ws, _ = _step_region(table, 0, device, workspace)
+    views["qkv"] = low16(ws[:b * nq * 8].view(torch.int64)).view(b, nq)
+    return views
 
 
 def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_kv_heads: int,
