@@ -378,7 +378,10 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
   // A release fetch_add and an acquire fence give the same order through the
   // memory model, but their L2 write-back and invalidate (buffer_wbl2 / buffer_inv
   // at agent scope) cost 12.5 us and 3.1 us per call at batch 16, context 577
-  // (25.2 and 15.8 us against 12.7 us), measured.
+  // (25.2 and 15.8 us against 12.7 us), measured.  Counting the arrival without
+  // waiting for the stores, with the states as flagged 64-bit words that the
+  // merger polls, measured slower too (13.4 against 11.8 us per call: the merger
+  // then meets the last chunk's words still in flight and polls again).
   wait_stores();
   __syncthreads();
   if (tid == 0) {

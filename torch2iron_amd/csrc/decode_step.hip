@@ -348,10 +348,10 @@ DsPlan ds_plan(int cus, int B, int L, int H, int I, int Hq, int Hkv) {
   if (H <= 0 || H % 128 || I <= 0 || I % 128) return pl;
   const int D = ATT_D;
   const int Nqkv = (Hq + 2 * Hkv) * D;
-  if (!ds_phase(plan_linear(B, H, Nqkv, false), 1, DS_CHUNKS, &pl.qkv)) return pl;
-  if (!ds_phase(plan_linear(B, Hq * D, H, false), 1, DS_CHUNKS, &pl.o)) return pl;
-  if (!ds_phase(plan_linear(B, H, 2 * I, true), 2, DS_CHUNKS, &pl.gu)) return pl;
-  if (!ds_phase(plan_linear(B, I, H, false), 1, DS_CHUNKS_DOWN, &pl.dn)) return pl;
+  if (!ds_phase(plan_linear(B, H, Nqkv, false, true), 1, DS_CHUNKS, &pl.qkv)) return pl;
+  if (!ds_phase(plan_linear(B, Hq * D, H, false, false), 1, DS_CHUNKS, &pl.o)) return pl;
+  if (!ds_phase(plan_linear(B, H, 2 * I, true, true), 2, DS_CHUNKS, &pl.gu)) return pl;
+  if (!ds_phase(plan_linear(B, I, H, false, false), 1, DS_CHUNKS_DOWN, &pl.dn)) return pl;
   pl.G = cus;
   pl.U = B * Hkv;
   if (pl.U > pl.G) return pl;

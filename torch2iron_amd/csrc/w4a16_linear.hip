@@ -458,7 +458,7 @@ void finish_plan(LinearPlan& pl, int M, int K, int N) {
 // the fp32 partials and an arrival counter add memory round trips that cost
 // more than the parallelism they add at these sizes, so K is only split
 // between the waves of a workgroup.
-LinearPlan plan_linear(int M, int K, int N, bool paired) {
+LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm) {
   LinearPlan pl{};
   pl.MT = 1;
   pl.CK = 4;
@@ -467,14 +467,15 @@ LinearPlan plan_linear(int M, int K, int N, bool paired) {
     // (N not a multiple of 32: 16-column blocks are the only whole ones)
     pl.LW = 1; pl.W = 16; pl.CK = 2;
   } else if ((N / 32) * mz <= 256 || N % 64) {
-    // Paired (gate/up) outputs take 16 waves of 2-step chunks, the configuration
-    // the one-launch decode step runs (its workgroups have 16 waves and 128
-    // registers a lane), so both paths give the same bits; 8 waves of 4-step
-    // chunks measured 0.1-0.2 us faster on the Qwen3-0.6B gate_up at M <= 16
-    // (4.62 against 4.73 us at M = 16) but need 148 registers a lane.
+    // The fused-norm paired (RMSNorm + gate/up) output takes 16 waves of 2-step
+    // chunks, the configuration the one-launch decode step runs (its workgroups
+    // have 16 waves and 128 registers a lane), so both paths give the same bits;
+    // 8 waves of 4-step chunks measured 0.1-0.2 us faster on the Qwen3-0.6B
+    // gate_up at M <= 16 (4.62 against 4.73 us at M = 16) but need 148 registers
+    // a lane with the norm, and stay the plan without it.
     pl.LW = 2;
-    pl.W = paired ? 16 : 8;
-    pl.CK = paired ? 2 : 4;
+    pl.W = paired && norm ? 16 : 8;
+    pl.CK = paired && norm ? 2 : 4;
   } else {
     pl.LW = 4; pl.W = 8;
   }
@@ -577,7 +578,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p);
     return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
   }
-  const LinearPlan pl = plan_linear(M, K, N, paired);
+  const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr);
   LinearParams p{};
   p.x = x;
   p.qw = reinterpret_cast<const uint32_t*>(qweight);

@@ -704,5 +704,5 @@ struct LinearPlan {
   int cbs;      // column blocks (grid.x)
   int chunks;   // K / (32 * CK)
 };
-LinearPlan plan_linear(int M, int K, int N, bool paired);
+LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm);
 }  // namespace t2i_host
