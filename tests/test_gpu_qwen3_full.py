@@ -10,7 +10,11 @@ of tokens, so every token must match) and ``centered`` (diverse tokens).
 
 Bars, per sequence, against the fp32 oracle (the reference runtime's default dtype):
 * the sequences that match all 32 tokens are counted and reported, and must reach
-  the floor written per draw below;
+  the floor written per draw below (all 16 for the uniform draw);
+* the tokens matched before each sequence's first divergence, summed over the
+  batch, reach at least half of what the bf16-mode oracle's own greedy tokens
+  match (its rounding is as legitimate as the GPU's, and this is the scale of
+  agreement bf16 compute allows);
 * a sequence that diverges does so at a near-tie: the fp32 top-2 margin at its
   first differing step is at most twice the logit shift that bf16 rounding itself
   causes there (the oracle's bf16 mode against its fp32 mode, teacher-forced along
@@ -24,9 +28,11 @@ Bars, per sequence, against the fp32 oracle (the reference runtime's default dty
   oracle's do, within 25 %.
 
 The centered draw is chaotic under bf16 rounding: the bf16-mode oracle's own
-greedy tokens match its fp32 mode on all 32 steps for only 3 of the 16 sequences,
-so the free-running exact-match floor there is low and the teacher-forced checks
-carry the weight.
+greedy tokens match its fp32 mode on all 32 steps for only 3 of the 16 sequences
+(first divergences 1-21 steps in the others, 197 matched steps of 512), and a
+change of fp32 summation order alone moves the GPU between 0 and 1 such
+sequences, so its exact-match floor is 0; the matched-prefix, near-tie and
+teacher-forced checks carry the weight there.
 """
 
 from pathlib import Path
@@ -41,7 +47,7 @@ pytestmark = pytest.mark.gpu
 FIXTURE = Path(__file__).resolve().parent / "golden" / "qwen3_0.6b_greedy.npz"
 DRAWS = {"uniform": 0, "centered": 1}
 # sequences (of 16) that must match the fp32 oracle on all 32 steps
-EXACT_FLOOR = {"uniform": 16, "centered": 1}
+EXACT_FLOOR = {"uniform": 16, "centered": 0}
 
 
 @pytest.fixture(scope="module")
@@ -77,6 +83,11 @@ def test_full_model_greedy_matches_oracle(gpu, golden, draw):
             assert margins[i, s] <= 2.0 * noise[i, s], \
                 f"sequence {i} step {s}: margin {margins[i, s]:.3f} > 2 x bf16 noise {noise[i, s]:.3f}"
     assert exact >= EXACT_FLOOR[draw], f"{exact} < {EXACT_FLOOR[draw]} sequences match all {new} steps"
+    t16 = golden[f"{draw}_tokens16"]
+    prefix16 = sum(int(np.argmin(t16[i] == ref[i])) if (t16[i] != ref[i]).any() else new for i in range(b))
+    print(f"{draw}: {sum(steps_matched)} steps matched before the first divergence (bf16-mode oracle {prefix16})",
+          flush=True)
+    assert sum(steps_matched) >= 0.5 * prefix16
 
     # logits along the oracle's tokens (teacher forcing), on the fixture's vocabulary sample
     sub_steps = [int(s) for s in golden["sub_steps"]]
