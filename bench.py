@@ -288,6 +288,21 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
             "first_token_equal_to_prefill": bool(torch.equal(tf[:, 0], toks[:, 0])),
             "tokens_equal_to_prefill_run": bool(torch.equal(tf, toks))}
         log(f"teacher-forced prompt: {tm['prompt_ms']:.1f} ms")
+    # every layer of a step as one cooperative launch (t2i_decode_step): built and
+    # tested, off by default because it measures slower; timed here beside the graph
+    one_launch = None
+    model.persistent = True
+    model.set_streams(1)
+    if model.step_table is not None:
+        model.generate(prompt[:, :8], new_tokens)     # warm-up and capture
+        tm = {}
+        ol = model.generate(prompt, new_tokens, timings=tm)
+        one_launch = {"ms_per_decode_step": round(tm["decode_ms"] / (new_tokens - 1), 4),
+                      "decode_tokens_per_s": round(batch * (new_tokens - 1) / (tm["decode_ms"] * 1e-3), 1),
+                      "sequences_equal_to_graph_path": int((ol == toks).all(dim=1).sum()), "of": batch}
+        log(f"one-launch step (t2i_decode_step): {one_launch['ms_per_decode_step']:.3f} ms/step")
+    model.persistent = False
+    model.set_streams(1)
     # the fp32 oracle's first 32 tokens for this exact model and prompt (written offline by
     # tests/golden/make_qwen3_greedy_golden.py from the same seeds)
     oracle = {}
@@ -306,6 +321,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         **best,
         "by_streams": {str(k): v for k, v in runs.items()},
         "teacher_forced_prompt": teacher_forced,
+        "one_launch_step": one_launch,
         "greedy_parity": oracle,
         "first_tokens": toks[:2, :8].tolist(),
     }

@@ -357,11 +357,15 @@ class Qwen3Model:
         return table if table.workspace_bytes() > 0 else None
 
     def check_errors(self) -> None:
-        """Raise if a wait inside the one-launch step timed out (synchronises)."""
+        """Raise if a wait inside a one-launch path timed out (synchronises)."""
+        c = self.cfg
         if self.step_table is not None:
-            err = ops.decode_step_errors(self.step_table, self.device, workspace=self.micro[0].buf.workspace)
-            if err:
+            if ops.decode_step_errors(self.step_table, self.device, workspace=self.micro[0].buf.workspace):
                 raise RuntimeError("t2i_decode_step: a wait inside the launch timed out (error word set)")
+        elif self.layers and self.layers[0].fused:
+            m = self.micro[0]
+            if ops.qkv_attention_errors(m.b1 - m.b0, c.n_heads, c.n_kv_heads, self.device, workspace=m.buf.workspace):
+                raise RuntimeError("t2i_qkv_attention: a wait inside the launch timed out (error word set)")
 
     @property
     def n_streams(self) -> int:
