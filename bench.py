@@ -131,33 +131,118 @@ class Sweep:
         return self.copies * self.per_copy / 1e6
 
     def run(self, steps, warmup):
-        torch = self.torch
-        for _ in range(warmup):
-            for gr in self.groups:
-                gr["replay"]()
-        torch.cuda.synchronize()
-        start = torch.cuda.Event(enable_timing=True)
-        marks = [[torch.cuda.Event(enable_timing=True) for _ in self.groups] for _ in range(steps)]
-        start.record()
-        for s in range(steps):
-            for i, gr in enumerate(self.groups):
-                gr["replay"]()
-                marks[s][i].record()
-        torch.cuda.synchronize()
-        total_ms = start.elapsed_time(marks[-1][-1])
-        per_group = [0.0] * len(self.groups)
-        for s in range(steps):
-            prev = start if s == 0 else marks[s - 1][-1]
-            for i in range(len(self.groups)):
-                per_group[i] += prev.elapsed_time(marks[s][i])
-                prev = marks[s][i]
-        per_group = [t / steps for t in per_group]
-        return total_ms, per_group
+        return run_groups(self.groups, steps, warmup)
 
     def breakdown(self, per_group):
         return {gr["label"]: {"TBps": round(gr["bytes"] / (t * 1e-3) / 1e12, 4),
                               "us_per_launch": round(t * 1e3 / gr["launches"], 3)}
                 for gr, t in zip(self.groups, per_group)}
+
+
+def run_groups(groups, steps: int, warmup: int):
+    """Replay every group's graph in order, ``steps`` times after ``warmup``; returns
+    the total ms and the average ms of each group (events between the groups)."""
+    import torch
+    for _ in range(warmup):
+        for gr in groups:
+            gr["replay"]()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in groups] for _ in range(steps)]
+    start.record()
+    for s in range(steps):
+        for i, gr in enumerate(groups):
+            gr["replay"]()
+            marks[s][i].record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(marks[-1][-1])
+    per_group = [0.0] * len(groups)
+    for s in range(steps):
+        prev = start if s == 0 else marks[s - 1][-1]
+        for i in range(len(groups)):
+            per_group[i] += prev.elapsed_time(marks[s][i])
+            prev = marks[s][i]
+    return total_ms, [t / steps for t in per_group]
+
+
+def read_ceiling(sweep_groups, pool_bytes: int, dev, steps: int, warmup: int, lpts=(1, 2, 4, 8)):
+    """The HBM read ceiling beside the sweep (``t2i_stream_read``, a kernel that only
+    streams bytes).  Its twin of the sweep reads, per group, the group's algorithmic
+    bytes per launch with the same number of launches, in the same M-major order,
+    each launch a fresh slice of a pool larger than twice the MALL (the same reuse
+    distance as the weight copies); per group the fastest loads-per-thread variant
+    counts.  The bulk leg reads one 1 GiB buffer per launch."""
+    import torch
+    from torch2iron_amd import ops
+    pool = torch.randint(0, 256, (pool_bytes,), dtype=torch.uint8, device=dev,
+                         generator=torch.Generator(device=dev).manual_seed(11))
+    out = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+    best = None
+    for lpt in lpts:
+        groups, off = [], 0
+        for gr in sweep_groups:
+            per = -(-(gr["bytes"] // gr["launches"]) // 16) * 16
+            slices = []
+            for _ in range(gr["launches"]):
+                if off + per > pool_bytes:
+                    off = 0
+                slices.append(off)
+                off += -(-per // 256) * 256
+            ops.stream_read(pool, per, slices[0], lpt, out=out)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for o in slices:
+                    ops.stream_read(pool, per, o, lpt, out=out)
+            groups.append(dict(label=gr["label"], replay=g.replay, bytes=per * gr["launches"],
+                               launches=gr["launches"], graph=g))
+        _, per_group = run_groups(groups, steps, warmup)
+        if best is None:
+            best = [dict(label=g["label"], bytes=g["bytes"], launches=g["launches"], ms=t, lpt=lpt)
+                    for g, t in zip(groups, per_group)]
+        else:
+            for b, t in zip(best, per_group):
+                if t < b["ms"]:
+                    b["ms"], b["lpt"] = t, lpt
+        del groups
+    total_bytes = sum(b["bytes"] for b in best)
+    total_ms = sum(b["ms"] for b in best)
+    launches = sum(b["launches"] for b in best)
+    del pool
+    torch.cuda.empty_cache()
+    # bulk: one 1 GiB read a launch
+    big = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(7)
+    bulk = {}
+    for lpt in lpts:
+        ops.stream_read(big, loads_per_thread=lpt, out=torch.empty(1 << 20, dtype=torch.int32, device=dev))
+        bout = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ops.stream_read(big, loads_per_thread=lpt, out=bout)
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        bulk[lpt] = (1 << 30) / (e0.elapsed_time(e1) / steps * 1e-3) / 1e12
+        del g, bout
+    del big
+    torch.cuda.empty_cache()
+    bulk_lpt = max(bulk, key=bulk.get)
+    return {
+        "kernel": "stream_read_kernel (t2i_stream_read: 16-byte non-temporal loads, XOR per wave)",
+        "same_launches_TBps": round(total_bytes / (total_ms * 1e-3) / 1e12, 4),
+        "same_launches_us_per_launch": round(total_ms * 1e3 / launches, 3),
+        "bulk_1GiB_TBps": round(bulk[bulk_lpt], 4),
+        "bulk_loads_per_thread": bulk_lpt,
+        "bulk_by_loads_per_thread": {str(k): round(v, 4) for k, v in bulk.items()},
+        "breakdown": {b["label"]: {"TBps": round(b["bytes"] / (b["ms"] * 1e-3) / 1e12, 4),
+                                   "us_per_launch": round(b["ms"] * 1e3 / b["launches"], 3),
+                                   "loads_per_thread": b["lpt"]} for b in best},
+    }
 
 
 def rate(sweep: Sweep, steps: int, warmup: int):
@@ -476,6 +561,7 @@ def main():
     cold_pool_mb = cold.pool_mb
     cold_copies = cold.copies
     cold_bytes = cold.bytes_per_step
+    cold_groups = [dict(label=gr["label"], bytes=gr["bytes"], launches=gr["launches"]) for gr in cold.groups]
 
     if args.calibrate_copy:
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
@@ -486,6 +572,15 @@ def main():
         del src, dst
     del cold
     torch.cuda.empty_cache()
+
+    ceiling = None
+    if not args.eager:
+        log("HBM read ceiling: the sweep's byte counts and launches through a read-only kernel, and a 1 GiB read")
+        ceiling = read_ceiling(cold_groups, args.pool_mb << 20, dev, args.steps, args.warmup)
+        log(f"read ceiling: {ceiling['same_launches_TBps']:.3f} TB/s at the sweep's launches "
+            f"({ceiling['same_launches_us_per_launch']:.2f} us per launch); bulk {ceiling['bulk_1GiB_TBps']:.3f} TB/s")
+        ceiling["frac_of_same_launches"] = round(value / ceiling["same_launches_TBps"], 4)
+        ceiling["frac_of_bulk"] = round(value / ceiling["bulk_1GiB_TBps"], 4)
 
     extra = {}
     if not args.skip_extra:
@@ -578,6 +673,7 @@ def main():
             "kernel": "w4a16_mfma_kernel",
             "avg_launch_us": round(avg_launch_us, 3),
             "launch_floor_us": None if floor_us is None else round(floor_us, 3),
+            "read_ceiling": ceiling,
             "kernel_time": None if not kernels else {
                 "avg_kernel_us": kernels.get("avg_kernel_us"),
                 "algorithmic_bytes_per_launch": kernels.get("algorithmic_bytes_per_launch"),

@@ -307,6 +307,18 @@ int t2i_greedy_advance(const uint64_t* argmax_keys, int32_t B, int32_t* tokens,
 int t2i_prompt_advance(const int32_t* prompt, int32_t B, int32_t P, int32_t* tokens,
                        int32_t* positions, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Measurement helper, no counterpart in the reference: the HBM read ceiling that
+ * a linear's bandwidth is compared with.  Reads `bytes` (a positive multiple of
+ * 16) from src with 16-byte loads, loads_per_thread (1, 2, 4 or 8) per thread in
+ * 256-thread workgroups, and writes the XOR of each wave's 32-bit words to out:
+ * t2i_stream_read_out_words(bytes, loads_per_thread) words, word w covering the
+ * 64 * loads_per_thread 16-byte words of wave w (0 when the arguments are invalid).
+ */
+int64_t t2i_stream_read_out_words(size_t bytes, int32_t loads_per_thread);
+int t2i_stream_read(const void* src, size_t bytes, int32_t loads_per_thread, uint32_t* out,
+                    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

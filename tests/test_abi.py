@@ -115,6 +115,12 @@ def test_other_entry_points_validate():
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151930, 1024, None, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151936, 1024, None, None, None) == _lib.T2I_ERR_NULL
     assert lib.t2i_w4a16_dequant_f32(FAKE, FAKE, FAKE, 1024, 3072, 128, None, None) == _lib.T2I_ERR_NULL
+    assert lib.t2i_stream_read(FAKE, 4096, 4, None, None) == _lib.T2I_ERR_NULL
+    assert lib.t2i_stream_read(FAKE, 4100, 4, FAKE, None) == _lib.T2I_ERR_SHAPE    # not a multiple of 16
+    assert lib.t2i_stream_read(FAKE, 4096, 3, FAKE, None) == _lib.T2I_ERR_VALUE    # loads per thread
+    assert lib.t2i_stream_read(FAKE + 8, 4096, 4, FAKE, None) == _lib.T2I_ERR_ALIGN
+    assert lib.t2i_stream_read_out_words(4096 * 4 * 3 + 16, 4) == 4 * 4   # 4 workgroups of 16 KB, 4 waves each
+    assert lib.t2i_stream_read_out_words(4096, 3) == 0
 
 
 def test_python_layer_rejects_cpu_tensors_and_bad_shapes():

@@ -64,6 +64,8 @@ SIGNATURES = {
     "t2i_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_greedy_advance": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "t2i_prompt_advance": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_stream_read_out_words": (ctypes.c_int64, [c_size_t, c_int32]),
+    "t2i_stream_read": (c_int32, [c_void_p, c_size_t, c_int32, c_void_p, c_void_p]),
 }
 
 _LIB = None

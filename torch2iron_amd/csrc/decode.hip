@@ -429,7 +429,12 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 // workgroups of 7 or 8 tiles), each workgroup taking a contiguous range: with
 // 8 tiles a workgroup (1187 workgroups) 163 CUs took a fifth one, ~8 % over an
 // even split.  64-row waves (594 workgroups: CUs with 3 against 2 set the tail)
-// and 2 or 8 waves a workgroup were slower.
+// and 2 or 8 waves a workgroup were slower.  So were grids whose workgroups are
+// all resident from the start (one to four a CU, up to 38 tiles a workgroup dealt
+// to its waves in a stride: 67-69 against 61 us at B = 16), and loads that take
+// 64 contiguous bytes of each row per instruction instead of 16-byte pieces 32
+// bytes apart (no change).  A read-only kernel streams at 6.7 TB/s against this
+// kernel's 5.1: every load instruction here spans 16 rows of the table 2 KB apart.
 constexpr int LMH_WAVES = 4;
 constexpr int LMH_COLS = 32;                // vocab columns per wave
 constexpr int LMH_TILES = LMH_COLS / 16;    // MFMA n-tiles per wave

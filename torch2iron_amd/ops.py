@@ -601,3 +601,29 @@ def prompt_advance(prompt, tokens, positions):
     rc = lib.t2i_prompt_advance(prompt.data_ptr(), b, plen, tokens.data_ptr(), positions.data_ptr(),
                                 _lib.stream_handle(tokens.device))
     _lib.check(rc, "t2i_prompt_advance")
+
+
+def stream_read(src, nbytes: int | None = None, offset: int = 0, loads_per_thread: int = 4, out=None):
+    """Read ``nbytes`` of ``src`` from byte ``offset`` with the HBM read-ceiling
+    kernel (``t2i_stream_read``) and return the per-wave XOR words (uint32 bit
+    patterns in an int32 tensor).  ``offset`` and ``nbytes`` must be multiples of
+    16; ``out`` may be a preallocated int32 tensor of at least the word count."""
+    _check_dev("src", src)
+    total = src.numel() * src.element_size()
+    nbytes = total - offset if nbytes is None else nbytes
+    if offset < 0 or nbytes <= 0 or offset % 16 or nbytes % 16 or offset + nbytes > total:
+        raise ValueError(f"bytes [{offset}, {offset + nbytes}) must be 16-aligned and inside the {total}-byte source")
+    lib = _lib.load()
+    words = lib.t2i_stream_read_out_words(nbytes, loads_per_thread)
+    if words <= 0:
+        raise ValueError(f"loads_per_thread must be 1, 2, 4 or 8 (got {loads_per_thread})")
+    if out is None:
+        out = torch.empty(words, dtype=torch.int32, device=src.device)
+    else:
+        _check_dev("out", out, torch.int32)
+        if out.numel() < words:
+            raise ValueError(f"out holds {out.numel()} words, {words} needed")
+    rc = lib.t2i_stream_read(src.data_ptr() + offset, nbytes, loads_per_thread, out.data_ptr(),
+                             _lib.stream_handle(src.device))
+    _lib.check(rc, "t2i_stream_read")
+    return out[:words]
