@@ -46,13 +46,21 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 
 // ============================================================================
 // Prompt-sized GEMM (hundreds of rows and more): a 64 x 128 output tile per
-// 256-thread workgroup, 4 waves of 32 x 64 (2 along M x 2 along N), one 128-k
-// tile (= one quantisation group) per step.  51 KB of LDS and at most 168
+// 256-thread workgroup, 4 waves of 64 x 32 (1 along M x 4 along N), one 128-k
+// tile (= one quantisation group) per step.  Each wave rebuilds the bf16 operand
+// of its own 32 columns only, and the weights are unpacked in k order
+// (b_operand_kord), so the activation fragments go to the MFMA as they lie in
+// LDS: 158 VALU instructions a wave per k-tile against 238 for 2 x 2 waves of
+// 32 x 64 (which rebuilt each column's operand in both wave rows and permuted
+// every activation fragment), for 48 MFMAs against 40 (each wave sums all 64
+// rows).  Measured at 8192 rows: qkv 117 -> 107 us, gate_up with SwiGLU 184 ->
+// 170 us, down with the residual 90 -> 79-82 us, o_proj unchanged at ~60 us;
+// the outputs are bit-identical.  51 KB of LDS and at most 168
 // registers a lane (launch bounds) let three workgroups share a CU, so the
 // others' k-loops cover one's barriers, prologue and epilogue, and the VALU and
 // MFMA work of three waves a SIMD interleave (measured against two workgroups a
-// CU with three stage buffers: gate_up at 8192 rows 208 -> 183 us, qkv 127 ->
-// 113 us; and against one 128 x 128 workgroup of 8 waves a CU before that).
+// CU with three stage buffers, for this tile too: qkv 107 -> 117 us, o_proj 62
+// -> 70 us; and against one 128 x 128 workgroup of 8 waves a CU before that).
 //   * Every operand of a k-tile (activations, packed weights, the group's scale
 //     and zero words) is loaded straight into LDS (global_load_lds, no
 //     registers); two stage buffers: k-tile kt + 1 loads while kt is computed.
@@ -73,8 +81,10 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 constexpr int GM_BM = 64, GM_BN = 128;
 constexpr int GM_WAVES = 4;
 constexpr int GM_THREADS = 64 * GM_WAVES;
-constexpr int GM_WN = GM_BN / 64;                        // waves along N (64 columns each)
-constexpr int GM_MF = GM_BM / (GM_WAVES / GM_WN) / 16;   // 16-row fragments per wave (2)
+constexpr int GM_WCOLS = 32;                             // columns per wave
+constexpr int GM_WN = GM_BN / GM_WCOLS;                  // waves along N (4)
+constexpr int GM_NJ = GM_WCOLS / 16;                     // 16-column n-tiles per wave (2)
+constexpr int GM_MF = GM_BM / (GM_WAVES / GM_WN) / 16;   // 16-row fragments per wave (4)
 constexpr int GM_AF = GM_BM / 16 * KSG;       // A fragments per k-tile (1 KB each)
 constexpr int GM_AF_W = GM_AF / GM_WAVES;     // issued per wave
 constexpr int GM_BPAIR = GS / 8 / 2;          // qweight row pairs per k-tile (1 KB each with GM_BN = 128)
@@ -83,10 +93,10 @@ constexpr int GM_BPAIR_W = 2 * GM_BROW + 32;  // words per padded row pair
 constexpr int GM_BPAIR_PW = GM_BPAIR / GM_WAVES;   // weight row pairs loaded per wave
 static_assert(GM_BPAIR % GM_WAVES == 0 && GM_BN == 128, "whole weight row pairs per wave, 1 KB loads");
 constexpr int GM_STAGES = 2;
-// epilogue: each wave parks its 32 x 64 results as bf16 in LDS (rows padded to
-// 72 values) and stores them back as 16-byte row pieces
-constexpr int GM_EP_LD = 64 + 8;
-constexpr int GM_EP_WAVE = 2 * 32 * GM_EP_LD;   // two regions (paired: gate and up outputs)
+// epilogue: each wave parks its 64 x 32 results as bf16 in LDS (rows padded to
+// 40 values) and stores them back as 16-byte row pieces
+constexpr int GM_EP_LD = GM_WCOLS + 8;
+constexpr int GM_EP_WAVE = 2 * GM_BM * GM_EP_LD;   // two regions (paired: gate and up outputs)
 
 struct GemmStage {
   u32x4 a[GM_AF * 64];
@@ -94,6 +104,7 @@ struct GemmStage {
   uint32_t qs[64];          // fp16 scales of the tile's 128 columns, two per word
   uint32_t qz[64];          // qzeros words of the tile's columns (16 used)
 };
+static_assert(GM_WAVES * GM_EP_WAVE * 2 <= (int)sizeof(GemmStage) * GM_STAGES, "epilogue fits in the stages");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void global_void_t;
@@ -164,19 +175,19 @@ __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0
 // Fragments of k-step ks: A of this wave's rows, B of its columns.
 struct GemmFrags {
   u32x4 a[GM_MF];
-  uint32_t b[4];
+  uint32_t b[GM_NJ];
 };
 
-// abase: this lane's slot of the wave's first A fragment; bbase: this lane's word
-// of k-step 0, fragment 0 (qweight row r = lane / 16, column 64 wn + c).  Every
+// abase: this lane's slot of the first A fragment; bbase: this lane's word of
+// k-step 0, fragment 0 (qweight row r = lane / 16, column 32 wn + c).  Every
 // other read is a constant offset from these.
 template <int KS, int I = 0>
 __device__ __forceinline__ void gemm_read(uint32_t abase, uint32_t bbase, GemmFrags& f) {
   if constexpr (I < GM_MF) {
     f.a[I] = lds_read16<(I * KSG + KS) * 1024>(abase);
     gemm_read<KS, I + 1>(abase, bbase, f);
-  } else if constexpr (I < GM_MF + 4) {
-    constexpr int j = I - GM_MF;   // qweight row 4 KS + r, column 64 wn + 16 j + c
+  } else if constexpr (I < GM_MF + GM_NJ) {
+    constexpr int j = I - GM_MF;   // qweight row 4 KS + r, column 32 wn + 16 j + c
     f.b[j] = lds_read4<4 * (2 * KS * GM_BPAIR_W + 16 * j)>(bbase);
     gemm_read<KS, I + 1>(abase, bbase, f);
   }
@@ -186,65 +197,64 @@ __device__ __forceinline__ void gemm_read(uint32_t abase, uint32_t bbase, GemmFr
 // the uses of the waited fragments after the wait).
 template <int N>
 __device__ __forceinline__ void wait_lds(GemmFrags& f) {
-  static_assert(N == 0 || N == 2 + 4, "one k-step of fragments or none");
+  static_assert(GM_MF == 4 && GM_NJ == 2, "the waits tie four A fragments and two B words");
+  static_assert(N == 0 || N == GM_MF + GM_NJ, "one k-step of fragments or none");
   if constexpr (N == 0)
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.b[0]), "+v"(f.b[1]), "+v"(f.b[2]),
-                 "+v"(f.b[3]));
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
+                 "+v"(f.b[1]));
   else
-    asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.b[0]), "+v"(f.b[1]), "+v"(f.b[2]),
-                 "+v"(f.b[3]));
+    asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(f.a[0]), "+v"(f.a[1]), "+v"(f.a[2]), "+v"(f.a[3]), "+v"(f.b[0]),
+                 "+v"(f.b[1]));
 }
 
 // k-step KS of a k-tile: read k-step KS + 1's fragments into nxt, then compute
 // KS from cur (read one k-step earlier).
 template <int KS>
 __device__ __forceinline__ void gemm_kstep(uint32_t abase, uint32_t bbase, GemmFrags& cur, GemmFrags& nxt,
-                                           uint32_t magic, f32x4 (&P)[GM_MF][4], f32x4 (&xs)[GM_MF]) {
+                                           uint32_t magic, f32x4 (&P)[GM_MF][GM_NJ], f32x4 (&xs)[GM_MF]) {
   if constexpr (KS + 1 < KSG) {
     gemm_read<KS + 1>(abase, bbase, nxt);
-    wait_lds<6>(cur);
+    wait_lds<GM_MF + GM_NJ>(cur);
   } else {
     wait_lds<0>(cur);
   }
   const bf16x8 ones = ones_operand();
-  bf16x8 a[GM_MF], b[4];
+  bf16x8 b[GM_NJ];
 #pragma unroll
-  for (int mi = 0; mi < GM_MF; ++mi) a[mi] = a_operand(cur.a[mi]);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) b[j] = b_operand(cur.b[j], magic);
+  for (int j = 0; j < GM_NJ; ++j) b[j] = b_operand_kord(cur.b[j], magic);
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi) {
-    xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], ones, xs[mi], 0, 0, 0);
+    const bf16x8 a = __builtin_bit_cast(bf16x8, cur.a[mi]);
+    xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mi], b[j], P[mi][j], 0, 0, 0);
+    for (int j = 0; j < GM_NJ; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], P[mi][j], 0, 0, 0);
   }
   if constexpr (KS + 1 < KSG) gemm_kstep<KS + 1>(abase, bbase, nxt, cur, magic, P, xs);
 }
 
-__device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn, int lane, int ncol0,
-                                             f32x4 (&total)[GM_MF][4]) {
-  static_assert(GM_MF == 2, "wait_lds ties two A fragments");
-  const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane + GM_MF * wm * KSG * 1024;
-  // lane (r, c): qweight row 4 ks + r = pair 2 ks + r / 2, row r % 2 of the pair; column 64 wn + c
+__device__ __forceinline__ void gemm_compute(const GemmStage& st, int wn, int lane, int ncol0,
+                                             f32x4 (&total)[GM_MF][GM_NJ]) {
+  const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane;
+  // lane (r, c): qweight row 4 ks + r = pair 2 ks + r / 2, row r % 2 of the pair; column 32 wn + c
   const int rr = lane >> 4, cc = lane & 15;
-  const uint32_t bbase = lds_addr(&st.b[0]) + 4 * ((rr >> 1) * GM_BPAIR_W + (rr & 1) * GM_BROW + 64 * wn + cc);
+  const uint32_t bbase =
+      lds_addr(&st.b[0]) + 4 * ((rr >> 1) * GM_BPAIR_W + (rr & 1) * GM_BROW + GM_WCOLS * wn + cc);
   // this lane's columns: ncol0 + 16 j, tile-local lc + 16 j; their scales are words
   // (lc >> 1) + 8 j, their zero words (lc >> 3) + 2 j
   const int lc = ncol0 & (GM_BN - 1);
   const uint32_t sbase = lds_addr(&st.qs[0]) + 4 * (lc >> 1);
   const uint32_t zbase = lds_addr(&st.qz[0]) + 4 * (lc >> 3);
-  uint32_t sw[4], zw[4];
+  static_assert(GM_NJ == 2, "two scale and zero words a lane");
+  uint32_t sw[GM_NJ], zw[GM_NJ];
   sw[0] = lds_read4<0>(sbase);  zw[0] = lds_read4<0>(zbase);
   sw[1] = lds_read4<32>(sbase); zw[1] = lds_read4<8>(zbase);
-  sw[2] = lds_read4<64>(sbase); zw[2] = lds_read4<16>(zbase);
-  sw[3] = lds_read4<96>(sbase); zw[3] = lds_read4<24>(zbase);
   const uint32_t magic = magic_vgpr();
-  f32x4 P[GM_MF][4], xs[GM_MF];
+  f32x4 P[GM_MF][GM_NJ], xs[GM_MF];
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi) {
     xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) P[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < GM_NJ; ++j) P[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   GemmFrags f0, f1;
   gemm_read<0>(abase, bbase, f0);
@@ -253,7 +263,7 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn
   const int zshift = (ncol0 & 7) * 4;   // the same for every fragment (16 j keeps the low bits)
   const bool odd = ncol0 & 1;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < GM_NJ; ++j) {
     const float zb = -(float)(128 + 1 + ((zw[j] >> zshift) & 0xFu));
     const float sc = f16_to_f32(odd ? (sw[j] >> 16) : (sw[j] & 0xFFFFu));
 #pragma unroll
@@ -266,8 +276,7 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wm, int wn
 __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearParams p) {
   __shared__ GemmStage stg[GM_STAGES];
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / GM_WN, wn = wave % GM_WN;
+  const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave's 32-column slice
   const int c = lane & 15, r = lane >> 4;
   // tiles in row-major order (row tile major), each XCD taking one contiguous
   // range of them so that the row tiles it works on stay in its L2
@@ -275,54 +284,54 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
   const int T = MT * NT, id = blockIdx.x;
   const int tile = (T & 7) ? id : (id & 7) * (T >> 3) + (id >> 3);
   const int m0 = (tile / NT) * GM_BM, n0 = (tile % NT) * GM_BN;
-  const int ncol0 = n0 + 64 * wn + c;          // this lane's column in fragment 0
+  const int ncol0 = n0 + GM_WCOLS * wn + c;   // this lane's column in n-tile 0
   const int KT = p.K / GS;
 
-  f32x4 total[GM_MF][4];
+  f32x4 total[GM_MF][GM_NJ];
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) total[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < GM_NJ; ++j) total[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Step kt: load k-tile kt + 1 into the other stage (its last reader, k-tile
   // kt - 1, is done: every wave met the barrier after it), compute k-tile kt, then
   // wait until this wave's loads of kt + 1 have landed and meet the other waves
   // (then everyone's have).  The last step issues no loads, so nothing is in
   // flight when the epilogue starts.
-  gemm_issue(p, m0, n0, 0, wave, lane, stg[0]);
+  gemm_issue(p, m0, n0, 0, wn, lane, stg[0]);
   wait_vm<0>();
   lds_barrier();
   int kt = 0;
   for (; kt + 1 < KT; ++kt) {
-    gemm_issue(p, m0, n0, kt + 1, wave, lane, stg[(kt + 1) & 1]);
-    gemm_compute(stg[kt & 1], wm, wn, lane, ncol0, total);
+    gemm_issue(p, m0, n0, kt + 1, wn, lane, stg[(kt + 1) & 1]);
+    gemm_compute(stg[kt & 1], wn, lane, ncol0, total);
     wait_vm<0>();
     lds_barrier();
   }
-  gemm_compute(stg[kt & 1], wm, wn, lane, ncol0, total);
+  gemm_compute(stg[kt & 1], wn, lane, ncol0, total);
   lds_barrier();   // every wave is done reading the stages: they become the epilogue's tiles
 
-  // ---- epilogue: total[mi][j][i] is row 16 (GM_MF wm + mi) + 4 r + i, column
-  // 64 wn + 16 j + c of the tile.  Each wave parks its bf16 results in its own
-  // LDS region, row-major, then stores them as 16-byte row pieces (a lane's
-  // MFMA outputs are one column of four rows, which would take 2-byte stores).
-  uint16_t* ep = reinterpret_cast<uint16_t*>(&stg[0]) + wave * GM_EP_WAVE;
-  const int row0 = m0 + 16 * GM_MF * wm;       // the wave's first row
+  // ---- epilogue: total[mi][j][i] is row 16 mi + 4 r + i, column 32 wn + 16 j + c
+  // of the tile.  Each wave parks its bf16 results in its own LDS region,
+  // row-major, then stores them as 16-byte row pieces (a lane's MFMA outputs are
+  // one column of four rows, which would take 2-byte stores).
+  uint16_t* ep = reinterpret_cast<uint16_t*>(&stg[0]) + wn * GM_EP_WAVE;
+  const int ncolw = n0 + GM_WCOLS * wn;        // the wave's first column
   if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
 #pragma unroll
     for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < GM_NJ; ++j)
           ep[(16 * mi + 4 * r + i) * GM_EP_LD + 16 * j + c] = (uint16_t)f32_to_bf16(total[mi][j][i]);
     __builtin_amdgcn_wave_barrier();
-    // 32 rows x 64 columns = 256 pieces of 8 values, 4 a lane
+    // 64 rows x 32 columns = 256 pieces of 8 values, 4 a lane
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int q = lane + 64 * u, row = q >> 3, ch = q & 7;
-      const int m = row0 + row;
-      const size_t off = (size_t)min(m, p.M - 1) * p.ldy + n0 + 64 * wn + 8 * ch;
+      const int q = lane + 64 * u, row = q >> 2, ch = q & 3;
+      const int m = m0 + row;
+      const size_t off = (size_t)min(m, p.M - 1) * p.ldy + ncolw + 8 * ch;
       u32x4 v = *reinterpret_cast<const u32x4*>(ep + row * GM_EP_LD + 8 * ch);
       if (p.epi == EPI_RESIDUAL) {
         const u32x4 rv = *reinterpret_cast<const u32x4*>(p.residual + off);
@@ -335,7 +344,7 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
     }
   } else {
     // interleaved pairs: gate in the even column, up in the odd one; output column
-    // (64 wn + 16 j + c) / 2 of the tile's 64.  SwiGLU: of MFMA rows i0, i0 + 1 the
+    // (32 wn + 16 j + c) / 2 of the tile's 64.  SwiGLU: of MFMA rows i0, i0 + 1 the
     // even lane computes row i0 and the odd lane row i0 + 1 (one exchange gives
     // each its other operand), so every lane evaluates SiLU 16 times, not 32;
     // results go to region 0.  Paired: gate to region 0, up to region 1.
@@ -343,7 +352,7 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
 #pragma unroll
     for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < GM_NJ; ++j) {
         if (p.epi == EPI_SWIGLU) {
 #pragma unroll
           for (int i0 = 0; i0 < 4; i0 += 2) {
@@ -357,22 +366,21 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            ep[(16 * mi + 4 * r + i) * GM_EP_LD + 8 * j + (c >> 1) + (odd ? 32 * GM_EP_LD : 0)] =
+            ep[(16 * mi + 4 * r + i) * GM_EP_LD + 8 * j + (c >> 1) + (odd ? GM_BM * GM_EP_LD : 0)] =
                 (uint16_t)f32_to_bf16(total[mi][j][i]);
         }
       }
     __builtin_amdgcn_wave_barrier();
-    // 32 rows x 32 output columns per region = 128 pieces of 8 values, 2 a lane
+    // 64 rows x 16 output columns per region = 128 pieces of 8 values, 2 a lane
     const int regions = p.epi == EPI_SWIGLU ? 1 : 2;
     for (int reg = 0; reg < regions; ++reg) {
       uint16_t* dst = reg ? p.y1 : p.y0;
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int q = lane + 64 * u, row = q >> 2, ch = q & 3;
-        const int m = row0 + row;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(ep + reg * 32 * GM_EP_LD + row * GM_EP_LD + 8 * ch);
-        if (m < p.M)
-          *reinterpret_cast<u32x4*>(dst + (size_t)m * p.ldy + ((n0 + 64 * wn) >> 1) + 8 * ch) = v;
+        const int q = lane + 64 * u, row = q >> 1, ch = q & 1;
+        const int m = m0 + row;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ep + reg * GM_BM * GM_EP_LD + row * GM_EP_LD + 8 * ch);
+        if (m < p.M) *reinterpret_cast<u32x4*>(dst + (size_t)m * p.ldy + (ncolw >> 1) + 8 * ch) = v;
       }
     }
   }

@@ -66,6 +66,23 @@ __device__ __forceinline__ bf16x8 b_operand(uint32_t w, uint32_t magic) {
   return __builtin_bit_cast(bf16x8, d);
 }
 
+// The same eight values in k order, to meet an activation fragment as it lies in
+// memory: word j is (k 2j, k 2j + 1), byte j of w (nibbles 2j, 2j + 1) put in
+// the low half and byte j of w >> 4 (nibble 2j + 1 at its bottom) in the high
+// half by one byte permute, then the AND-OR.  One shift and two instructions a
+// pair: nine a word against b_operand's seven, and the activations need no
+// reordering.
+__device__ __forceinline__ bf16x8 b_operand_kord(uint32_t w, uint32_t magic) {
+  const uint32_t w4 = w >> 4;
+  u32x4 d;
+  // selector bytes 0-3 take bytes of w, 4-7 bytes of w4, 0x0C gives a zero byte
+  d.x = (__builtin_amdgcn_perm(w4, w, 0x0C040C00u) & NIB2) | magic;   // (k0, k1)
+  d.y = (__builtin_amdgcn_perm(w4, w, 0x0C050C01u) & NIB2) | magic;   // (k2, k3)
+  d.z = (__builtin_amdgcn_perm(w4, w, 0x0C060C02u) & NIB2) | magic;   // (k4, k5)
+  d.w = (__builtin_amdgcn_perm(w4, w, 0x0C070C03u) & NIB2) | magic;   // (k6, k7)
+  return __builtin_bit_cast(bf16x8, d);
+}
+
 // v holds bf16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7); reorder to match b_operand,
 // one byte permute (v_perm_b32) per output word.
 __device__ __forceinline__ bf16x8 a_operand(u32x4 v) {
