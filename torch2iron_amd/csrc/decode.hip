@@ -381,7 +381,9 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
   // (25.2 and 15.8 us against 12.7 us), measured.  Counting the arrival without
   // waiting for the stores, with the states as flagged 64-bit words that the
   // merger polls, measured slower too (13.4 against 11.8 us per call: the merger
-  // then meets the last chunk's words still in flight and polls again).
+  // then meets the last chunk's words still in flight and polls again), and so did
+  // merging in a second kernel after this one, with the launch boundary as the
+  // hand-off (0.897 against 0.874 ms per decode step at batch 16).
   wait_stores();
   __syncthreads();
   if (tid == 0) {
