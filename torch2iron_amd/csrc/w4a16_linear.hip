@@ -32,7 +32,9 @@
 
 namespace t2i {
 
-template <int MT, int LW, int W, int CK, bool NORM>
+// XROWS: the activation rows are read whole (see load_chunk); the host picks it for
+// row tiles of 8 or 16 rows.
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, const uint32_t* qw_, const uint16_t* sc_,
                                                              const uint32_t* qz_, const uint16_t* aux_, int N_, int M_,
                                                              int K_, int G_, const LinearParams p_) {
@@ -41,7 +43,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   p.M = M_ & 0xFFFFFF;
   p.rt = 1 << (M_ >> 24);
   if constexpr (NORM) p.gamma = aux_; else p.residual = aux_;
-  linear_tile<MT, LW, W, CK, NORM>(p, G_, blockIdx.x, blockIdx.z);
+  linear_tile<MT, LW, W, CK, NORM, XROWS>(p, G_, blockIdx.x, blockIdx.z);
 }
 
 // ============================================================================
@@ -510,22 +512,37 @@ using t2i_host::fail;
 using t2i_host::LinearPlan;
 using t2i_host::plan_linear;
 
-template <int MT, int LW, int W, int CK, bool NORM>
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS>
 hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   // the kernel takes x rows of K values (ldx = K) and K / (32 CK) chunks, as every plan here sets them
   if (p.ldx != p.K || p.chunks != p.K / (32 * CK)) return hipErrorInvalidValue;
   if (p.M >= (1 << 24) || p.rt < 1 || p.rt > 16 * MT || (p.rt & (p.rt - 1))) return hipErrorInvalidValue;
   const int m_rt = p.M | (__builtin_ctz((unsigned)p.rt) << 24);   // M and log2 of the row-tile height
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc, p.qz,
-                     NORM ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM, XROWS>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc,
+                     p.qz, NORM ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
   return hipGetLastError();
+}
+
+// Whole-row activation loads pay for their trip through LDS only when a row tile
+// holds many distinct rows: measured over the HBM-cold sweep, 0.07-0.8 us less
+// per launch with tiles of 8 or 16 rows (qkv and gate_up at M = 16: -0.26 and
+// -0.29 us; down at M = 64: -0.8 us), 0.04-0.15 us more with tiles of 1 to 4 rows
+// (M = 1; o_proj and down at M = 8 and 16).  Not compiled for 16 waves of 4-step
+// chunks, whose registers are already at the limit.
+template <int MT, int LW, int W, int CK>
+hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm) {
+  constexpr bool XOK = MT == 1 && (CK == 2 || (CK == 4 && W < 16));
+  if constexpr (XOK) {
+    if (p.rt >= 8)
+      return norm ? launch_t<MT, LW, W, CK, true, true>(p, grid, s) : launch_t<MT, LW, W, CK, false, true>(p, grid, s);
+  }
+  return norm ? launch_t<MT, LW, W, CK, true, false>(p, grid, s) : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
 }
 
 hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
-#define T2I_LAUNCH(a, b, c, d)                                         \
-  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)             \
-    return norm ? launch_t<a, b, c, d, true>(p, grid, s) : launch_t<a, b, c, d, false>(p, grid, s);
+#define T2I_LAUNCH(a, b, c, d) \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_cfg<a, b, c, d>(p, grid, s, norm);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;

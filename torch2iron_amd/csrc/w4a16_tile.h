@@ -171,19 +171,47 @@ __device__ __forceinline__ int tile_row(const LinearParams& p, int mbase, int lo
   return min(mbase + min(local, p.rt - 1), p.M - 1);
 }
 
-template <int MT, int LW, int CK, bool NORM>
+// Activation rows read whole (XROWS, one 16-row tile): load instruction i of a
+// chunk covers tile rows (16 / CK) i .. (16 / CK) (i + 1) - 1, lane l row
+// (16 / CK) i + l / (4 CK) and k-block l % (4 CK) (8 bf16 values) of the chunk, so
+// an instruction reads 16 / CK pieces of CK * 64 contiguous bytes instead of 16
+// pieces of 64 bytes.  Every workgroup reads the tile's activation rows through
+// its XCD's L2, and the fewer, longer pieces cost fewer L2 requests (a read-only
+// probe of the qkv loads at M = 16: 0.4 us less per launch).  x_fragments then
+// moves the values into the MFMA layout through LDS.
+template <int CK>
+__device__ __forceinline__ int xrow_of(int lane, int i) { return (16 / CK) * i + lane / (4 * CK); }
+
+// 16-byte LDS unit of (tile row, k-block) in a wave's chunk region: k-block
+// major, the row XOR-swizzled with the k-block so that the stores of one load
+// instruction and the reads of one k-step each meet 16 distinct bank groups per
+// 16 lanes.
+template <int CK>
+__device__ __forceinline__ int xunit(int row, int kb) { return 16 * kb + (row ^ ((kb * 4 / CK) & 15)); }
+
+template <int MT, int LW, int CK, bool NORM, bool XROWS = false>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
   const int ks0 = ch * CK;
 #pragma unroll
   for (int j = 0; j < CK; ++j)
     load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+  if constexpr (XROWS) {
+    static_assert(MT == 1 && (CK == 2 || CK == 4), "whole-row loads of one 16-row tile");
+    const int lane = 16 * r + c;
 #pragma unroll
-  for (int mi = 0; mi < MT; ++mi) {
-    const int m = tile_row(p, mbase, mi * 16 + c);
+    for (int i = 0; i < CK; ++i) {
+      const int m = tile_row(p, mbase, xrow_of<CK>(lane, i));
+      b.x[0][i] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + ks0 * 32 + 8 * (lane % (4 * CK)));
+    }
+  } else {
 #pragma unroll
-    for (int j = 0; j < CK; ++j)
-      b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+    for (int mi = 0; mi < MT; ++mi) {
+      const int m = tile_row(p, mbase, mi * 16 + c);
+#pragma unroll
+      for (int j = 0; j < CK; ++j)
+        b.x[mi][j] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + (ks0 + j) * 32 + r * 8);
+    }
   }
   if constexpr (NORM) {
 #pragma unroll
@@ -269,6 +297,22 @@ __device__ __forceinline__ void load_chunk_x_coh(const LinearParams& p, int ch, 
 __device__ __forceinline__ void pin(uint32_t& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
 
+// The activation rows of a chunk loaded whole (load_chunk with XROWS) into the MFMA
+// layout (lane (c, r), k-step j: tile row c, k 32 j + 8 r .. + 7 of the chunk),
+// through this wave's CK * 1 KB region of LDS.  One wave writes and reads its own
+// region, so no barrier is needed.
+template <int LW, int CK>
+__device__ __forceinline__ void x_fragments(Chunk<1, LW, CK>& b, u32x4* region, int lane) {
+#pragma unroll
+  for (int i = 0; i < CK; ++i) {
+    pin(b.x[0][i]);
+    region[xunit<CK>(xrow_of<CK>(lane, i), lane % (4 * CK))] = b.x[0][i];
+  }
+  const int c = lane & 15, r = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < CK; ++j) b.x[0][j] = region[xunit<CK>(c, 4 * j + r)];
+}
+
 // NORM (fused-norm variant, MT = 1): the A operand is bf16(x * gamma), and the
 // lane's share of its row's sum of squares accumulates in ss; the row's 1 / rms
 // multiplies the finished sums (see the kernel).
@@ -342,19 +386,30 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
 // each computation waits for its own chunk only: one memory round trip for the
 // whole K slice of the wave.  Up to 6 chunks of 2 k-steps without the fused
 // norm (12 registers a chunk at one word per lane), 3 otherwise.
-template <int MT, int LW, int CK, bool NORM, int NC>
+// A chunk from load_chunk, computed: its activation rows first into the MFMA
+// layout when they were loaded whole (XROWS; xreg is the wave's LDS region).
+template <int MT, int LW, int CK, bool NORM, bool XROWS>
+__device__ __forceinline__ void compute_loaded(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4], float& ss,
+                                               int zshift, u32x4* xreg, int lane) {
+  if constexpr (XROWS) x_fragments<LW, CK>(b, xreg, lane);
+  compute_chunk<MT, LW, CK, NORM>(b, total, ss, zshift);
+}
+
+template <int MT, int LW, int CK, bool NORM, bool XROWS, int NC>
 __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_begin, int ncol, int c, int r, int mbase,
                                                 Chunk<MT, LW, CK>& A, float (&total)[MT][LW][4], float& ss,
-                                                int zshift) {
+                                                int zshift, u32x4* xreg) {
+  const int lane = 16 * r + c;
   if constexpr (NC == 1) {
-    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
   } else {
     Chunk<MT, LW, CK> rest[NC - 1];
 #pragma unroll
-    for (int i = 1; i < NC; ++i) load_chunk<MT, LW, CK, NORM>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
-    compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+    for (int i = 1; i < NC; ++i)
+      load_chunk<MT, LW, CK, NORM, XROWS>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
+    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
 #pragma unroll
-    for (int i = 1; i < NC; ++i) compute_chunk<MT, LW, CK, NORM>(rest[i - 1], total, ss, zshift);
+    for (int i = 1; i < NC; ++i) compute_loaded<MT, LW, CK, NORM, XROWS>(rest[i - 1], total, ss, zshift, xreg, lane);
   }
 }
 
@@ -513,7 +568,8 @@ __device__ __forceinline__ int xcd_block(int b, int G) {
 struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
-template <int MT, int LW, int W, int CK, bool NORM, class Hook = NoHook>
+// XROWS: activation rows read whole (load_chunk), through a per-wave LDS region.
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS = false, class Hook = NoHook>
 __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx, int bz,
                                             const Hook& after_loads = Hook()) {
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
@@ -542,7 +598,9 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
 
   // every wave loads a first chunk (a wave without chunks reloads the last and computes nothing)
   Chunk<MT, LW, CK> A, B;
-  load_chunk<MT, LW, CK, NORM>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
+  __shared__ u32x4 xsh[XROWS ? W * CK * 64 : 1];   // each wave's chunk region (XROWS)
+  u32x4* const xreg = &xsh[XROWS ? wave * CK * 64 : 0];
+  load_chunk<MT, LW, CK, NORM, XROWS>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
   // The residual values this wave stores (residual epilogue) are fetched now, so
   // the epilogue waits for nothing.  The load is unconditional: waves that store
   // nothing fetch a clamped row and drop it, and without a residual the first
@@ -566,28 +624,28 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
     constexpr bool DEEP = !NORM && CK == 2;   // 4..6 chunks in registers: 12 a chunk
     looped = false;
     if (n == 1) {
-      straight_chunks<MT, LW, CK, NORM, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else if (n == 2) {
-      straight_chunks<MT, LW, CK, NORM, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else if (n == 3) {
-      straight_chunks<MT, LW, CK, NORM, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else if (DEEP && n == 4) {
-      straight_chunks<MT, LW, CK, NORM, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else if (DEEP && n == 5) {
-      straight_chunks<MT, LW, CK, NORM, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else if (DEEP && n == 6) {
-      straight_chunks<MT, LW, CK, NORM, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
     } else {
       looped = true;
     }
   }
   if (looped) {
     for (int ch = c_begin; ch < c_end; ch += 2) {
-      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 1, ncol, c, r, mbase, B);
-      compute_chunk<MT, LW, CK, NORM>(A, total, ss, zshift);
+      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 1, ncol, c, r, mbase, B);
+      compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
       if (ch + 1 >= c_end) break;
-      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM>(p, ch + 2, ncol, c, r, mbase, A);
-      compute_chunk<MT, LW, CK, NORM>(B, total, ss, zshift);
+      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 2, ncol, c, r, mbase, A);
+      compute_loaded<MT, LW, CK, NORM, XROWS>(B, total, ss, zshift, xreg, lane);
     }
   }
 
