@@ -523,17 +523,22 @@ hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Whole-row activation loads pay for their trip through LDS only when a row tile
-// holds many distinct rows: measured over the HBM-cold sweep, 0.07-0.8 us less
-// per launch with tiles of 8 or 16 rows (qkv and gate_up at M = 16: -0.26 and
-// -0.29 us; down at M = 64: -0.8 us), 0.04-0.15 us more with tiles of 1 to 4 rows
-// (M = 1; o_proj and down at M = 8 and 16).  Not compiled for 16 waves of 4-step
-// chunks, whose registers are already at the limit.
+// Whole-row activation loads, from row tiles of 4 rows up: measured over the
+// HBM-cold sweep, 0.05-0.7 us less per launch with tiles of 8 or 16 rows (qkv and
+// gate_up at M = 16: -0.22 us; down at M = 64: -0.7 us) and ~0.04 us less with
+// tiles of 4 (o_proj and down at M = 16, a tile loading only the instructions that
+// hold its rows); tiles of 1 or 2 rows gain nothing, within +-0.07 us.  Not compiled
+// for 16 waves of 4-step chunks, whose registers are already at the limit.
 template <int MT, int LW, int W, int CK>
 hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm) {
   constexpr bool XOK = MT == 1 && (CK == 2 || (CK == 4 && W < 16));
+  int min_rt = 4;
+#ifdef T2I_TUNING
+  // tuning builds only: T2I_XROWS_MIN_RT = smallest row tile given whole-row loads (17: never)
+  if (const char* env = getenv("T2I_XROWS_MIN_RT")) min_rt = atoi(env);
+#endif
   if constexpr (XOK) {
-    if (p.rt >= 8)
+    if (p.rt >= min_rt)
       return norm ? launch_t<MT, LW, W, CK, true, true>(p, grid, s) : launch_t<MT, LW, W, CK, false, true>(p, grid, s);
   }
   return norm ? launch_t<MT, LW, W, CK, true, false>(p, grid, s) : launch_t<MT, LW, W, CK, false, false>(p, grid, s);

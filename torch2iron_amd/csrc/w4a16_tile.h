@@ -201,8 +201,11 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
     const int lane = 16 * r + c;
 #pragma unroll
     for (int i = 0; i < CK; ++i) {
-      const int m = tile_row(p, mbase, xrow_of<CK>(lane, i));
-      b.x[0][i] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + ks0 * 32 + 8 * (lane % (4 * CK)));
+      // only the loads that hold real rows of the tile (workgroup-uniform)
+      if (i == 0 || xrow_of<CK>(0, i) < p.rt) {
+        const int m = tile_row(p, mbase, xrow_of<CK>(lane, i));
+        b.x[0][i] = *reinterpret_cast<const u32x4*>(p.x + (size_t)m * p.ldx + ks0 * 32 + 8 * (lane % (4 * CK)));
+      }
     }
   } else {
 #pragma unroll
@@ -301,16 +304,21 @@ __device__ __forceinline__ void pin(u32x4& v) { asm volatile("" : "+v"(v)); }
 // layout (lane (c, r), k-step j: tile row c, k 32 j + 8 r .. + 7 of the chunk),
 // through this wave's CK * 1 KB region of LDS.  One wave writes and reads its own
 // region, so no barrier is needed.
+// A tile of rt < 16 rows loads only the instructions that hold its real rows, and
+// every MFMA row past rt reads the tile's last row.
 template <int LW, int CK>
-__device__ __forceinline__ void x_fragments(Chunk<1, LW, CK>& b, u32x4* region, int lane) {
+__device__ __forceinline__ void x_fragments(Chunk<1, LW, CK>& b, u32x4* region, int lane, int rt) {
 #pragma unroll
   for (int i = 0; i < CK; ++i) {
-    pin(b.x[0][i]);
-    region[xunit<CK>(xrow_of<CK>(lane, i), lane % (4 * CK))] = b.x[0][i];
+    if (i == 0 || xrow_of<CK>(0, i) < rt) {
+      pin(b.x[0][i]);
+      region[xunit<CK>(xrow_of<CK>(lane, i), lane % (4 * CK))] = b.x[0][i];
+    }
   }
   const int c = lane & 15, r = lane >> 4;
+  const int row = min(c, rt - 1);
 #pragma unroll
-  for (int j = 0; j < CK; ++j) b.x[0][j] = region[xunit<CK>(c, 4 * j + r)];
+  for (int j = 0; j < CK; ++j) b.x[0][j] = region[xunit<CK>(row, 4 * j + r)];
 }
 
 // NORM (fused-norm variant, MT = 1): the A operand is bf16(x * gamma), and the
@@ -390,8 +398,8 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
 // layout when they were loaded whole (XROWS; xreg is the wave's LDS region).
 template <int MT, int LW, int CK, bool NORM, bool XROWS>
 __device__ __forceinline__ void compute_loaded(Chunk<MT, LW, CK>& b, float (&total)[MT][LW][4], float& ss,
-                                               int zshift, u32x4* xreg, int lane) {
-  if constexpr (XROWS) x_fragments<LW, CK>(b, xreg, lane);
+                                               int zshift, u32x4* xreg, int lane, int rt) {
+  if constexpr (XROWS) x_fragments<LW, CK>(b, xreg, lane, rt);
   compute_chunk<MT, LW, CK, NORM>(b, total, ss, zshift);
 }
 
@@ -401,15 +409,16 @@ __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_beg
                                                 int zshift, u32x4* xreg) {
   const int lane = 16 * r + c;
   if constexpr (NC == 1) {
-    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
+    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
   } else {
     Chunk<MT, LW, CK> rest[NC - 1];
 #pragma unroll
     for (int i = 1; i < NC; ++i)
       load_chunk<MT, LW, CK, NORM, XROWS>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
-    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
+    compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
 #pragma unroll
-    for (int i = 1; i < NC; ++i) compute_loaded<MT, LW, CK, NORM, XROWS>(rest[i - 1], total, ss, zshift, xreg, lane);
+    for (int i = 1; i < NC; ++i)
+      compute_loaded<MT, LW, CK, NORM, XROWS>(rest[i - 1], total, ss, zshift, xreg, lane, p.rt);
   }
 }
 
@@ -642,10 +651,10 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   if (looped) {
     for (int ch = c_begin; ch < c_end; ch += 2) {
       if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 1, ncol, c, r, mbase, B);
-      compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane);
+      compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
       if (ch + 1 >= c_end) break;
       if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 2, ncol, c, r, mbase, A);
-      compute_loaded<MT, LW, CK, NORM, XROWS>(B, total, ss, zshift, xreg, lane);
+      compute_loaded<MT, LW, CK, NORM, XROWS>(B, total, ss, zshift, xreg, lane, p.rt);
     }
   }
 
