@@ -290,43 +290,53 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     out = {}
 
     # ---- config 3: one decode layer, B = 8, context 1024 (write at 1024) ----
-    b3, cap3 = 8, 1088
+    # 12 distinct layers (weights and caches, 530 MB: past the 256 MB MALL, as the
+    # layers of a decode step are) run back to back in one graph, so that every
+    # layer reads HBM and the host's replay calls stay off the timed path.
+    b3, cap3, n3 = 8, 1088, 12
     rope = gm.rope_table(cfg.head_dim, cap3, cfg.rope_theta, dev)
-    layer = gm.Qwen3DecodeLayer(gm.Qwen3LayerWeights(tensors, 0, cfg, dev), cfg, rope)
     buf = gm.DecodeBuffers(cfg, b3, dev)
     gen = torch.Generator(device=dev).manual_seed(5)
-    kc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
-    vc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+    layers3 = []
+    for li in range(n3):
+        lay = gm.Qwen3DecodeLayer(gm.Qwen3LayerWeights(tensors, li, cfg, dev), cfg, rope)
+        kc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+        vc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
+        layers3.append((lay, kc, vc))
     pos = torch.full((b3,), 1024, dtype=torch.int32, device=dev)
     x0 = torch.randn(b3, cfg.hidden, generator=gen, device=dev).to(torch.bfloat16)
     buf.x.copy_(x0)
-    layer(buf, pos, kc, vc)                      # eager warm-up (allocates the attention workspace)
+    for lay, kc, vc in layers3:
+        lay(buf, pos, kc, vc)                    # eager warm-up (allocates the attention workspace)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        layer(buf, pos, kc, vc)
-    reps = max(steps, 10) * 5
+        for lay, kc, vc in layers3:
+            lay(buf, pos, kc, vc)
+    reps = max(steps, 10)
     for _ in range(warmup):
         buf.x.copy_(x0)
         g.replay()
     torch.cuda.synchronize()
+    buf.x.copy_(x0)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    layer_us = e0.elapsed_time(e1) * 1e3 / reps
-    w = layer.w
+    layer_us = e0.elapsed_time(e1) * 1e3 / (reps * n3)
+    w = layers3[0][0].w
     layer_bytes = (w.qkv.nbytes + w.o.nbytes + w.gate_up.nbytes + w.down.nbytes + 4 * 2 * cfg.hidden
                    + 2 * 2 * cfg.head_dim + b3 * cfg.n_kv_heads * 1025 * cfg.head_dim * 2 * 2
                    + b3 * cfg.n_kv_heads * cfg.head_dim * 2 * 2 + b3 * cfg.hidden * 2 * 2)
-    out["decode_layer"] = {"workload": "one fused Qwen3-0.6B decode layer, batch 8, context 1024",
+    out["decode_layer"] = {"workload": f"one fused Qwen3-0.6B decode layer, batch 8, context 1024 ({n3} distinct "
+                                       "layers back to back in one graph, HBM-cold)",
                            "us": round(layer_us, 2), "algorithmic_bytes": layer_bytes,
                            "TBps": round(layer_bytes / (layer_us * 1e-6) / 1e12, 4),
                            "frac_of_8TBps": round(layer_bytes / (layer_us * 1e-6) / 8e12, 4)}
     log(f"decode layer (B=8, ctx 1024): {layer_us:.1f} us, {out['decode_layer']['TBps']} TB/s")
-    del g, buf, layer, kc, vc
+    del g, buf, layers3, kc, vc
     torch.cuda.empty_cache()
 
     # ---- config 4: full model, batch 16, prompt 512, 128 new tokens ----
