@@ -440,7 +440,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 constexpr int LMH_WAVES = 4;
 constexpr int LMH_COLS = 32;                // vocab columns per wave
 constexpr int LMH_TILES = LMH_COLS / 16;    // MFMA n-tiles per wave
-constexpr int LMH_MAX_K = 4096;   // 16 x (K + 8) bf16 of LDS
+constexpr int LMH_MAX_K = 4096;   // 16 x K bf16 of LDS (plus 8 KB of regions)
 
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint32_t idx) {
   const uint32_t u = __float_as_uint(v);
@@ -454,17 +454,36 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
 
 // One workgroup: LMH_WAVES waves x LMH_COLS vocab rows; the activation rows
 // (M <= 16) are staged once in LDS and shared by the waves.
+//   * The table is read as 8 rows x 128 bytes per load instruction (lane l: row
+//     8 h + l / 8 of the tile, 16 bytes at k-block l % 8 of the 64-deep slice):
+//     whole 128-byte lines.  The MFMA operand (lane (c, r): row c, 8 k) would take
+//     16 rows x 16 bytes per instruction, 64-byte pieces of each row per
+//     instruction pair; a read-only probe of the two patterns streamed the table at
+//     7.2 against 5.7 TB/s.  Each tile's slice goes through the wave's 2 KB LDS
+//     region into the operand layout: 16-byte units k-block major, the row
+//     XOR-swizzled by the k-block, so that the stores of a load and the reads of an
+//     MFMA operand each meet 16 distinct bank groups per 16 lanes.
+//   * The activation rows sit unpadded, 16-byte unit u of row m at u ^ (m & 15)
+//     (m & 7 when K is not a multiple of 128): conflict-free operand reads, and
+//     32 KB plus the 8 KB of regions at K = 1024, so four workgroups share a CU.
+//   * The MFMA pairs k-block r of the slice's first half with the activation's
+//     k-block r and the second half likewise (lane (c, r) takes k 8 r and 32 + 8 r).
+__device__ __forceinline__ int lmh_unit(int row, int kb) { return 16 * kb + (row ^ ((2 * kb) & 15)); }
+
 __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
     const uint16_t* __restrict__ hin, int M, const uint16_t* __restrict__ E, int V, int K,
     float* __restrict__ logits, unsigned long long* __restrict__ keys) {
   // this workgroup's tiles [tb, te) of the V / 16 (contiguous, balanced)
-  extern __shared__ uint16_t s_h[];                 // [16][K + 8]
-  const int ldh = K + 8;
+  extern __shared__ u32x4 s_dyn[];                  // [16][K / 8] units of h, then the waves' regions
+  const int ku = K / 8;                             // 16-byte units per activation row
+  const int hmask = (ku & 15) ? 7 : 15;
+  u32x4* const s_hu = s_dyn;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int c = lane & 15;
   const int r = lane >> 4;
+  u32x4* const region = s_dyn + 16 * ku + wave * 128;
   const int T = V / 16;
   const int tb = (int)((long long)blockIdx.x * T / gridDim.x);
   const int te = (int)((long long)(blockIdx.x + 1) * T / gridDim.x);
@@ -486,20 +505,29 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
   auto load_slice = [&](int k0, u32x4 (&bv)[LMH_TILES][2]) {
 #pragma unroll
     for (int t = 0; t < LMH_TILES; ++t) {
-      const int row = (tile_ok[t] ? n0 + 16 * t : nfirst) + c;
-      const uint16_t* src = E + (size_t)row * K + k0 + 16 * r;
-      bv[t][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src));
-      bv[t][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + 8));
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int row = (tile_ok[t] ? n0 + 16 * t : nfirst) + 8 * h + (lane >> 3);
+        bv[t][h] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(E + (size_t)row * K + k0 + 8 * (lane & 7)));
+      }
     }
   };
   auto mul_slice = [&](int k0, const u32x4 (&bv)[LMH_TILES][2]) {
-    const uint16_t* ha = s_h + c * ldh + k0 + 16 * r;
-    const bf16x8 a0 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ha));
-    const bf16x8 a1 = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(ha + 8));
+    const int u0 = k0 / 8;
+    const u32x4* hrow = s_hu + c * ku;
+    const bf16x8 a0 = __builtin_bit_cast(bf16x8, hrow[(u0 + r) ^ (c & hmask)]);
+    const bf16x8 a1 = __builtin_bit_cast(bf16x8, hrow[(u0 + 4 + r) ^ (c & hmask)]);
 #pragma unroll
     for (int t = 0; t < LMH_TILES; ++t) {
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, __builtin_bit_cast(bf16x8, bv[t][0]), acc[t], 0, 0, 0);
-      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, __builtin_bit_cast(bf16x8, bv[t][1]), acc[t], 0, 0, 0);
+      // the wave's region holds one tile's slice at a time (LDS operations of a
+      // wave complete in order, so the next tile's stores follow these reads)
+      region[lmh_unit(lane >> 3, lane & 7)] = bv[t][0];
+      region[lmh_unit(8 + (lane >> 3), lane & 7)] = bv[t][1];
+      const bf16x8 b0 = __builtin_bit_cast(bf16x8, region[lmh_unit(c, r)]);
+      const bf16x8 b1 = __builtin_bit_cast(bf16x8, region[lmh_unit(c, 4 + r)]);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, acc[t], 0, 0, 0);
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, acc[t], 0, 0, 0);
     }
   };
   // Stage h (rows >= M are zero) while the first weight slice is in flight: each
@@ -509,13 +537,13 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
   // for every load in flight.
   u32x4 b0[LMH_TILES][2], b1[LMH_TILES][2];
   {
-    const int nst = 16 * (K / 8);   // 16-byte pieces of the 16-row tile
+    const int nst = 16 * ku;   // 16-byte pieces of the 16-row tile
     for (int base = 0; base < nst; base += 8 * 64 * LMH_WAVES) {
       u32x4 hv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         const int idx = min(base + u * 64 * LMH_WAVES + tid, nst - 1);
-        const int m = idx / (K / 8), ch = idx - m * (K / 8);
+        const int m = idx / ku, ch = idx - m * ku;
         hv[u] = *reinterpret_cast<const u32x4*>(hin + (size_t)min(m, M - 1) * K + ch * 8);
       }
       if (base == 0) {
@@ -526,8 +554,8 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
 #pragma unroll
       for (int u = 0; u < 8; ++u) {   // past the tile: the last piece again (same value)
         const int idx = min(base + u * 64 * LMH_WAVES + tid, nst - 1);
-        const int m = idx / (K / 8), ch = idx - m * (K / 8);
-        *reinterpret_cast<u32x4*>(s_h + m * ldh + ch * 8) = m < M ? hv[u] : u32x4{0u, 0u, 0u, 0u};
+        const int m = idx / ku, ch = idx - m * ku;
+        s_hu[m * ku + (ch ^ (m & hmask))] = m < M ? hv[u] : u32x4{0u, 0u, 0u, 0u};
       }
     }
   }
@@ -556,8 +584,9 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
     mul_slice(k0, b0);
   }
 
-  // lane holds logits[m = 4r + i][n = n0 + 16t + c]
-  __shared__ unsigned long long s_best[LMH_WAVES][16];
+  // lane holds logits[m = 4r + i][n = n0 + 16t + c]; each wave's best keys go to
+  // the start of its own region (16 words of 8 bytes), read after the barrier
+  unsigned long long* s_best = reinterpret_cast<unsigned long long*>(region);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * r + i;
@@ -574,13 +603,14 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
       const unsigned long long o = __shfl_xor(best, off, 64);
       best = umax64(best, o);
     }
-    if (c == 0) s_best[wave][m] = best;
+    if (c == 0) s_best[m] = best;
   }
   __syncthreads();
   if (tid < M) {
-    unsigned long long best = s_best[0][tid];
+    const unsigned long long* s0 = reinterpret_cast<const unsigned long long*>(s_dyn + 16 * ku);
+    unsigned long long best = s0[tid];
 #pragma unroll
-    for (int w = 1; w < LMH_WAVES; ++w) best = umax64(best, s_best[w][tid]);
+    for (int w = 1; w < LMH_WAVES; ++w) best = umax64(best, s0[w * 256 + tid]);   // 128 units = 256 words a region
     if (best) atomicMax(&keys[tid], best);
   }
 }
@@ -845,7 +875,7 @@ extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* 
   int wgs = (tiles + LMH_WAVES * LMH_TILES - 1) / (LMH_WAVES * LMH_TILES);
   if (wgs > 256) wgs = (wgs + 255) / 256 * 256;
   dim3 grid(wgs);
-  const size_t lds = (size_t)16 * (K + 8) * sizeof(uint16_t);
+  const size_t lds = (size_t)16 * K * sizeof(uint16_t) + (size_t)LMH_WAVES * 128 * 16;   // h + the waves' regions
   if (lds > 65536) {
     // the attribute belongs to the function on the current device: remember the
     // raised limit per device (a larger K raises it again)
