@@ -128,9 +128,11 @@ struct AttnParams {
 //      loaded alongside the position, the RoPE row and then the chunk's K and V rows
 //      once it is known: loads retire in issue order, so the q/k RMSNorm + RoPE below
 //      waits only for its own inputs while K/V are in flight;
-//   2. every 16-lane group scores its slots (8 dims per lane), keeps a softmax state
-//      (max, sum, unnormalised context) in registers, and the states are merged across
-//      the wave with lane shuffles and across the waves in LDS, in a fixed order;
+//   2. every 16-lane group scores its slots (8 dims per lane, a dot2 chain and a
+//      16-lane DPP sum); each wave keeps one softmax state (max, sum over its four
+//      groups) and forms its unnormalised context on the MFMA from the fp32
+//      weights (as three bf16 parts) and the V rows as they lie in registers; the
+//      waves' states meet in LDS, in a fixed order;
 //   3. with several chunks per (b, h), each chunk stores its state agent-coherently and
 //      the last chunk to arrive merges all of them in chunk order (deterministic) and
 //      writes the bf16 context; it also resets the arrival counter for the next launch.
@@ -166,7 +168,7 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
   __shared__ __align__(16) uint16_t s_q[Q][D];    // q heads after norm + RoPE (bf16)
   __shared__ __align__(16) uint16_t s_kv[2][D];   // current k (after norm + RoPE) and v
   __shared__ float s_wm[4][Q], s_wl[4][Q];
-  __shared__ float s_wacc[4][Q][D];
+  __shared__ __align__(16) float s_wacc[4][Q][D];
   __shared__ int s_last;
 
   // ---- 1. loads that do not need the position go out with it ----
@@ -255,23 +257,35 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
     }
     __syncthreads();
 
-    // ---- 2. scores and the softmax state of each 16-lane group ----
+    // ---- 2. scores on the VALU, the wave's softmax state, the context on the MFMA ----
+    // The chunk that owns the current slot loaded its cache rows before writing
+    // them: the lanes that hold that slot take k and v from LDS instead (a
+    // divergent patch in one wave; the other lanes never hold it).
+    if (t0 <= pos && pos < t1) {   // workgroup-uniform
+      const int rel = pos - t0;
+      if (grp == (rel & 15)) {
+        const u32x4 kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0])[c];
+        const u32x4 vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0])[c];
+        const int itp = rel >> 4;
+#pragma unroll
+        for (int it = 0; it < ROWS; ++it) {
+          if (it == itp) {
+            kreg[it] = kcur;
+            vreg[it] = vcur;
+          }
+        }
+      }
+    }
     u32x4 qv[Q];   // dims 8c .. 8c+7 of each q head, bf16 pairs
 #pragma unroll
     for (int j = 0; j < Q; ++j) qv[j] = reinterpret_cast<const u32x4*>(&s_q[j][0])[c];
-    const u32x4 kcur = reinterpret_cast<const u32x4*>(&s_kv[0][0])[c];
-    const u32x4 vcur = reinterpret_cast<const u32x4*>(&s_kv[1][0])[c];
-    const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
     const float sl2 = p.scale * 1.4426950408889634f;   // log2 units
+    // every lane of a 16-lane group ends with its slot's full score (row_sum16)
     float sc[ROWS][Q];
 #pragma unroll
     for (int it = 0; it < ROWS; ++it) {
       const int t = t0 + it * 16 + grp;
-      // the current slot comes from LDS (the cache row is being replaced); a slot
-      // past the chunk's end scores -inf, and its V is zeroed so that its zero
-      // softmax weight cannot meet a non-finite value from the reload
-      const u32x4 kk = t == pos ? kcur : kreg[it];
-      vreg[it] = t < t1 ? (t == pos ? vcur : vreg[it]) : zero4;
+      const u32x4 kk = kreg[it];
 #pragma unroll
       for (int j = 0; j < Q; ++j) {
         float d = dot2_bf16(qv[j].x, kk.x, 0.0f);   // bf16 products are exact in fp32
@@ -279,54 +293,115 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
         d = dot2_bf16(qv[j].z, kk.z, d);
         d = dot2_bf16(qv[j].w, kk.w, d);
         d = row_sum16(d);
-        sc[it][j] = t < t1 ? d * sl2 : -INFINITY;
+        sc[it][j] = t < t1 ? d * sl2 : -INFINITY;   // a slot past the chunk's end weighs nothing
       }
     }
-    float m[Q], mz[Q], l[Q], acc[Q][8];
+    // one softmax state per wave: the max and the sum over its four groups' slots
+    float m[Q], mz[Q], l[Q];
 #pragma unroll
     for (int j = 0; j < Q; ++j) {
       m[j] = sc[0][j];
 #pragma unroll
       for (int it = 1; it < ROWS; ++it) m[j] = fmaxf(m[j], sc[it][j]);
-      mz[j] = m[j] > -INFINITY ? m[j] : 0.0f;   // a group with no slot: 2^-inf = 0 below
+      m[j] = fmaxf(m[j], __shfl_xor(m[j], 16, 64));
+      m[j] = fmaxf(m[j], __shfl_xor(m[j], 32, 64));
+      mz[j] = m[j] > -INFINITY ? m[j] : 0.0f;   // a wave with no slot: 2^-inf = 0 below
       l[j] = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
     }
+    float pe[ROWS][Q];
 #pragma unroll
-    for (int it = 0; it < ROWS; ++it) {
-      float vf[8];
-      unpack8(vreg[it], vf);
+    for (int it = 0; it < ROWS; ++it)
 #pragma unroll
       for (int j = 0; j < Q; ++j) {
-        const float pe = exp2_fast(sc[it][j] - mz[j]);
-        l[j] += pe;
+        pe[it][j] = exp2_fast(sc[it][j] - mz[j]);
+        l[j] += pe[it][j];
+      }
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(pe, vf[e], acc[j][e]);
+    for (int j = 0; j < Q; ++j) {
+      l[j] += __shfl_xor(l[j], 16, 64);
+      l[j] += __shfl_xor(l[j], 32, 64);
+    }
+    // Context O[h][d] = sum over the wave's slots of P[h][slot] V[slot][d] on
+    // v_mfma_f32_16x16x32_bf16: the 32 k values are the 8 rows (it) of each of the
+    // four groups, which is how the slots already lie (lane (c, rg) holds rows it
+    // of slot group rg).  A = P: lane (c, rg) row h = c (zero past Q), k = its rows,
+    // as three bf16 parts, p = p0 + p1 + p2 (p0 = bf16(p), p1 = bf16(p - p0),
+    // p2 = p - p0 - p1, each difference exact in fp32), which carry all 24 bits of
+    // the fp32 weight: products with bf16 V are exact and the MFMA sums in fp32.
+    // (With bf16 weights, or two parts, more outputs miss the correctly rounded
+    // bf16 value and greedy decode drifts at near-ties.)  B = V for dim 8 c + e: lane
+    // (c, rg) column c, k = its rows, one byte permute per pair of rows.  So lane
+    // (c, r) ends with O[4 r + i][8 c + e] in acc[e][i], and the MFMA has summed the
+    // four groups.
+    constexpr int NB = (ROWS + 7) / 8;   // k-blocks of 8 rows
+    f32x4 acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float pw[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int it = 8 * b + u;
+        float v = 0.0f;
+        if (it < ROWS) {
+          v = pe[it][0];
+#pragma unroll
+          for (int j = 1; j < Q; ++j) v = c == j ? pe[it][j] : v;
+          v = c < Q ? v : 0.0f;
+        }
+        pw[u] = v;
+      }
+      float p1[8], p2[8];   // what bf16 leaves of each weight, in two parts
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        p1[u] = pw[u] - round_bf16(pw[u]);
+        p2[u] = p1[u] - round_bf16(p1[u]);
+      }
+      const bf16x8 a[3] = {
+          __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(pw[0], pw[1]), pack_bf16x2(pw[2], pw[3]),
+                                           pack_bf16x2(pw[4], pw[5]), pack_bf16x2(pw[6], pw[7])}),
+          __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(p1[0], p1[1]), pack_bf16x2(p1[2], p1[3]),
+                                           pack_bf16x2(p1[4], p1[5]), pack_bf16x2(p1[6], p1[7])}),
+          __builtin_bit_cast(bf16x8, u32x4{pack_bf16x2(p2[0], p2[1]), pack_bf16x2(p2[2], p2[3]),
+                                           pack_bf16x2(p2[4], p2[5]), pack_bf16x2(p2[6], p2[7])})};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        uint32_t wv[8];   // bf16 bits of dim 8 c + e, rows 8 b .. 8 b + 7
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int it = 8 * b + u;
+          const uint32_t w = it < ROWS ? (e < 2 ? vreg[it].x : e < 4 ? vreg[it].y : e < 6 ? vreg[it].z : vreg[it].w) : 0u;
+          wv[u] = w;
+        }
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;   // high or low halves of the pair
+        const u32x4 vb = u32x4{__builtin_amdgcn_perm(wv[1], wv[0], sel), __builtin_amdgcn_perm(wv[3], wv[2], sel),
+                               __builtin_amdgcn_perm(wv[5], wv[4], sel), __builtin_amdgcn_perm(wv[7], wv[6], sel)};
+        // smallest part first, so each sum adds the larger terms last
+#pragma unroll
+        for (int k = 2; k >= 0; --k)
+          acc[e] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[k], __builtin_bit_cast(bf16x8, vb), acc[e], 0, 0, 0);
       }
     }
-    // merge the four groups of the wave (lanes c, c+16, c+32, c+48 hold the same dims)
+    // the wave's state: heads 4 r + i < Q of this lane, dims 8 c .. 8 c + 7
 #pragma unroll
-    for (int off = 16; off <= 32; off <<= 1) {
-#pragma unroll
-      for (int j = 0; j < Q; ++j) {
-        const float mo = __shfl_xor(m[j], off, 64);
-        const float lo = __shfl_xor(l[j], off, 64);
-        const float mn = fmaxf(m[j], mo);
-        const float fa = state_weight(m[j], mn), fb = state_weight(mo, mn);
-        l[j] = l[j] * fa + lo * fb;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] * fa + __shfl_xor(acc[j][e], off, 64) * fb;
-        m[j] = mn;
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * rg + i;
+      if (h < Q) {
+        float* dst = &s_wacc[wave][h][8 * c];
+        *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
       }
     }
-    if (rg == 0) {
+    if (lane < Q) {
+      float mw = m[0], lw = l[0];
 #pragma unroll
-      for (int j = 0; j < Q; ++j) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) s_wacc[wave][j][8 * c + e] = acc[j][e];
-        if (c == 0) { s_wm[wave][j] = m[j]; s_wl[wave][j] = l[j]; }
+      for (int j = 1; j < Q; ++j) {
+        mw = lane == j ? m[j] : mw;
+        lw = lane == j ? l[j] : lw;
       }
+      s_wm[wave][lane] = mw;
+      s_wl[wave][lane] = lw;
     }
     __syncthreads();
 
