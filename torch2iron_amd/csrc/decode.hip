@@ -174,8 +174,11 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
   // ---- 1. loads that do not need the position go out with it ----
   // The raw q/k/v rows of this kv head and the norm weights are loaded while
   // the position is (a scalar load, waited for on its own counter).  Loading
-  // the chunk's first K / V rows here too, clamped to the cache capacity, was
-  // measured slower (0.927 against 0.919 ms per decode step).  Every load is
+  // the chunk's K / V rows here too, clamped to the cache capacity, was
+  // measured slower (0.927 against 0.919 ms per decode step), and so was the
+  // same with the RoPE row through scalar loads, so that its wait does not
+  // cover the K / V rows (10.5 -> 11.0 us a call, 0.848 -> 0.864 ms a step): the
+  // stream is bandwidth-bound once every workgroup runs.  Every load is
   // unconditional (clamped indices, results selected after the load): a load
   // under a lane-divergent condition whose other side writes the same registers
   // makes the compiler wait for all loads in flight there.
