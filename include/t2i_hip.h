@@ -290,6 +290,18 @@ int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t 
                        int32_t K, float* logits, uint64_t* argmax_keys, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * The final RMSNorm and the lm_head in one launch: exactly t2i_rmsnorm(x,
+ * norm_weight, eps) followed by t2i_lm_head_argmax on the normalised rows (the
+ * same bits in logits and argmax_keys), with the norm applied by every workgroup
+ * to its staged copy of the rows.  K must be a power of two in [64, 4096];
+ * argmax_keys zeroed beforehand (e.g. by the step's embedding-gather t2i_rmsnorm).
+ * Replaces: logits = self.lm_head(self.norm(x)) of quantized_qwen3/model.py:477.
+ */
+int t2i_rmsnorm_lm_head_argmax(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                               const uint16_t* E, int32_t V, int32_t K, float* logits,
+                               uint64_t* argmax_keys, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Greedy bookkeeping between decode steps, on the device:
  * tokens[b] = index decoded from argmax_keys[b]; history[b*hist_cap + step[0]] = tokens[b];
  * positions[b] += 1; step[0] += 1 (by one thread after all rows).  Lets a captured

@@ -114,6 +114,11 @@ def test_other_entry_points_validate():
     assert lib.t2i_decode_attention(*args) == _lib.T2I_ERR_WORKSPACE        # workspace too small
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151930, 1024, None, FAKE, None) == _lib.T2I_ERR_SHAPE
     assert lib.t2i_lm_head_argmax(FAKE, 16, FAKE, 151936, 1024, None, None, None) == _lib.T2I_ERR_NULL
+    fused = lib.t2i_rmsnorm_lm_head_argmax
+    assert fused(FAKE, 16, None, 1e-6, FAKE, 151936, 1024, None, FAKE, None) == _lib.T2I_ERR_NULL
+    assert fused(FAKE, 16, FAKE, 1e-6, FAKE, 151936, 192, None, FAKE, None) == _lib.T2I_ERR_SHAPE   # K not 2^n
+    assert fused(FAKE, 16, FAKE, 0.0, FAKE, 151936, 1024, None, FAKE, None) == _lib.T2I_ERR_VALUE
+    assert fused(FAKE, 16, FAKE + 2, 1e-6, FAKE, 151936, 1024, None, FAKE, None) == _lib.T2I_ERR_ALIGN
     assert lib.t2i_w4a16_dequant_f32(FAKE, FAKE, FAKE, 1024, 3072, 128, None, None) == _lib.T2I_ERR_NULL
     assert lib.t2i_stream_read(FAKE, 4096, 4, None, None) == _lib.T2I_ERR_NULL
     assert lib.t2i_stream_read(FAKE, 4100, 4, FAKE, None) == _lib.T2I_ERR_SHAPE    # not a multiple of 16

@@ -162,6 +162,30 @@ def test_lm_head_argmax(gpu, m, v, k):
     assert torch.equal(tok, torch.argmax(lg, dim=1))   # the fused argmax agrees with its own logits
 
 
+@pytest.mark.parametrize("m,v,k", [(16, 151936, 1024), (1, 4096, 1024), (5, 1040, 64), (20, 2064, 2048),
+                                   (3, 1040, 4096), (16, 528, 128)])
+def test_rmsnorm_lm_head_matches_two_launches(gpu, m, v, k):
+    """The final norm inside the lm_head gives the bits of t2i_rmsnorm followed by
+    t2i_lm_head_argmax: logits and keys, for one and two 16-row slices, K from 64 to
+    4096 (one or two gamma pieces a thread), residual-stream-sized inputs."""
+    print(f"rmsnorm + lm_head m={m} v={v} k={k}", flush=True)
+    g = torch.Generator().manual_seed(m * v + k)
+    x = (torch.randn(m, k, generator=g) * 40).to(BF16).to(gpu)
+    w = (torch.rand(k, generator=g) * 0.2 + 0.9).to(BF16).to(gpu)
+    e = torch.randn(v, k, generator=g).to(BF16).to(gpu)
+    keys_ref = torch.zeros(m, dtype=torch.int64, device=gpu)
+    logits_ref = torch.empty(m, v, dtype=torch.float32, device=gpu)
+    ops.lm_head_argmax(ops.rmsnorm(x, w, 1e-6), e, keys_ref, logits=logits_ref)
+    keys = torch.zeros(m, dtype=torch.int64, device=gpu)
+    logits = torch.empty(m, v, dtype=torch.float32, device=gpu)
+    ops.rmsnorm_lm_head_argmax(x, w, 1e-6, e, keys, logits=logits)
+    assert torch.equal(logits, logits_ref)
+    assert torch.equal(keys, keys_ref)
+    keys2 = torch.zeros(m, dtype=torch.int64, device=gpu)
+    ops.rmsnorm_lm_head_argmax(x, w, 1e-6, e, keys2)   # without logits
+    assert torch.equal(keys2, keys_ref)
+
+
 def test_decode_layer_config3(gpu):
     """One Qwen3-0.6B decode layer, batch 8, 1024 cached tokens, write at 1024."""
     cfg = gm.Qwen3Config(n_layers=1, vocab=256)

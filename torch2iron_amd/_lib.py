@@ -62,6 +62,8 @@ SIGNATURES = {
     "t2i_prefill_attention": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                                         c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "t2i_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_rmsnorm_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32,
+                                             c_void_p, c_void_p, c_void_p]),
     "t2i_greedy_advance": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
     "t2i_prompt_advance": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_stream_read_out_words": (ctypes.c_int64, [c_size_t, c_int32]),

@@ -548,9 +548,18 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
 //     k-block r and the second half likewise (lane (c, r) takes k 8 r and 32 + 8 r).
 __device__ __forceinline__ int lmh_unit(int row, int kb) { return 16 * kb + (row ^ ((2 * kb) & 15)); }
 
+//   * NORM: hin holds the un-normalised rows and the workgroup applies the final
+//     RMSNorm (gamma, eps) to its staged copy before the first product, in
+//     rmsnorm_kernel's order (thread t sums chunks t, t + 256, ... of each row,
+//     then wave_sum and the four wave partials in order), so the normalised rows
+//     and every logit carry the bits of t2i_rmsnorm followed by t2i_lm_head_argmax.
+//     This runs while the first table slice is in flight.  K is a power of two, so
+//     each thread's pieces use one or two gamma pieces, loaded with its h.
+template <bool NORM>
 __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
     const uint16_t* __restrict__ hin, int M, const uint16_t* __restrict__ E, int V, int K,
-    float* __restrict__ logits, unsigned long long* __restrict__ keys) {
+    float* __restrict__ logits, unsigned long long* __restrict__ keys, const uint16_t* __restrict__ gamma,
+    float eps) {
   // this workgroup's tiles [tb, te) of the V / 16 (contiguous, balanced)
   extern __shared__ u32x4 s_dyn[];                  // [16][K / 8] units of h, then the waves' regions
   const int ku = K / 8;                             // 16-byte units per activation row
@@ -614,17 +623,23 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
   // and stores are unconditional (clamped): a load sunk into a branch gets a wait
   // for every load in flight.
   u32x4 b0[LMH_TILES][2], b1[LMH_TILES][2];
+  constexpr int NSTEP = 64 * LMH_WAVES;   // threads: the stride of every piece loop below
+  u32x4 gv[2];                            // NORM: gamma pieces (tid + j NSTEP) % ku, j = 0, 1
   {
     const int nst = 16 * ku;   // 16-byte pieces of the 16-row tile
-    for (int base = 0; base < nst; base += 8 * 64 * LMH_WAVES) {
+    for (int base = 0; base < nst; base += 8 * NSTEP) {
       u32x4 hv[8];
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const int idx = min(base + u * 64 * LMH_WAVES + tid, nst - 1);
+        const int idx = min(base + u * NSTEP + tid, nst - 1);
         const int m = idx / ku, ch = idx - m * ku;
         hv[u] = *reinterpret_cast<const u32x4*>(hin + (size_t)min(m, M - 1) * K + ch * 8);
       }
       if (base == 0) {
+        if constexpr (NORM) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) gv[j] = *reinterpret_cast<const u32x4*>(gamma + ((tid + j * NSTEP) & (ku - 1)) * 8);
+        }
         __builtin_amdgcn_sched_barrier(0);
         load_slice(0, b0);
         __builtin_amdgcn_sched_barrier(0);
@@ -638,6 +653,63 @@ __global__ __launch_bounds__(64 * LMH_WAVES) void lm_head_kernel(
     }
   }
   __syncthreads();
+  if constexpr (NORM) {
+    // per-row sums of squares in rmsnorm_kernel's order; the partials and the
+    // rows' 1 / rms sit in the waves' regions, unused until the first product
+    float* const s_part = reinterpret_cast<float*>(s_dyn + 16 * ku);   // [16][LMH_WAVES]
+    float* const s_inv = s_part + 16 * LMH_WAVES;                       // [16]
+    float ss[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) ss[m] = 0.0f;
+    for (int ch = tid; ch < ku; ch += NSTEP) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const u32x4 v = s_hu[m * ku + (ch ^ (m & hmask))];
+        const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float lo = bf16_lo(a[j]), hi = bf16_hi(a[j]);
+          ss[m] = fmaf(lo, lo, ss[m]);
+          ss[m] = fmaf(hi, hi, ss[m]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const float w = wave_sum(ss[m]);
+      if (lane == 0) s_part[m * LMH_WAVES + wave] = w;
+    }
+    __syncthreads();
+    if (tid < 16) {
+      float total = 0.0f;
+#pragma unroll
+      for (int w = 0; w < LMH_WAVES; ++w) total += s_part[tid * LMH_WAVES + w];
+      s_inv[tid] = round_bf16(1.0f / sqrtf(total / (float)K + eps));
+    }
+    __syncthreads();
+    // each thread normalises its pieces tid + j NSTEP (gamma piece j % 2)
+    for (int j = 0; j * NSTEP < 16 * ku; ++j) {
+      const int idx = tid + j * NSTEP;
+      const int m = idx / ku, ch = idx - m * ku;
+      if (m < M) {
+        u32x4* const dst = &s_hu[m * ku + (ch ^ (m & hmask))];
+        const u32x4 v = *dst;
+        const u32x4 g = (j & 1) ? gv[1] : gv[0];
+        const float inv = s_inv[m];
+        const uint32_t a[4] = {v.x, v.y, v.z, v.w};
+        const uint32_t b[4] = {g.x, g.y, g.z, g.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float lo = round_bf16(round_bf16(bf16_lo(a[q]) * inv) * bf16_lo(b[q]));
+          const float hi = round_bf16(round_bf16(bf16_hi(a[q]) * inv) * bf16_hi(b[q]));
+          o[q] = pack_bf16x2(lo, hi);
+        }
+        *dst = u32x4{o[0], o[1], o[2], o[3]};
+      }
+    }
+    __syncthreads();
+  }
   // Loads inside the loop are unconditional (a load skipped on one path makes the
   // compiler's wait counts conservative for both); the last one or two slices are
   // peeled.
@@ -939,14 +1011,25 @@ extern "C" int t2i_decode_attention_noalloc(const uint16_t* qkv, const int32_t* 
                        stream);
 }
 
-extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,
-                                  float* logits, uint64_t* argmax_keys, void* stream) {
+namespace {
+
+// Launch the lm_head (NORM: with the final RMSNorm of x applied in the kernel)
+// over 16-row slices of the M rows.
+template <bool NORM>
+int run_lm_head(const uint16_t* h, int32_t M, const uint16_t* gamma, float eps, const uint16_t* E, int32_t V,
+                int32_t K, float* logits, uint64_t* argmax_keys, void* stream) {
   if (!h || !E || !argmax_keys) return fail(T2I_ERR_NULL, "h, E and argmax_keys must not be NULL");
   if (M < 1) return fail(T2I_ERR_SHAPE, "M=%d must be positive", M);
   if (V < 16 || V % 16) return fail(T2I_ERR_SHAPE, "V=%d must be a positive multiple of 16", V);
   if (K < 64 || K % 64 || K > LMH_MAX_K) return fail(T2I_ERR_SHAPE, "K=%d must be a multiple of 64 in [64, %d]", K, LMH_MAX_K);
   if (!aligned16(h) || !aligned16(E) || (logits && !aligned16(logits)))
     return fail(T2I_ERR_ALIGN, "lm_head tensors must be 16-byte aligned");
+  if (NORM) {
+    if (!gamma) return fail(T2I_ERR_NULL, "norm_weight must not be NULL");
+    if (K & (K - 1)) return fail(T2I_ERR_SHAPE, "K=%d must be a power of two with the fused norm", K);
+    if (!aligned16(gamma)) return fail(T2I_ERR_ALIGN, "norm_weight must be 16-byte aligned");
+    if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  }
   // at most LMH_WAVES * LMH_TILES tiles a workgroup; a multiple of 256 workgroups
   // once there are more than 256
   const int tiles = V / 16;
@@ -964,7 +1047,7 @@ extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* 
     if (rc) return rc;
     if (dev < 0 || dev >= kMaxDevices || lds > raised[dev].load(std::memory_order_relaxed)) {
       rc = t2i_host::hip_status(
-          hipFuncSetAttribute(reinterpret_cast<const void*>(t2i::lm_head_kernel),
+          hipFuncSetAttribute(reinterpret_cast<const void*>(t2i::lm_head_kernel<NORM>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds),
           "lm_head LDS attribute");
       if (rc) return rc;
@@ -978,13 +1061,26 @@ extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* 
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   for (int m0 = 0; m0 < M; m0 += 16) {
     const int mc = (M - m0) < 16 ? (M - m0) : 16;
-    hipLaunchKernelGGL(t2i::lm_head_kernel, grid, dim3(64 * LMH_WAVES), lds, s, h + (size_t)m0 * K, mc, E, V, K,
-                       logits ? logits + (size_t)m0 * V : nullptr,
-                       reinterpret_cast<unsigned long long*>(argmax_keys) + m0);
+    hipLaunchKernelGGL(t2i::lm_head_kernel<NORM>, grid, dim3(64 * LMH_WAVES), lds, s, h + (size_t)m0 * K, mc, E, V,
+                       K, logits ? logits + (size_t)m0 * V : nullptr,
+                       reinterpret_cast<unsigned long long*>(argmax_keys) + m0, gamma, eps);
     int rc = t2i_host::hip_status(hipGetLastError(), "lm_head launch");
     if (rc) return rc;
   }
   return T2I_OK;
+}
+
+}  // namespace
+
+extern "C" int t2i_lm_head_argmax(const uint16_t* h, int32_t M, const uint16_t* E, int32_t V, int32_t K,
+                                  float* logits, uint64_t* argmax_keys, void* stream) {
+  return run_lm_head<false>(h, M, nullptr, 0.0f, E, V, K, logits, argmax_keys, stream);
+}
+
+extern "C" int t2i_rmsnorm_lm_head_argmax(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                                          const uint16_t* E, int32_t V, int32_t K, float* logits,
+                                          uint64_t* argmax_keys, void* stream) {
+  return run_lm_head<true>(x, M, norm_weight, eps, E, V, K, logits, argmax_keys, stream);
 }
 
 extern "C" int t2i_greedy_advance(const uint64_t* argmax_keys, int32_t B, int32_t* tokens, int32_t* positions,

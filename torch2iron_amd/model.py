@@ -373,9 +373,11 @@ class Qwen3Model:
 
     # ---- the pieces of one step ----
     def _micro_layers(self, m: _Micro):
-        """Embedding gather + every layer for the rows of one micro-batch."""
+        """Embedding gather + every layer for the rows of one micro-batch (the gather
+        also clears the rows' argmax keys for the step's lm_head)."""
         c, b = self.cfg, m.buf
-        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens[m.b0:m.b1], x_out=b.x)
+        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=b.xn, tokens=self.tokens[m.b0:m.b1], x_out=b.x,
+                    argmax_keys=self.keys[m.b0:m.b1])
         pos = self.positions[m.b0:m.b1]
         if self.step_table is not None:
             ops.decode_step(self.step_table, b.xn, b.x, pos, c.eps, self.rope, rope_style=self.layers[0].rope_style,
@@ -388,10 +390,16 @@ class Qwen3Model:
         ops.prompt_advance(self.prompt[m.b0:m.b1], self.tokens[m.b0:m.b1], self.positions[m.b0:m.b1])
 
     def _head(self, want_logits: bool = False):
-        """Final RMSNorm of the whole batch and the tied lm_head with the fused argmax."""
+        """Final RMSNorm of the whole batch and the tied lm_head with the fused argmax,
+        in one launch (the keys were cleared by the step's embedding gather); two
+        launches when the hidden size is not a power of two."""
         c = self.cfg
+        logits = self._logits_out(want_logits)
+        if c.hidden & (c.hidden - 1) == 0:
+            ops.rmsnorm_lm_head_argmax(self.x, self.norm, c.eps, self.lm_head, self.keys, logits=logits)
+            return
         ops.rmsnorm(self.x, self.norm, c.eps, out=self.xn, argmax_keys=self.keys)
-        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=self._logits_out(want_logits))
+        ops.lm_head_argmax(self.xn, self.lm_head, self.keys, logits=logits)
 
     def _logits_out(self, want_logits: bool):
         """The fp32 ``[batch, vocab]`` logits buffer when logits are wanted, else None."""

@@ -561,6 +561,33 @@ def lm_head_argmax(h: torch.Tensor, embed: torch.Tensor, keys: torch.Tensor,
     return keys
 
 
+def rmsnorm_lm_head_argmax(x: torch.Tensor, weight: torch.Tensor, eps: float, embed: torch.Tensor,
+                           keys: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
+    """``lm_head_argmax(rmsnorm(x, weight, eps), embed, keys, logits)`` in one launch, with
+    the same bits (``keys`` zeroed beforehand; the hidden size a power of two)."""
+    _check_dev("x", x, BF16)
+    _check_dev("weight", weight, BF16)
+    _check_dev("embed", embed, BF16)
+    _check_dev("keys", keys, torch.int64)
+    if x.dim() != 2 or embed.dim() != 2:
+        raise ValueError("x must be [M, K] and embed [V, K]")
+    m, k = x.shape
+    v = embed.shape[0]
+    if embed.shape[1] != k or weight.numel() != k:
+        raise ValueError("embed must be [V, K] and weight [K] with K = x.shape[1]")
+    if keys.numel() < m:
+        raise ValueError(f"keys must hold at least {m} entries")
+    if logits is not None:
+        _check_dev("logits", logits, torch.float32)
+        if logits.numel() != m * v:
+            raise ValueError("logits must be [M, V]")
+    lib = _lib.load()
+    rc = lib.t2i_rmsnorm_lm_head_argmax(x.data_ptr(), m, weight.data_ptr(), float(eps), embed.data_ptr(), v, k,
+                                        _lib.ptr(logits), keys.data_ptr(), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_rmsnorm_lm_head_argmax")
+    return keys
+
+
 def keys_to_tokens(keys: torch.Tensor) -> torch.Tensor:
     """Decode argmax keys (``ordered << 32 | (0xFFFFFFFF - index)``) into indices."""
     low = keys & 0xFFFFFFFF
