@@ -1,9 +1,11 @@
 """The decode layer's front in one cooperative launch (``t2i_qkv_attention``): the
-RMSNorm + q|k|v projection must give the same bits as ``t2i_w4a16_rmsnorm_linear``
-(its tagged words are read back from the workspace), the KV-cache write the same
-bits as ``t2i_decode_attention``, and the context must match the oracle within the
-attention test's bars and the unfused kernels within a bf16 rounding.  Repeated
-launches and graph replays keep working (the tag advances per launch)."""
+RMSNorm + q|k|v projection (the decode linear's 16-wave tile) must match
+``t2i_w4a16_rmsnorm_linear``, whose plan may split K over 8 waves instead, up to
+the order of the fp32 partial sums (within one bf16 rounding, mostly identical;
+its tagged words are read back from the workspace); on those projection rows the
+KV-cache write must give the bits of ``t2i_decode_attention`` and the context
+match it within a bf16 rounding, and the oracle within the attention test's bars.
+Repeated launches and graph replays keep working (the tag advances per launch)."""
 
 import pytest
 import torch
@@ -58,11 +60,14 @@ def test_fused_front_matches_unfused_kernels_and_oracle(gpu, b, hq, hkv, hidden,
                             rope_style=style, workspace=ws)
     torch.cuda.synchronize()
     assert ops.qkv_attention_errors(b, hq, hkv, gpu, workspace=ws) == 0
-    # the projection, bit for bit
-    qkv = ops.linear(x, w) if normed else ops.rmsnorm_linear(x, ln, 1e-6, w)
+    # the projection, up to the order of the partial sums
+    unfused = ops.linear(x, w) if normed else ops.rmsnorm_linear(x, ln, 1e-6, w)
     buf = next(iter(ws._bufs.values()))
-    assert torch.equal(_ll_values(buf, b, n), qkv)
-    # the unfused attention on the same rows
+    qkv = _ll_values(buf, b, n)
+    g, r = qkv.float(), unfused.float()
+    assert ((g - r).abs() <= 2.0 ** -7 * r.abs() + 1e-3 * r.abs().max()).all()
+    assert (g == r).float().mean().item() >= 0.9
+    # the unfused attention on the launch's own projection rows
     ref = ops.decode_attention(qkv, pos, hq, hkv, qn, kn, 1e-6, rope, kc, vc, rope_style=style)
     assert torch.equal(kc2, kc) and torch.equal(vc2, vc), "KV-cache writes differ from the unfused kernel"
     diff = (ctx.float() - ref.float()).abs()

@@ -1,9 +1,12 @@
 """Every layer of a decode step in one cooperative launch (``t2i_decode_step``).
 
-Each linear phase must give the bits of the standalone kernel on the same input
-(read back from the launch's per-layer activations), the attention must match
-``t2i_decode_attention`` on the same q/k/v rows within one bf16 rounding with
-identical KV-cache writes, and greedy decode through the one-launch step must
+Each linear phase runs the decode linear's 16-wave tile; the standalone kernels
+may split K over 8 waves instead, so a phase must match the standalone kernel on
+the same input (read back from the launch's per-layer activations) up to the
+order of the fp32 partial sums: within one bf16 rounding, and identical for most
+outputs.  The attention must match ``t2i_decode_attention`` on the same q/k/v
+rows within one bf16 rounding (identical KV-cache writes where the launch's own
+q/k/v words are read back), and greedy decode through the one-launch step must
 agree with the separate-kernel path (tokens, logits) and with itself across
 graph replays."""
 
@@ -15,6 +18,19 @@ from torch2iron_amd import ops
 
 pytestmark = pytest.mark.gpu
 BF16 = torch.bfloat16
+
+
+def _one_rounding(got, ref, residual=None, what=""):
+    """got and ref differ at most by the order of fp32 partial sums before a bf16
+    rounding: within 2^-6 of each value (a SwiGLU output carries two roundings)
+    plus, with a residual epilogue, 2^-7 of the residual (one rounding of the sum
+    before it is added); and most values are identical."""
+    g, r = got.float(), ref.float()
+    tol = 2.0 ** -6 * r.abs() + 1e-3 * r.abs().max()
+    if residual is not None:
+        tol = tol + 2.0 ** -7 * residual.float().abs()
+    assert ((g - r).abs() <= tol).all(), f"{what}: beyond one rounding"
+    assert (g == r).float().mean().item() >= 0.9, f"{what}: fewer than 90 % identical"
 
 
 def _model(gpu, cfg, b, cap, seed, persistent=True, weights="centered"):
@@ -53,19 +69,26 @@ def test_step_phases_match_standalone_kernels(gpu, b, cap, positions):
         x_in = x0 if li == 0 else mid["x"][li - 1]
         x_out = m.x if li == cfg.n_layers - 1 else mid["x"][li]
         qkv = ops.linear(xn0, w.qkv) if li == 0 else ops.rmsnorm_linear(x_in, w.ln1, c.eps, w.qkv)
-        if li == cfg.n_layers - 1:
-            assert torch.equal(mid["qkv"], qkv), "qkv projection bits"
+        last = li == cfg.n_layers - 1
+        if last:
+            _one_rounding(mid["qkv"], qkv, what=f"layer {li} qkv")
+            qkv = mid["qkv"]   # the launch's own q/k/v words: the KV writes must then be identical
         ref = ops.decode_attention(qkv, m.positions, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, m.rope,
                                    kc_ref[li], vc_ref[li], rope_style=layer.rope_style)
         got = mid["ctx"][li]
         diff = (got.float() - ref.float()).abs()
         assert (diff <= 2.0 ** -7 * ref.float().abs() + 1e-3 * ref.float().abs().max()).all(), f"layer {li} context"
-        assert torch.equal(m.k_cache[li], kc_ref[li]) and torch.equal(m.v_cache[li], vc_ref[li]), f"layer {li} KV"
-        # the linear phases, bit for bit, each on the launch's own input rows
-        assert torch.equal(mid["xmid"][li], ops.linear(got, w.o, residual=x_in)), f"layer {li} o_proj"
-        assert torch.equal(mid["h"][li], ops.rmsnorm_gate_up(mid["xmid"][li], w.ln2, c.eps, w.gate_up)), \
-            f"layer {li} gate_up"
-        assert torch.equal(x_out, ops.linear(mid["h"][li], w.down, residual=mid["xmid"][li])), f"layer {li} down"
+        if last:
+            assert torch.equal(m.k_cache[li], kc_ref[li]) and torch.equal(m.v_cache[li], vc_ref[li]), f"layer {li} KV"
+        else:
+            _one_rounding(m.k_cache[li], kc_ref[li], what=f"layer {li} K")
+            _one_rounding(m.v_cache[li], vc_ref[li], what=f"layer {li} V")
+        # the linear phases, each on the launch's own input rows
+        _one_rounding(mid["xmid"][li], ops.linear(got, w.o, residual=x_in), residual=x_in, what=f"layer {li} o_proj")
+        _one_rounding(mid["h"][li], ops.rmsnorm_gate_up(mid["xmid"][li], w.ln2, c.eps, w.gate_up),
+                      what=f"layer {li} gate_up")
+        _one_rounding(x_out, ops.linear(mid["h"][li], w.down, residual=mid["xmid"][li]), residual=mid["xmid"][li],
+                      what=f"layer {li} down")
 
 
 def test_step_greedy_decode_matches_separate_kernels(gpu):

@@ -4,8 +4,10 @@
 //
 // One 16-wave workgroup per CU, all co-resident (cooperative launch).  Every
 // workgroup first computes one 16-column block of the qkv projection for all
-// rows (the decode linear's tile, bit-identical to t2i_w4a16_rmsnorm_linear)
-// and sends each value out as a tagged 64-bit word; it then runs one
+// rows (the decode linear's 16-wave tile: t2i_w4a16_rmsnorm_linear's arithmetic,
+// whose standalone plan may split K over 8 waves instead, so the two agree up to
+// the order of the fp32 partial sums) and sends each value out as a tagged
+// 64-bit word; it then runs one
 // (sequence, kv head, context split) attention item on those words
 // (attn_item.h).  The item's first K / V slots are issued into LDS right after
 // the projection's first loads, so the context stream overlaps the projection.

@@ -17,9 +17,11 @@
 // written once all of layer l's residual stream exists, which needs every
 // context row of layer l, which needs every read of layer l's qkv words.
 //
-// The linear phases run the standalone linear's plans (plan_linear) with its
-// chunk ranges, arithmetic and reduction order: each phase's output has the
-// bits t2i_w4a16_* give on the same input.  The attention items are those of
+// The linear phases run the decode linear's tiles (linear_phase, with
+// linear_tile's chunk ranges, arithmetic and reduction order) on the plans
+// plan_linear gives 16-wave workgroups: the standalone kernels take 8 waves
+// where that is faster, so a phase's output matches t2i_w4a16_* on the same
+// input up to the order of the fp32 partial sums (within one bf16 rounding).  The attention items are those of
 // t2i_qkv_attention.  Layer 0 takes its input already normalised (the embedding
 // gather fuses that RMSNorm); the residual stream comes in and goes out in x.
 //
@@ -348,10 +350,10 @@ DsPlan ds_plan(int cus, int B, int L, int H, int I, int Hq, int Hkv) {
   if (H <= 0 || H % 128 || I <= 0 || I % 128) return pl;
   const int D = ATT_D;
   const int Nqkv = (Hq + 2 * Hkv) * D;
-  if (!ds_phase(plan_linear(B, H, Nqkv, false, true), 1, DS_CHUNKS, &pl.qkv)) return pl;
-  if (!ds_phase(plan_linear(B, Hq * D, H, false, false), 1, DS_CHUNKS, &pl.o)) return pl;
-  if (!ds_phase(plan_linear(B, H, 2 * I, true, true), 2, DS_CHUNKS, &pl.gu)) return pl;
-  if (!ds_phase(plan_linear(B, I, H, false, false), 1, DS_CHUNKS_DOWN, &pl.dn)) return pl;
+  if (!ds_phase(plan_linear(B, H, Nqkv, false, true, true), 1, DS_CHUNKS, &pl.qkv)) return pl;
+  if (!ds_phase(plan_linear(B, Hq * D, H, false, false, true), 1, DS_CHUNKS, &pl.o)) return pl;
+  if (!ds_phase(plan_linear(B, H, 2 * I, true, true, true), 2, DS_CHUNKS, &pl.gu)) return pl;
+  if (!ds_phase(plan_linear(B, I, H, false, false, true), 1, DS_CHUNKS_DOWN, &pl.dn)) return pl;
   pl.G = cus;
   pl.U = B * Hkv;
   if (pl.U > pl.G) return pl;

@@ -418,6 +418,8 @@ using namespace t2i;
 // Row tiles beyond 16 rows go to grid.z (measured faster than multi-tile waves
 // on every Qwen3 shape at M = 32 and 64).
 #define T2I_LINEAR_CONFIGS(X) \
+  X(1, 1, 8, 2)               \
+  X(1, 1, 8, 4)               \
   X(1, 1, 16, 4)              \
   X(1, 1, 16, 2)              \
   X(1, 2, 16, 4)              \
@@ -462,13 +464,14 @@ void finish_plan(LinearPlan& pl, int M, int K, int N) {
 // compiled plans: one 16-row tile per workgroup (more rows go to grid.z and
 // share the weights in their XCD's L2), and the narrowest column block that
 // keeps the column-block x row-tile count at 256 or less: 16 columns (1 word
-// per lane, 16 waves, chunks of 2 k-steps), else 32 (2 words, 8 waves; paired
-// outputs 16 waves, see below), else 64 (4 words, 8 waves).  The rule picks the measured optimum, or a plan
-// within 4 % of it, at 38 of the 40 shape/M points, and is within 9 % at all.  Splitting K across workgroups was measured slower:
+// per lane, 16 waves, chunks of 2 k-steps; 8 waves up to 16 rows, see the end),
+// else 32 (2 words, 8 waves), else 64 (4 words, 8 waves).  The rule picks the
+// measured optimum, or a plan within 4 % of it, at 38 of the 40 shape/M points,
+// and is within 9 % at all.  Splitting K across workgroups was measured slower:
 // the fp32 partials and an arrival counter add memory round trips that cost
 // more than the parallelism they add at these sizes, so K is only split
 // between the waves of a workgroup.
-LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm) {
+LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm, bool wide) {
   LinearPlan pl{};
   pl.MT = 1;
   pl.CK = 4;
@@ -477,28 +480,50 @@ LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm) {
     // (N not a multiple of 32: 16-column blocks are the only whole ones)
     pl.LW = 1; pl.W = 16; pl.CK = 2;
   } else if ((N / 32) * mz <= 256 || N % 64) {
-    // The fused-norm paired (RMSNorm + gate/up) output takes 16 waves of 2-step
-    // chunks, the configuration the one-launch decode step runs (its workgroups
-    // have 16 waves and 128 registers a lane), so both paths give the same bits;
-    // 8 waves of 4-step chunks measured 0.1-0.2 us faster on the Qwen3-0.6B
-    // gate_up at M <= 16 (4.62 against 4.73 us at M = 16) but need 148 registers
-    // a lane with the norm, and stay the plan without it.
+    // The fused-norm paired (RMSNorm + gate/up) output takes 8 waves of 4-step
+    // chunks like the plain one (0.12-0.18 us faster than 16 waves of 2-step
+    // chunks on the Qwen3-0.6B gate_up at M <= 16, at 148 registers a lane);
+    // 16-wave workgroups (wide) take 16 waves of 2-step chunks.
     pl.LW = 2;
-    pl.W = paired && norm ? 16 : 8;
-    pl.CK = paired && norm ? 2 : 4;
+    pl.W = paired && norm && wide ? 16 : 8;
+    pl.CK = paired && norm && wide ? 2 : 4;
   } else {
     pl.LW = 4; pl.W = 8;
   }
+  bool chosen = false;   // tuning builds: a plan given in T2I_PLAN is kept as given
 #ifdef T2I_TUNING
   // tuning builds only: T2I_PLAN="MT,LW,W,CK" overrides the choice
   if (const char* env = getenv("T2I_PLAN")) {
     LinearPlan o = pl;
     if (sscanf(env, "%d,%d,%d,%d", &o.MT, &o.LW, &o.W, &o.CK) == 4 && config_exists(o.MT, o.LW, o.W, o.CK) &&
-        N % (16 * o.LW) == 0 && (!paired || o.LW >= 2))
+        N % (16 * o.LW) == 0 && (!paired || o.LW >= 2)) {
       pl = o;
+      chosen = true;
+    }
   }
 #endif
   finish_plan(pl, M, K, N);
+  // 16-column blocks of one row tile (M <= 16): 8 waves, when each wave's chunks
+  // still fit the straight schedules (6 a wave, 3 with the fused norm): half the
+  // partial sums to reduce and half the waves to meet at the barrier, the same
+  // loads in flight.  Chunks of 4 k-steps for the narrow, deep outputs (N <= 1024,
+  // K >= 2048: the Qwen3-0.6B o_proj and down), else 2 -- chosen by the shape
+  // alone, so that every M up to 16 splits K alike and a row's outputs do not
+  // depend on how many rows share the launch.  Measured HBM-cold (us a launch,
+  // the 16-wave plan -> this one), Qwen3-0.6B: qkv 2.97 -> 2.80 (M = 1), 3.37 ->
+  // 3.23 (M = 16), with the fused norm 4.18 -> 3.91 (M = 16); down 3.99 -> 3.82
+  // (M = 1), 4.21 -> 4.03 (M = 16); o_proj 3.38 -> 3.31 (M = 1), 3.49 -> 3.36
+  // (M = 16); at M = 32 and 64 the two are within 0.1 us.  More chunks a wave
+  // than the straight schedules hold (Qwen3-1.7B down, K = 6144) stay at 16 waves.
+  const int lim = norm ? 3 : 6;
+  if (!wide && !chosen && pl.LW == 1 && M <= 16) {
+    const int ck = N <= 1024 && K >= 2048 ? 4 : 2;
+    if (K / (32 * ck * 8) <= lim) {
+      pl.W = 8;
+      pl.CK = ck;
+      pl.chunks = K / (32 * ck);
+    }
+  }
   return pl;
 }
 
@@ -608,7 +633,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p);
     return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
   }
-  const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr);
+  const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr, false);
   LinearParams p{};
   p.x = x;
   p.qw = reinterpret_cast<const uint32_t*>(qweight);

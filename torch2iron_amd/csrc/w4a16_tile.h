@@ -788,5 +788,6 @@ struct LinearPlan {
   int cbs;      // column blocks (grid.x)
   int chunks;   // K / (32 * CK)
 };
-LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm);
+// wide: the plan for 16-wave workgroups (the one-launch decode step's).
+LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm, bool wide);
 }  // namespace t2i_host

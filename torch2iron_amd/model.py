@@ -20,7 +20,8 @@ KV write live in the attention prologue.
 A whole decode step is captured once into a HIP graph and replayed; token ids,
 positions and the output history stay on the device between steps.  The
 layers can instead run as one cooperative launch per step (``t2i_decode_step``,
-``persistent=True``), whose phases give the separate kernels' bits; it measured
+``persistent=True``), whose phases match the separate kernels within one bf16
+rounding (16-wave tiles: another order of the fp32 partial sums); it measured
 slower (see ``Qwen3Model``) and is off by default.
 """
 
