@@ -26,6 +26,9 @@ CASES += [(3, 1024, 3072), (17, 2048, 1024), (50, 1024, 4096), (33, 3072, 1024),
 # row tiles shorter than 16 rows (few column blocks): 4-row tiles with a 1-row last
 # tile, 1-row tiles, 2-row tiles
 CASES += [(13, 2048, 1024), (16, 1024, 256), (6, 3072, 1024)]
+# two 16-row m-tiles a workgroup (64-column blocks needing one to two rounds of the
+# CUs): a ragged second tile, and the Qwen3-1.7B gate_up at M = 32
+CASES += [(48, 1024, 6144), (32, 2048, 12288)]
 
 
 def _inputs(m, k, n, seed):

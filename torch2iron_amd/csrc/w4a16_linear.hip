@@ -418,6 +418,7 @@ using namespace t2i;
 // Row tiles beyond 16 rows go to grid.z (measured faster than multi-tile waves
 // on every Qwen3 shape at M = 32 and 64).
 #define T2I_LINEAR_CONFIGS(X) \
+  X(2, 4, 8, 4)               \
   X(1, 1, 8, 2)               \
   X(1, 1, 8, 4)               \
   X(1, 1, 16, 4)              \
@@ -489,6 +490,15 @@ LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm, bool wide) {
     pl.CK = paired && norm && wide ? 2 : 4;
   } else {
     pl.LW = 4; pl.W = 8;
+    // Two 16-row m-tiles a workgroup (each weight dequantised once for 32 rows)
+    // when the one-tile plan would need between one and two rounds of the 256
+    // CUs: then one round.  Measured HBM-cold (us a launch, one tile -> two):
+    // Qwen3-0.6B gate_up at M = 64 6.56 -> 5.79, Qwen3-1.7B gate_up at M = 32
+    // 9.72 -> 9.09; at 2 or more rounds (Qwen3-1.7B gate_up, M = 64) and at
+    // every other plan, one tile is faster.  Outputs carry the one-tile plan's
+    // bits (the rows of an MFMA tile are independent).
+    const int groups = (N / 64) * mz;
+    if (!norm && !wide && groups > 256 && groups <= 512) pl.MT = 2;
   }
   bool chosen = false;   // tuning builds: a plan given in T2I_PLAN is kept as given
 #ifdef T2I_TUNING
@@ -562,11 +572,16 @@ hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm
   // tuning builds only: T2I_XROWS_MIN_RT = smallest row tile given whole-row loads (17: never)
   if (const char* env = getenv("T2I_XROWS_MIN_RT")) min_rt = atoi(env);
 #endif
-  if constexpr (XOK) {
-    if (p.rt >= min_rt)
-      return norm ? launch_t<MT, LW, W, CK, true, true>(p, grid, s) : launch_t<MT, LW, W, CK, false, true>(p, grid, s);
+  if constexpr (MT > 1) {   // the fused norm and whole-row loads work on one 16-row tile
+    (void)min_rt;
+    return norm ? hipErrorInvalidValue : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
+  } else {
+    if constexpr (XOK) {
+      if (p.rt >= min_rt)
+        return norm ? launch_t<MT, LW, W, CK, true, true>(p, grid, s) : launch_t<MT, LW, W, CK, false, true>(p, grid, s);
+    }
+    return norm ? launch_t<MT, LW, W, CK, true, false>(p, grid, s) : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
   }
-  return norm ? launch_t<MT, LW, W, CK, true, false>(p, grid, s) : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
 }
 
 hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, hipStream_t s) {
