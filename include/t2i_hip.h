@@ -278,6 +278,24 @@ int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, i
                           uint16_t* out, void* stream);
 
 /* ---------------------------------------------------------------------------
+ * The prompt pass's q|k|v projection and its q/k RMSNorm + RoPE + KV-cache write
+ * in one launch: exactly t2i_w4a16_linear(x, B*T rows, the fused q|k|v weight,
+ * N = (Hq + 2*Hkv) * D) followed by t2i_prefill_qk_rope_kv on its output (the
+ * same bits in q_out and the caches), without writing or reading back the
+ * projection.  Each 64-row x 128-column tile of the prompt GEMM is one head, and
+ * its epilogue runs the prep on it.  B*T >= 512 (the prompt GEMM's rows), D = 128;
+ * every pointer 16-byte aligned.
+ * Replaces: the q|k|v projection and the per-head norm / RoPE / cache write of the
+ *           prompt pass (quantized_qwen3/model.py:240-253 per token, and
+ *           quantized_qwen3/prefill_runtime.py:95-164 on the NPU).
+ */
+int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0, const int32_t* qweight,
+                            const int32_t* qzeros, const uint16_t* scales, int32_t K, int32_t group_size,
+                            int32_t Hq, int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
+                            float eps, const uint16_t* rope, int32_t rope_style, uint16_t* q_out,
+                            uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Tied bf16 lm_head with a fused greedy argmax.
  * logits[m][v] = sum_k h[m][k] * E[v][k] in fp32 (E bf16 [V, K], K % 64 == 0, V % 16 == 0).
  * argmax_keys (uint64 [M], zeroed beforehand, e.g. by t2i_rmsnorm) receives

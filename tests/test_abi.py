@@ -93,6 +93,21 @@ def test_prefill_entry_points_validate():
     assert att(*a) == _lib.T2I_ERR_ALIGN
     a = list(args); a[2], a[3] = 700, 0
     assert att(*a) == _lib.T2I_ERR_SHAPE
+    fused = lib.t2i_prefill_qkv_rope_kv
+    args = [FAKE, 16, 512, 0, FAKE, FAKE, FAKE, 1024, 128, 16, 8, 128, FAKE, FAKE, 1e-6, FAKE, 0, FAKE, FAKE, FAKE,
+            640, None]
+    a = list(args); a[1], a[2] = 2, 100
+    assert fused(*a) == _lib.T2I_ERR_SHAPE                      # 200 rows: below the prompt GEMM
+    a = list(args); a[11] = 64
+    assert fused(*a) == _lib.T2I_ERR_SHAPE                      # head_dim 64
+    a = list(args); a[20] = 500
+    assert fused(*a) == _lib.T2I_ERR_SHAPE                      # positions beyond the cache
+    a = list(args); a[8] = 64
+    assert fused(*a) == _lib.T2I_ERR_GROUP
+    a = list(args); a[17] = FAKE + 2
+    assert fused(*a) == _lib.T2I_ERR_ALIGN
+    a = list(args); a[12] = None
+    assert fused(*a) == _lib.T2I_ERR_NULL
 
 
 def test_other_entry_points_validate():

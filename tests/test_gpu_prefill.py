@@ -106,6 +106,40 @@ def _oracle_cfg(cfg):
     return oq.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__})
 
 
+@pytest.mark.parametrize("style", [0, 1])
+@pytest.mark.parametrize("b,t,p0,hq,hkv,k,cap", [
+    (16, 512, 0, 16, 8, 1024, 640),     # the Qwen3-0.6B prompt pass
+    (3, 200, 37, 16, 4, 2048, 300),     # 600 rows: a ragged last row tile; 4 q heads a kv head; p0 > 0
+    (1, 512, 0, 8, 8, 1024, 512),       # one q head a kv head, the cache exactly full
+])
+def test_fused_prompt_projection_matches_two_launches(gpu, b, t, p0, hq, hkv, k, cap, style):
+    """The prompt GEMM with the q/k norm + RoPE + cache write in its epilogue gives
+    the bits of the projection followed by t2i_prefill_qk_rope_kv: q rows and both
+    caches (slots outside p0 .. p0 + T - 1 untouched)."""
+    print(f"fused prompt projection B={b} T={t} p0={p0} Hq={hq} Hkv={hkv} K={k} style={style}", flush=True)
+    from oracle import w4a16 as ow
+    from torch2iron_amd.formats import W4A16Weight
+    d = 128
+    n = (hq + 2 * hkv) * d
+    w = W4A16Weight.from_numpy(*ow.synthetic_tensors(k, n, seed=b + t + k), device=gpu)
+    g = torch.Generator().manual_seed(t + p0)
+    x = (torch.randn(b * t, k, generator=g) * 2).to(BF16).to(gpu)
+    kc0 = torch.randn(b, hkv, cap, d, generator=g).to(BF16).to(gpu)
+    vc0 = torch.randn(b, hkv, cap, d, generator=g).to(BF16).to(gpu)
+    qn = (torch.rand(d, generator=g) * 0.2 + 0.9).to(BF16).to(gpu)
+    kn = (torch.rand(d, generator=g) * 0.2 + 0.9).to(BF16).to(gpu)
+    rope = gm.rope_table(d, cap, 1e6, gpu)
+    kc_ref, vc_ref = kc0.clone(), vc0.clone()
+    q_ref = ops.prefill_qk_rope_kv(ops.linear(x, w), b, p0, hq, hkv, qn, kn, 1e-6, rope, kc_ref, vc_ref,
+                                   rope_style=style)
+    kc, vc = kc0.clone(), vc0.clone()
+    q = ops.prefill_qkv_rope_kv(x, w, b, p0, hq, hkv, qn, kn, 1e-6, rope, kc, vc, rope_style=style)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q_ref), "q rows"
+    assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref), "KV cache"
+    assert not torch.equal(kc, kc0)   # the prompt's slots were written
+
+
 @pytest.mark.parametrize("weights", ["centered", "uniform"])
 def test_model_prefill_matches_oracle(gpu, weights):
     """Whole prompt pass (3 layers, batch 4, 70 tokens): the KV cache and the first

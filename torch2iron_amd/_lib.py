@@ -61,6 +61,9 @@ SIGNATURES = {
                                          c_void_p, c_int32, c_void_p]),
     "t2i_prefill_attention": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
                                         c_void_p, c_void_p, c_int32, c_void_p, c_void_p]),
+    "t2i_prefill_qkv_rope_kv": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
+                                          c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p,
+                                          c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
     "t2i_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_rmsnorm_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32,
                                              c_void_p, c_void_p, c_void_p]),

@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "t2i_common.h"
+#include "qk_prep.h"
 
 namespace t2i {
 
@@ -37,54 +38,13 @@ struct PrefillPrepParams {
   float eps;
 };
 
-// One workgroup (4 waves) per prompt row.  A head vector (D = 128) is held by a
-// 16-lane row of a wave: lane c holds the 4 rotation pairs p = 4c .. 4c + 3,
-// elements (i0, i1) = (p, p + 64) (two halves) or (2p, 2p + 1) (interleaved),
-// that is two 8-byte pieces or one 16-byte piece of the vector, and the 4
-// (cos, sin) pairs of the RoPE row as one 16-byte piece.  A wave covers 4
-// vectors, the workgroup 16 at a time; every load of PREP_NB such batches (and
-// the norm weights and the RoPE row) is issued before the first vector is
-// normalised.  Loads are unconditional (vectors past the last reload it; nothing
-// is stored for them).  The sum of squares of a vector is a 16-lane DPP sum.
+// One workgroup (4 waves) per prompt row.  A head vector is held by a 16-lane
+// row of a wave (the lane layout of qk_prep.h).  A wave covers 4 vectors, the
+// workgroup 16 at a time; every load of PREP_NB such batches (and the norm
+// weights and the RoPE row) is issued before the first vector is normalised.
+// Loads are unconditional (vectors past the last reload it; nothing is stored
+// for them).
 constexpr int PREP_NB = 2;
-
-// Lane c's piece of a head vector: style 0 the i0 values of pairs 4c .. 4c + 3
-// then their i1 values (two 8-byte pieces), style 1 the four pairs interleaved.
-__device__ __forceinline__ u32x4 prep_load(const uint16_t* vec, int c, int style) {
-  if (style == 0) {
-    const u32x2 a = *reinterpret_cast<const u32x2*>(vec + 4 * c);
-    const u32x2 b = *reinterpret_cast<const u32x2*>(vec + 64 + 4 * c);
-    return u32x4{a.x, a.y, b.x, b.y};
-  }
-  return *reinterpret_cast<const u32x4*>(vec + 8 * c);
-}
-
-__device__ __forceinline__ void prep_unpack(u32x4 v, int style, float (&x0)[4], float (&x1)[4]) {
-  if (style == 0) {
-    x0[0] = bf16_lo(v.x); x0[1] = bf16_hi(v.x); x0[2] = bf16_lo(v.y); x0[3] = bf16_hi(v.y);
-    x1[0] = bf16_lo(v.z); x1[1] = bf16_hi(v.z); x1[2] = bf16_lo(v.w); x1[3] = bf16_hi(v.w);
-  } else {
-    x0[0] = bf16_lo(v.x); x1[0] = bf16_hi(v.x); x0[1] = bf16_lo(v.y); x1[1] = bf16_hi(v.y);
-    x0[2] = bf16_lo(v.z); x1[2] = bf16_hi(v.z); x0[3] = bf16_lo(v.w); x1[3] = bf16_hi(v.w);
-  }
-}
-
-__device__ __forceinline__ u32x4 prep_pack(const float (&y0)[4], const float (&y1)[4], int style) {
-  if (style == 0)
-    return u32x4{pack_bf16x2(y0[0], y0[1]), pack_bf16x2(y0[2], y0[3]), pack_bf16x2(y1[0], y1[1]),
-                 pack_bf16x2(y1[2], y1[3])};
-  return u32x4{pack_bf16x2(y0[0], y1[0]), pack_bf16x2(y0[1], y1[1]), pack_bf16x2(y0[2], y1[2]),
-               pack_bf16x2(y0[3], y1[3])};
-}
-
-__device__ __forceinline__ void prep_store(uint16_t* vec, int c, int style, u32x4 v) {
-  if (style == 0) {
-    *reinterpret_cast<u32x2*>(vec + 4 * c) = u32x2{v.x, v.y};
-    *reinterpret_cast<u32x2*>(vec + 64 + 4 * c) = u32x2{v.z, v.w};
-  } else {
-    *reinterpret_cast<u32x4*>(vec + 8 * c) = v;
-  }
-}
 
 __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepParams p) {
   constexpr int D = PF_D;
@@ -110,37 +70,18 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepPara
 #pragma unroll
     for (int j = 0; j < PREP_NB; ++j) asm volatile("" : "+v"(raw[j]));
     __builtin_amdgcn_sched_barrier(0);
-    const float cs[4] = {bf16_lo(rp.x), bf16_lo(rp.y), bf16_lo(rp.z), bf16_lo(rp.w)};
-    const float sn[4] = {bf16_hi(rp.x), bf16_hi(rp.y), bf16_hi(rp.z), bf16_hi(rp.w)};
-    float gq0[4], gq1[4], gk0[4], gk1[4];
-    prep_unpack(gqv, p.style, gq0, gq1);
-    prep_unpack(gkv, p.style, gk0, gk1);
 #pragma unroll
     for (int j = 0; j < PREP_NB; ++j) {
       const int vi = base + 16 * j + slot;   // uniform over the 16-lane row
-      float x0[4], x1[4];
-      prep_unpack(raw[j], p.style, x0, x1);
       const bool isq = vi < p.Hq;
       const bool normed = vi < p.Hq + p.Hkv;   // q and k: RMSNorm + RoPE; v as is
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) ss += x0[e] * x0[e] + x1[e] * x1[e];
-      ss = row_sum16(ss);
-      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-      float y0[4], y1[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float n0 = round_bf16(round_bf16(x0[e] * inv) * (isq ? gq0[e] : gk0[e]));
-        const float n1 = round_bf16(round_bf16(x1[e] * inv) * (isq ? gq1[e] : gk1[e]));
-        y0[e] = normed ? round_bf16(round_bf16(n0 * cs[e]) + round_bf16(-n1 * sn[e])) : x0[e];
-        y1[e] = normed ? round_bf16(round_bf16(n1 * cs[e]) + round_bf16(n0 * sn[e])) : x1[e];
-      }
+      const u32x4 y = prep_vector(raw[j], rp, isq ? gqv : gkv, normed, p.style, p.eps);
       if (vi >= nvec) continue;
       uint16_t* dst;
       if (isq) dst = p.q + (((size_t)b * p.Hq + vi) * p.T + t) * D;
       else if (normed) dst = p.kc + (((size_t)b * p.Hkv + (vi - p.Hq)) * p.cap + pos) * D;
       else dst = p.vc + (((size_t)b * p.Hkv + (vi - p.Hq - p.Hkv)) * p.cap + pos) * D;
-      prep_store(dst, c, p.style, prep_pack(y0, y1, p.style));
+      prep_store(dst, c, p.style, y);
     }
   }
 }

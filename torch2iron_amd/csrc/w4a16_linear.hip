@@ -29,6 +29,7 @@
 
 #include "t2i_common.h"
 #include "w4a16_tile.h"
+#include "qk_prep.h"
 
 namespace t2i {
 
@@ -275,7 +276,7 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wn, int la
   }
 }
 
-__global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearParams p) {
+__global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearParams p, const QkvPrepParams pp) {
   __shared__ GemmStage stg[GM_STAGES];
   const int lane = threadIdx.x & 63;
   const int wn = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // the wave's 32-column slice
@@ -319,7 +320,50 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
   // one column of four rows, which would take 2-byte stores).
   uint16_t* ep = reinterpret_cast<uint16_t*>(&stg[0]) + wn * GM_EP_WAVE;
   const int ncolw = n0 + GM_WCOLS * wn;        // the wave's first column
-  if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
+  if (p.epi == EPI_QKV_PREP) {
+    // The 64 x 128 tile is one head of rows m0 .. m0 + 63: every wave parks its 32
+    // columns, then each 16-lane row g = 4 wn + r takes tile rows g, g + 16, g + 32,
+    // g + 48 through prep_vector, as prefill_prep_kernel does for the same rows.
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < GM_NJ; ++j)
+          ep[(16 * mi + 4 * r + i) * GM_EP_LD + 16 * j + c] = (uint16_t)f32_to_bf16(total[mi][j][i]);
+    const int head = n0 / ATT_D;   // uniform: q heads, then k, then v
+    const bool isq = head < pp.Hq;
+    const bool normed = head < pp.Hq + pp.Hkv;
+    const u32x4 gv = prep_load(isq ? pp.qn : pp.kn, c, pp.style);   // loaded (unused) for v too
+    __syncthreads();   // the other waves' columns are in LDS (waits for the stores, unlike lds_barrier)
+    const uint16_t* tile = reinterpret_cast<const uint16_t*>(&stg[0]);
+    const int g = 4 * wn + r;
+#pragma unroll
+    for (int rr = 0; rr < GM_BM / 16; ++rr) {
+      const int row = g + 16 * rr;
+      const int m = m0 + row;
+      if (m >= p.M) continue;   // uniform over the 16-lane row
+      const int b = m / pp.T, t = m - b * pp.T, pos = pp.p0 + t;
+      // the lane's piece (prep_load's layout): column col of the tile lies in wave
+      // col / 32's region at col % 32
+      u32x4 raw;
+      if (pp.style == 0) {
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(tile + (c >> 3) * GM_EP_WAVE + row * GM_EP_LD + 4 * (c & 7));
+        const u32x2 hi =
+            *reinterpret_cast<const u32x2*>(tile + (2 + (c >> 3)) * GM_EP_WAVE + row * GM_EP_LD + 4 * (c & 7));
+        raw = u32x4{lo.x, lo.y, hi.x, hi.y};
+      } else {
+        raw = *reinterpret_cast<const u32x4*>(tile + (c >> 2) * GM_EP_WAVE + row * GM_EP_LD + 8 * (c & 3));
+      }
+      const u32x4 rp = *reinterpret_cast<const u32x4*>(pp.rope + (size_t)pos * ATT_D + 8 * c);
+      const u32x4 y = prep_vector(raw, rp, gv, normed, pp.style, pp.eps);
+      uint16_t* dst;
+      if (isq) dst = pp.q + (((size_t)b * pp.Hq + head) * pp.T + t) * ATT_D;
+      else if (normed) dst = pp.kc + (((size_t)b * pp.Hkv + (head - pp.Hq)) * pp.cap + pos) * ATT_D;
+      else dst = pp.vc + (((size_t)b * pp.Hkv + (head - pp.Hq - pp.Hkv)) * pp.cap + pos) * ATT_D;
+      prep_store(dst, c, pp.style, y);
+    }
+  } else if (p.epi == EPI_STORE || p.epi == EPI_RESIDUAL) {
 #pragma unroll
     for (int mi = 0; mi < GM_MF; ++mi)
 #pragma unroll
@@ -415,8 +459,8 @@ namespace t2i_host {
 using namespace t2i;
 
 // Compiled tile configurations: (MT m-tiles, LW words per lane, W waves, CK k-steps per chunk).
-// Row tiles beyond 16 rows go to grid.z (measured faster than multi-tile waves
-// on every Qwen3 shape at M = 32 and 64).
+// Row tiles beyond 16 rows go to grid.z, except for the 64-column outputs that
+// two m-tiles bring from one-to-two rounds of the CUs to one (plan_linear).
 #define T2I_LINEAR_CONFIGS(X) \
   X(2, 4, 8, 4)               \
   X(1, 1, 8, 2)               \
@@ -645,7 +689,8 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     p.ldy = paired ? N / 2 : N;
     p.epi = epi;
     const unsigned tiles = (unsigned)((M + GM_BM - 1) / GM_BM) * (unsigned)(N / GM_BN);
-    hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p);
+    hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p,
+                       QkvPrepParams{});
     return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
   }
   const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr, false);
@@ -670,6 +715,49 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
 }
 
 }  // namespace
+
+extern "C" int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0, const int32_t* qweight,
+                                       const int32_t* qzeros, const uint16_t* scales, int32_t K, int32_t group_size,
+                                       int32_t Hq, int32_t Hkv, int32_t D, const uint16_t* q_norm,
+                                       const uint16_t* k_norm, float eps, const uint16_t* rope, int32_t rope_style,
+                                       uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
+                                       void* stream) {
+  if (!x || !q_norm || !k_norm || !rope || !q_out || !k_cache || !v_cache)
+    return fail(T2I_ERR_NULL, "prefill projection pointers must not be NULL");
+  if (D != ATT_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
+  if (B < 1 || T < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq + 2 * Hkv > 0x3FFF)
+    return fail(T2I_ERR_SHAPE, "B=%d T=%d Hq=%d Hkv=%d invalid", B, T, Hq, Hkv);
+  const long long M = (long long)B * T;
+  if (M < gemm_min_rows() || M > T2I_MAX_ROWS)
+    return fail(T2I_ERR_SHAPE, "B*T=%lld must be in [%d, %d] (the prompt GEMM)", M, gemm_min_rows(), T2I_MAX_ROWS);
+  if (p0 < 0 || ctx_cap < 1 || p0 + T > ctx_cap)
+    return fail(T2I_ERR_SHAPE, "positions %d..%d exceed the cache (%d)", p0, p0 + T - 1, ctx_cap);
+  if (rope_style != 0 && rope_style != 1) return fail(T2I_ERR_VALUE, "rope_style must be 0 or 1");
+  if (!(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+  const int N = (Hq + 2 * Hkv) * ATT_D;
+  int rc = check_weights(qweight, qzeros, scales, K, N, group_size);
+  if (rc) return rc;
+  if (!aligned16(x) || !aligned16(q_out) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(rope) ||
+      !aligned16(q_norm) || !aligned16(k_norm))
+    return fail(T2I_ERR_ALIGN, "prefill projection tensors must be 16-byte aligned");
+  LinearParams p{};
+  p.x = x;
+  p.qw = reinterpret_cast<const uint32_t*>(qweight);
+  p.qz = reinterpret_cast<const uint32_t*>(qzeros);
+  p.sc = scales;
+  p.M = (int)M; p.K = K; p.N = N;
+  p.ldx = K;
+  p.ldy = N;
+  p.epi = EPI_QKV_PREP;
+  QkvPrepParams pp{};
+  pp.qn = q_norm; pp.kn = k_norm; pp.rope = rope; pp.q = q_out; pp.kc = k_cache; pp.vc = v_cache;
+  pp.T = T; pp.Hq = Hq; pp.Hkv = Hkv; pp.cap = ctx_cap; pp.p0 = p0; pp.style = rope_style; pp.eps = eps;
+  static_assert(GM_BN == ATT_D, "one prompt-GEMM column tile is one head");
+  const unsigned tiles = (unsigned)((M + GM_BM - 1) / GM_BM) * (unsigned)(N / GM_BN);
+  hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p,
+                     pp);
+  return t2i_host::hip_status(hipGetLastError(), "prefill projection launch");
+}
 
 extern "C" int t2i_w4a16_linear(const uint16_t* x, int32_t M, const int32_t* qweight,
                                 const int32_t* qzeros, const uint16_t* scales, int32_t K,

@@ -16,7 +16,24 @@ constexpr uint32_t NIB2 = 0x000F000Fu;
 // (written through to the device-coherent level), so a consumer in the same
 // launch on any XCD can poll the word itself until the tag shows it is this
 // launch's value (one word per lane and column: one-word-per-lane tiles only).
-enum : int { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_PAIRED = 3, EPI_LL = 4 };
+// EPI_QKV_PREP (the prompt GEMM only): the tile is one q, k or v head of the
+// fused projection; it gets the q/k RMSNorm + RoPE of qk_prep.h and goes to the
+// q rows and the KV cache (QkvPrepParams) instead of y0.
+enum : int { EPI_STORE = 0, EPI_RESIDUAL = 1, EPI_SWIGLU = 2, EPI_PAIRED = 3, EPI_LL = 4, EPI_QKV_PREP = 5 };
+
+// Destinations and norm/RoPE inputs of EPI_QKV_PREP (row m = b * T + t, position
+// p0 + t): q heads to q [B, Hq, T, 128], k and v heads to the caches
+// [B, Hkv, cap, 128] at that position.
+struct QkvPrepParams {
+  const uint16_t* qn;     // [128] q norm weight
+  const uint16_t* kn;     // [128] k norm weight
+  const uint16_t* rope;   // [>= p0 + T, 128] cos even / sin odd
+  uint16_t* q;
+  uint16_t* kc;
+  uint16_t* vc;
+  int T, Hq, Hkv, cap, p0, style;
+  float eps;
+};
 
 struct LinearParams {
   const uint16_t* x;

@@ -489,9 +489,16 @@ class Qwen3Model:
             w = layer.w
             if i > 0:
                 ops.rmsnorm(pf["x"], w.ln1, c.eps, out=pf["xn"])
-            ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
-            ops.prefill_qk_rope_kv(pf["qkv"], b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps, self.rope,
-                                   self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style, q_out=pf["q"])
+            if b * t >= ops.PROMPT_GEMM_ROWS:
+                # the projection's epilogue does the q/k norm, RoPE and cache write
+                ops.prefill_qkv_rope_kv(pf["xn"], w.qkv, b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps,
+                                        self.rope, self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style,
+                                        q_out=pf["q"])
+            else:
+                ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
+                ops.prefill_qk_rope_kv(pf["qkv"], b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps,
+                                       self.rope, self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style,
+                                       q_out=pf["q"])
             ops.prefill_attention(pf["q"], 0, c.n_kv_heads, self.k_cache[i], self.v_cache[i], out=pf["ctx"])
             ops.linear(pf["ctx"], w.o, residual=pf["x"], out=pf["x"])
             ops.rmsnorm(pf["x"], w.ln2, c.eps, out=pf["xn"])

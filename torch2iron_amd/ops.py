@@ -16,6 +16,7 @@ from torch2iron_amd.formats import GROUP_SIZE, W4A16Weight
 BF16 = torch.bfloat16
 
 ROPE_HALVES = 0
+PROMPT_GEMM_ROWS = 512   # rows from which the linear runs the LDS-tiled prompt GEMM (t2i_w4a16_linear)
 ROPE_INTERLEAVED = 1
 
 
@@ -507,6 +508,47 @@ def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_k
                                     q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap,
                                     _lib.stream_handle(qkv.device))
     _lib.check(rc, "t2i_prefill_qk_rope_kv")
+    return q_out
+
+
+def prefill_qkv_rope_kv(x: torch.Tensor, w_qkv: W4A16Weight, batch: int, p0: int, n_heads: int, n_kv_heads: int,
+                        q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float, rope: torch.Tensor,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
+                        q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """``prefill_qk_rope_kv(linear(x, w_qkv), ...)`` in one launch, with the same bits:
+    the prompt GEMM's epilogue normalises and rotates each q/k head and writes q
+    and the caches, and the projection is never stored.  ``x`` bf16 ``[B * T, K]``
+    with ``B * T >= 512`` (the prompt GEMM's rows); returns q bf16 ``[B, Hq, T, D]``."""
+    _check_dev("x", x, BF16)
+    _check_weight(w_qkv)
+    for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_dev(n, t, BF16)
+    d = q_norm.numel()
+    if k_norm.numel() != d:
+        raise ValueError("q_norm and k_norm must both hold head_dim values")
+    if batch < 1 or x.dim() != 2 or x.shape[0] % batch:
+        raise ValueError("x must be [B * T, K] with B = batch")
+    if x.shape[1] != w_qkv.K or w_qkv.N != (n_heads + 2 * n_kv_heads) * d:
+        raise ValueError("w_qkv must be [K = x.shape[1], (Hq + 2 Hkv) * D]")
+    t = x.shape[0] // batch
+    if (k_cache.dim() != 4 or k_cache.shape != v_cache.shape or tuple(k_cache.shape[:2]) != (batch, n_kv_heads)
+            or k_cache.shape[3] != d):
+        raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
+    ctx_cap = k_cache.shape[2]
+    if rope.shape[0] < p0 + t:
+        raise ValueError("rope table shorter than the prompt positions")
+    if q_out is None:
+        q_out = torch.empty(batch, n_heads, t, d, dtype=BF16, device=x.device)
+    _check_dev("q_out", q_out, BF16)
+    if q_out.numel() != batch * n_heads * t * d:
+        raise ValueError("q_out must be [B, Hq, T, D]")
+    lib = _lib.load()
+    rc = lib.t2i_prefill_qkv_rope_kv(x.data_ptr(), batch, t, p0, w_qkv.qweight.data_ptr(), w_qkv.qzeros.data_ptr(),
+                                     w_qkv.scales.data_ptr(), w_qkv.K, w_qkv.group_size, n_heads, n_kv_heads, d,
+                                     q_norm.data_ptr(), k_norm.data_ptr(), float(eps), rope.data_ptr(),
+                                     int(rope_style), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                     ctx_cap, _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_prefill_qkv_rope_kv")
     return q_out
 
 
