@@ -392,7 +392,25 @@ def test_wrappers_reject_undersized_outputs(gpu):
         ops.lm_head_argmax(x, emb, torch.zeros(2, dtype=torch.int64, device=gpu))
     with pytest.raises(ValueError):
         ops.lm_head_argmax(x.view(-1), emb, torch.zeros(3, dtype=torch.int64, device=gpu))
-    wp = W4A16Weight.from_numpy(*interleave_gate_up(random_tensors(256, 64, 1), random_tensors(256, 64, 2)),
+    with pytest.raises(ValueError):
+        ops.rmsnorm_lm_head_argmax(x, w, 1e-6, emb, torch.zeros(2, dtype=torch.int64, device=gpu))
+    with pytest.raises(ValueError):
+        ops.rmsnorm_lm_head_argmax(x, w[:128], 1e-6, emb, torch.zeros(3, dtype=torch.int64, device=gpu))
+    with pytest.raises(ValueError):
+        ops.rmsnorm_lm_head_argmax(x, w, 1e-6, emb, torch.zeros(3, dtype=torch.int64, device=gpu),
+                                   logits=torch.zeros(3, 63, device=gpu))
+    # the prompt preps: a rope table narrower than head_dim
+    t, hp = 256, 2   # B * T = 512 rows, the prompt GEMM's minimum
+    kcp = torch.zeros(b, hkv, t, d, dtype=BF16, device=gpu)
+    narrow = gm.rope_table(d, t, 1e6, gpu)[:, : d // 2].contiguous()   # every position, half the width
+    with pytest.raises(ValueError):
+        ops.prefill_qk_rope_kv(torch.zeros(b * t, (hp + 2 * hkv) * d, dtype=BF16, device=gpu), b, 0, hp, hkv,
+                               ones, ones, 1e-6, narrow, kcp, kcp.clone())
+    wq = W4A16Weight.from_numpy(*random_tensors(256, (hp + 2 * hkv) * d, 3), device=gpu)
+    with pytest.raises(ValueError):
+        ops.prefill_qkv_rope_kv(torch.zeros(b * t, 256, dtype=BF16, device=gpu), wq, b, 0, hp, hkv, ones, ones,
+                                1e-6, narrow, kcp, kcp.clone())
+    wp =W4A16Weight.from_numpy(*interleave_gate_up(random_tensors(256, 64, 1), random_tensors(256, 64, 2)),
                                 device=gpu)
     with pytest.raises(ValueError):
         ops.gate_up(x, wp, swiglu=False, out_up=small)

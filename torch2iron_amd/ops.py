@@ -495,8 +495,8 @@ def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_k
             or k_cache.shape[3] != d):
         raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
     ctx_cap = k_cache.shape[2]
-    if rope.shape[0] < p0 + t:
-        raise ValueError("rope table shorter than the prompt positions")
+    if rope.dim() != 2 or rope.shape[0] < p0 + t or rope.shape[1] != d:
+        raise ValueError("rope must be [>= p0 + T positions, D]")
     if q_out is None:
         q_out = torch.empty(batch, n_heads, t, d, dtype=BF16, device=qkv.device)
     _check_dev("q_out", q_out, BF16)
@@ -535,8 +535,8 @@ def prefill_qkv_rope_kv(x: torch.Tensor, w_qkv: W4A16Weight, batch: int, p0: int
             or k_cache.shape[3] != d):
         raise ValueError("caches must be [B, Hkv, ctx_cap, D]")
     ctx_cap = k_cache.shape[2]
-    if rope.shape[0] < p0 + t:
-        raise ValueError("rope table shorter than the prompt positions")
+    if rope.dim() != 2 or rope.shape[0] < p0 + t or rope.shape[1] != d:
+        raise ValueError("rope must be [>= p0 + T positions, D]")
     if q_out is None:
         q_out = torch.empty(batch, n_heads, t, d, dtype=BF16, device=x.device)
     _check_dev("q_out", q_out, BF16)
