@@ -257,3 +257,69 @@ def test_rmsnorm_gate_up_fused(gpu, m, k, inter):
     h_chain = (torch.nn.functional.silu(gb).to(torch.bfloat16).float() * ub).to(torch.bfloat16).float()
     assert (h - h_chain).abs().max() <= 2.0 ** -7 * h_chain.abs().max()
     assert (h == h_chain).float().mean() > 0.999
+
+
+def _random_cases(n_cases: int, seed: int):
+    """Seeded random shapes for every linear form: M from 1 to 96 (prompt rows from 512
+    for the GEMM form), K any multiple of 128 up to 4096, N any multiple of 16 (of 128 for
+    the GEMM), within a size each oracle call finishes in
+    about a second.  The paired layout interleaves gate and up in 32-column blocks, so a
+    paired N is a multiple of 64."""
+    rs = np.random.RandomState(seed)
+    forms = ["plain", "residual", "norm", "paired", "prompt"]
+    cases = []
+    while len(cases) < n_cases:
+        form = forms[len(cases) % len(forms)]
+        k = 128 * int(rs.randint(1, 33))
+        if form == "prompt":
+            m, n = int(rs.randint(512, 901)), 128 * int(rs.randint(1, 17))
+        else:
+            m = int(rs.randint(1, 97))
+            n = 64 * int(rs.randint(1, 49)) if form == "paired" else 16 * int(rs.randint(1, 257))
+        if k * n <= 6 << 20 and m * k * n <= 1536 << 20:
+            cases.append((form, m, k, n))
+    return cases
+
+
+RANDOM_CASES = _random_cases(25, seed=2026)
+
+
+@pytest.mark.parametrize("form,m,k,n", RANDOM_CASES, ids=[f"{f}-M{m}-K{k}-N{n}" for f, m, k, n in RANDOM_CASES])
+def test_random_shapes_match_oracle(gpu, form, m, k, n):
+    """Shapes off the model's list, each form against the fp64 oracle at the bars above
+    (paired: both outputs; residual: two roundings; fused norm: the bf16 RMSNorm chain
+    then the linear bar)."""
+    seed = 3000 + m + 7 * k + 13 * n
+    if form == "paired":
+        gate, up = ow.synthetic_tensors(k, n // 2, seed=seed), ow.synthetic_tensors(k, n // 2, seed=seed + 1)
+        x = torch.randn(m, k, generator=torch.Generator().manual_seed(seed + 2)).to(torch.bfloat16)
+        w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
+        g, u = ops.gate_up(x.to(gpu), w, swiglu=False)
+        check_linear(g, ow.linear(x.float().numpy(), *gate, accumulate="fp64"))
+        check_linear(u, ow.linear(x.float().numpy(), *up, accumulate="fp64"))
+        return
+    qw, qz, sc, x = _inputs(m, k, n, seed=seed)
+    w = W4A16Weight.from_numpy(qw, qz, sc, device=gpu)
+    if form == "norm":
+        from oracle import qwen3 as oq
+        x = (x.float() * 3.0).to(torch.bfloat16)
+        gam = (torch.rand(k, generator=torch.Generator().manual_seed(seed + 3)) * 0.2 + 0.9).to(torch.bfloat16)
+        y = ops.rmsnorm_linear(x.to(gpu), gam.to(gpu), 1e-6, w)
+        xn = oq.rmsnorm(x.float(), gam.float(), 1e-6, oq._Round("bf16")).numpy()
+        ref = ow.linear(xn, qw, qz, sc, accumulate="fp64")
+        assert np.abs(y.float().cpu().numpy() - ref).max() / np.abs(ref).max() <= 1e-2
+        check_rounding_of_activations(y, ops.linear(ops.rmsnorm(x.to(gpu), gam.to(gpu), 1e-6), w), xn,
+                                      ow.dequantize(qw, qz, sc))
+        return
+    lin = ow.linear(x.float().numpy(), qw, qz, sc, accumulate="fp64")
+    if form == "residual":
+        res = torch.randn(m, n, generator=torch.Generator().manual_seed(seed + 4)).to(torch.bfloat16)
+        out = res.clone().to(gpu)
+        y = ops.linear(x.to(gpu), w, residual=out, out=out)
+        ref = lin + res.float().numpy()
+        err = np.abs(y.float().cpu().numpy() - ref)
+        assert (err <= 2.0 ** -8 * (np.abs(lin) + np.abs(ref)) * 1.01 + 1e-4 * np.abs(ref).max()).all()
+        return
+    y = ops.linear(x.to(gpu), w)
+    check_linear(y, lin)
+    assert torch.equal(y, ops.linear(x.to(gpu), w)), "repeat call differs"
