@@ -125,6 +125,46 @@ def test_decode_attention_matches_oracle(gpu, b, hq, hkv, ctx_cap, positions, st
     assert torch.equal(kd.float().permute(0, 2, 1, 3)[mask], kref.permute(0, 2, 1, 3)[mask])
 
 
+def _random_attention_cases(n_cases: int, seed: int):
+    """Seeded random decode-attention shapes: 1-40 sequences, 1/2/4/8 q heads per kv
+    head over 1-8 kv heads, a cache of 1-2500 slots and a random position per sequence
+    (the first and last slot among them), both RoPE styles."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    for i in range(n_cases):
+        b = int(rs.randint(1, 41))
+        hkv = int(rs.choice([1, 2, 4, 8]))
+        hq = hkv * int(rs.choice([1, 2, 4, 8]))
+        cap = int(rs.randint(1, 2501))
+        pos = [int(p) for p in rs.randint(0, cap, size=b)]
+        pos[0] = cap - 1
+        pos[-1] = 0 if b > 1 else pos[-1]
+        cases.append((b, hq, hkv, cap, pos, "halves" if i % 2 else "interleaved"))
+    return cases
+
+
+RANDOM_ATTENTION = _random_attention_cases(16, seed=77)
+
+
+@pytest.mark.parametrize("b,hq,hkv,ctx_cap,positions,style", RANDOM_ATTENTION,
+                         ids=[f"B{c[0]}-Hq{c[1]}-Hkv{c[2]}-cap{c[3]}-{c[5]}" for c in RANDOM_ATTENTION])
+def test_decode_attention_random_shapes(gpu, b, hq, hkv, ctx_cap, positions, style):
+    """The bars of test_decode_attention_matches_oracle at seeded random shapes."""
+    out, ref, kd, vd, kref, vref, pos = _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed=ctx_cap + b)
+    err = (out - ref).abs().max() / ref.abs().max()
+    assert err <= 1e-2, f"max relative error {err:.3e}"
+    assert ((out - ref).abs() <= 2.0 ** -8 * ref.abs() + 2e-3 * ref.abs().max()).all()
+    for i in range(b):
+        p = int(pos[i])
+        fk, wk = ulp_mismatch_fraction(kd[i, :, p], kref[i, :, p])
+        fv, wv = ulp_mismatch_fraction(vd[i, :, p], vref[i, :, p])
+        assert wk <= 1 and fk < 0.02 and fv == 0.0
+    mask = torch.ones(kd.shape[0], kd.shape[2], dtype=torch.bool)
+    for i in range(b):
+        mask[i, int(pos[i])] = False
+    assert torch.equal(kd.float().permute(0, 2, 1, 3)[mask], kref.permute(0, 2, 1, 3)[mask])
+
+
 @pytest.mark.parametrize("b", [2, 16])
 def test_decode_attention_out_of_range_position_is_inert(gpu, b):
     d, hq, hkv, cap = 128, 16, 8, 128
