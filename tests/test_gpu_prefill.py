@@ -10,6 +10,7 @@ oracle's within the bf16 rounding of a head vector.
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -99,6 +100,41 @@ def test_prefill_prep_and_attention_match_oracle(gpu, b, t, p0, hq, hkv, cap, st
     assert err.max() / scale <= 1e-2, f"max relative error {err.max() / scale:.3e}"
     # each softmax weight is rounded to bf16 (relative 2^-9) before P . V, and the
     # output to bf16 (2^-9): |err| <= 2^-9 (sum_j p_j |v_j| + |ref|), bound taken at 2^-8
+    assert (err <= 2.0 ** -8 * (mag + ref.abs()) + 1e-6).all(), (err / (mag + ref.abs())).max()
+
+
+def _random_prefill_cases(n_cases: int, seed: int):
+    """Seeded random prompt chunks: 1-4 sequences of 1-300 rows at a start position of
+    0-300 (earlier slots cached), 1/2/4/8 q heads per kv head, a cache with up to 100
+    slots past the chunk, both RoPE styles."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    for i in range(n_cases):
+        hkv = int(rs.choice([1, 2, 4, 8]))
+        hq = hkv * int(rs.choice([1, 2, 4])) if hkv == 8 else hkv * int(rs.choice([1, 2, 4, 8]))
+        b, t = int(rs.randint(1, 5)), int(rs.randint(1, 301))
+        p0 = 0 if i % 3 == 0 else int(rs.randint(0, 301))
+        cases.append((b, t, p0, hq, hkv, p0 + t + int(rs.randint(0, 101)), "halves" if i % 2 else "interleaved"))
+    return cases
+
+
+RANDOM_PREFILL = _random_prefill_cases(12, seed=5)
+
+
+@pytest.mark.parametrize("b,t,p0,hq,hkv,cap,style", RANDOM_PREFILL,
+                         ids=[f"B{c[0]}-T{c[1]}-p{c[2]}-Hq{c[3]}-Hkv{c[4]}-cap{c[5]}-{c[6]}" for c in RANDOM_PREFILL])
+def test_prefill_random_shapes(gpu, b, t, p0, hq, hkv, cap, style):
+    """The bars of test_prefill_prep_and_attention_match_oracle at seeded random shapes."""
+    qd, qb, kd, vd, kref, vref, out, ref, mag = _case(gpu, b, t, p0, hq, hkv, cap, style, seed=7 * b + t + p0)
+    fq, wq = ulp_diff(qd.float(), qb)
+    assert wq <= 1 and fq < 0.01, (fq, wq)
+    fk, wk = ulp_diff(kd[:, :, p0:p0 + t].float(), kref[:, :, p0:p0 + t])
+    assert wk <= 1 and fk < 0.01, (fk, wk)
+    assert torch.equal(vd[:, :, p0:p0 + t].float(), vref[:, :, p0:p0 + t])
+    assert torch.equal(kd[:, :, :p0].float(), kref[:, :, :p0])
+    assert torch.equal(kd[:, :, p0 + t:].float(), kref[:, :, p0 + t:])
+    err = (out - ref).abs()
+    assert err.max() / ref.abs().max() <= 1e-2
     assert (err <= 2.0 ** -8 * (mag + ref.abs()) + 1e-6).all(), (err / (mag + ref.abs())).max()
 
 
