@@ -179,9 +179,22 @@ def test_decode_attention_out_of_range_position_is_inert(gpu, b):
     assert torch.equal(kc, kc0)
 
 
+def _random_head_cases(n_cases: int, seed: int, pow2: bool):
+    """Seeded random lm_head shapes: 1-40 rows, any vocabulary a multiple of 16, K a
+    multiple of 64 up to 4096 (a power of two for the fused norm), V * K up to 16M."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    while len(cases) < n_cases:
+        m, v = int(rs.randint(1, 41)), 16 * int(rs.randint(1, 4001))
+        k = 64 << int(rs.randint(0, 7)) if pow2 else 64 * int(rs.randint(1, 65))
+        if v * k <= 16 << 20:
+            cases.append((m, v, k))
+    return cases
+
+
 @pytest.mark.parametrize("m,v,k", [(16, 151936, 1024), (1, 4096, 1024), (5, 1040, 1024), (20, 2048, 1024),
                                    (3, 1040, 64), (7, 528, 128), (16, 2064, 192), (2, 4096, 2048),
-                                   (3, 1040, 4096)])
+                                   (3, 1040, 4096)] + _random_head_cases(8, seed=91, pow2=False))
 def test_lm_head_argmax(gpu, m, v, k):
     """Slices of 64 k: one (peeled), two, an odd count after the loop, K = 2048 (the
     staged tile spans two load batches and needs more than 64 KB of LDS) and the
@@ -203,7 +216,7 @@ def test_lm_head_argmax(gpu, m, v, k):
 
 
 @pytest.mark.parametrize("m,v,k", [(16, 151936, 1024), (1, 4096, 1024), (5, 1040, 64), (20, 2064, 2048),
-                                   (3, 1040, 4096), (16, 528, 128)])
+                                   (3, 1040, 4096), (16, 528, 128)] + _random_head_cases(6, seed=92, pow2=True))
 def test_rmsnorm_lm_head_matches_two_launches(gpu, m, v, k):
     """The final norm inside the lm_head gives the bits of t2i_rmsnorm followed by
     t2i_lm_head_argmax: logits and keys, for one and two 16-row slices, K from 64 to
