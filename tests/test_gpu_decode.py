@@ -239,47 +239,85 @@ def test_rmsnorm_lm_head_matches_two_launches(gpu, m, v, k):
     assert torch.equal(keys2, keys_ref)
 
 
-def test_decode_layer_config3(gpu):
-    """One Qwen3-0.6B decode layer, batch 8, 1024 cached tokens, write at 1024."""
-    cfg = gm.Qwen3Config(n_layers=1, vocab=256)
+LAYER_CASES = [
+    ("0.6b", 8, 1088, [1024] * 8),                                   # config 3
+    ("0.6b", 16, 640, [(41 * i) % 640 for i in range(15)] + [639]),  # the decode bench's batch, ragged
+    ("0.6b", 4, 2100, [2099, 0, 1000, 1500]),                         # long context, both cache ends
+    ("1.7b", 8, 1088, [1024] * 8),                                   # config 3 at Qwen3-1.7B shapes
+    ("1.7b", 8, 520, [512, 3, 256, 511, 100, 7, 300, 519]),           # short contexts: outputs up to ~4e4
+]
+
+
+@pytest.mark.parametrize("dims,b,cap,positions", LAYER_CASES,
+                         ids=[f"{c[0]}-B{c[1]}-cap{c[2]}" for c in LAYER_CASES])
+def test_decode_layer_config3(gpu, dims, b, cap, positions):
+    """One decode layer against the oracle: config 3 (Qwen3-0.6B, batch 8, 1024
+    cached tokens, write at 1024), ragged positions, a long context and the
+    Qwen3-1.7B shapes.
+
+    The GPU rounds to bf16 where a bf16 runtime does, except that the fused RMSNorm
+    scales each row's product sums instead of each activation.  So the layer is held
+    to the fp32 truth twice:
+      * composed from the standalone kernels (RMSNorm, linear, attention, gate/up,
+        linear), which round at the oracle's bf16 points: output and written k row no
+        farther from fp32 than the oracle's own bf16 chain, in the largest and in the
+        RMS deviation (within 25 %);
+      * as the model runs it (Qwen3DecodeLayer, fused norms): within 2e-2 max relative
+        error of fp32, and -- at config 3 -- inside the same bands.  Elsewhere the
+        fused rounding point can land on either side of the chain's (at outputs of
+        magnitude ~4e4 both are about one bf16 ulp, 256, from fp32), so the bands are
+        not applied to it there.
+    (A whole layer of bf16 steps on a residual of magnitude ~300 and more is not held
+    to the 1e-2 of one linear.)"""
+    base = gm.QWEN3_0_6B if dims == "0.6b" else gm.QWEN3_1_7B
+    cfg = gm.Qwen3Config(**{**base.__dict__, "n_layers": 1, "vocab": 256})
     t = gm.random_qwen3_tensors(cfg, seed=11)
-    b, cap = 8, 1088
     g = torch.Generator().manual_seed(12)
     x = torch.randn(b, cfg.hidden, generator=g).to(BF16)
     kc = torch.randn(b, cfg.n_kv_heads, cap, cfg.head_dim, generator=g).to(BF16)
     vc = torch.randn(b, cfg.n_kv_heads, cap, cfg.head_dim, generator=g).to(BF16)
-    pos = torch.full((b,), 1024, dtype=torch.int32)
-    # oracle, bf16 rounding points
+    pos = torch.tensor(positions, dtype=torch.int32)
+    rows, slots = torch.arange(b), pos.long()
+    # oracle, bf16 rounding points and fp32
     layer = oq.DenseLayer(t, "model.layers.0", oracle_cfg(cfg))
+    ang = oq.rope_angles(cfg.head_dim, cap, cfg.rope_theta)
     kref, vref = kc.float().clone(), vc.float().clone()
-    ref = layer.decode(x.float(), kref, vref, pos.long(), oq.rope_angles(cfg.head_dim, cap, cfg.rope_theta),
-                       oq._Round("bf16"))
-    # GPU
+    ref = layer.decode(x.float(), kref, vref, slots, ang, oq._Round("bf16"))
+    kf, vf = kc.float().clone(), vc.float().clone()
+    ref32 = layer.decode(x.float(), kf, vf, slots, ang, oq._Round("fp32"))
+    # GPU: the model's layer, and the same layer from the standalone kernels
     rope = gm.rope_table(cfg.head_dim, cap, cfg.rope_theta, gpu)
-    dl = gm.Qwen3DecodeLayer(gm.Qwen3LayerWeights(t, 0, cfg, gpu), cfg, rope)
+    w = gm.Qwen3LayerWeights(t, 0, cfg, gpu)
+    dl = gm.Qwen3DecodeLayer(w, cfg, rope)
     buf = gm.DecodeBuffers(cfg, b, gpu)
     buf.x.copy_(x.to(gpu))
     kd, vd = kc.to(gpu), vc.to(gpu)
     dl(buf, pos.to(gpu), kd, vd)
     out = buf.x.float().cpu()
-    # The GPU rounds to bf16 where a bf16 runtime does, but not at every point of the
-    # oracle's bf16 chain (the fused RMSNorm scales the product's sums, not each
-    # activation), so it is held to the fp32 truth: no farther from it than the
-    # oracle's own bf16 chain, in the largest and in the RMS deviation, for the
-    # layer output and for the k row written to the cache.  (A whole layer of bf16
-    # steps on a residual of magnitude ~300 is not held to the 1e-2 of one linear.)
-    kf, vf = kc.float().clone(), vc.float().clone()
-    ref32 = layer.decode(x.float(), kf, vf, pos.long(), oq.rope_angles(cfg.head_dim, cap, cfg.rope_theta),
-                         oq._Round("fp32"))
+    xg, ku, vu = x.to(gpu), kc.to(gpu), vc.to(gpu)
+    qkv = ops.linear(ops.rmsnorm(xg, w.ln1, cfg.eps), w.qkv)
+    ctx = ops.decode_attention(qkv, pos.to(gpu), cfg.n_heads, cfg.n_kv_heads, w.q_norm, w.k_norm, cfg.eps, rope,
+                               ku, vu)
+    h = ops.linear(ctx, w.o, residual=xg)
+    outu = ops.linear(ops.gate_up(ops.rmsnorm(h, w.ln2, cfg.eps), w.gate_up, swiglu=True), w.down, residual=h)
     rms = lambda a: a.pow(2).mean().sqrt().item()
-    for name, got, r16, r32 in (("output", out, ref, ref32),
-                                ("k row", kd[:, :, 1024].float().cpu(), kref[:, :, 1024], kf[:, :, 1024])):
+    banded = [("standalone kernels: output", outu.float().cpu(), ref, ref32),
+              ("standalone kernels: k row", ku.cpu()[rows, :, slots].float(), kref[rows, :, slots], kf[rows, :, slots])]
+    if positions == [1024] * 8 and dims == "0.6b":
+        banded += [("model layer: output", out, ref, ref32),
+                   ("model layer: k row", kd.cpu()[rows, :, slots].float(), kref[rows, :, slots], kf[rows, :, slots])]
+    failures = []
+    for name, got, r16, r32 in banded:
         band_max, band_rms = (r16 - r32).abs().max().item(), rms(r16 - r32)
         dev_max, dev_rms = (got - r32).abs().max().item(), rms(got - r32)
-        assert dev_max <= 1.25 * band_max, f"{name}: max deviation {dev_max:.4f} vs bf16 chain {band_max:.4f}"
-        assert dev_rms <= 1.25 * band_rms, f"{name}: RMS deviation {dev_rms:.5f} vs bf16 chain {band_rms:.5f}"
+        if dev_max > 1.25 * band_max:
+            failures.append(f"{name}: max deviation {dev_max:.4f} vs bf16 chain {band_max:.4f}")
+        if dev_rms > 1.25 * band_rms:
+            failures.append(f"{name}: RMS deviation {dev_rms:.5f} vs bf16 chain {band_rms:.5f}")
     err = (out - ref32).abs().max() / ref32.abs().max()
-    assert err <= 2e-2, f"decode layer max relative error {err:.3e} against fp32"
+    if err > 2e-2:
+        failures.append(f"model layer: max relative error {err:.3e} against fp32")
+    assert not failures, "; ".join(failures)
 
 
 @pytest.mark.parametrize("weights", ["centered", "uniform"])
