@@ -142,12 +142,30 @@ def _oracle_cfg(cfg):
     return oq.Qwen3Config(**{k: getattr(cfg, k) for k in oq.Qwen3Config.__dataclass_fields__})
 
 
+def _random_projection_cases(n_cases: int, seed: int):
+    """Seeded random fused-projection shapes: 512-1500 prompt rows over 1-8
+    sequences, 1/2/4/8 q heads per kv head over 1-8 kv heads, K any multiple of 128 up
+    to 3072, a start position of 0-200 and up to 64 slots past the prompt."""
+    rs = np.random.RandomState(seed)
+    cases = []
+    while len(cases) < n_cases:
+        b = int(rs.randint(1, 9))
+        t = int(rs.randint(-(-512 // b), 1500 // b + 1))
+        hkv = int(rs.choice([1, 2, 4, 8]))
+        hq = hkv * int(rs.choice([1, 2, 4, 8]))
+        k = 128 * int(rs.randint(1, 25))
+        p0 = int(rs.randint(0, 201))
+        if 512 <= b * t <= 1500 and hq + 2 * hkv <= 40:
+            cases.append((b, t, p0, hq, hkv, k, p0 + t + int(rs.randint(0, 65))))
+    return cases
+
+
 @pytest.mark.parametrize("style", [0, 1])
 @pytest.mark.parametrize("b,t,p0,hq,hkv,k,cap", [
     (16, 512, 0, 16, 8, 1024, 640),     # the Qwen3-0.6B prompt pass
     (3, 200, 37, 16, 4, 2048, 300),     # 600 rows: a ragged last row tile; 4 q heads a kv head; p0 > 0
     (1, 512, 0, 8, 8, 1024, 512),       # one q head a kv head, the cache exactly full
-])
+] + _random_projection_cases(5, seed=8))
 def test_fused_prompt_projection_matches_two_launches(gpu, b, t, p0, hq, hkv, k, cap, style):
     """The prompt GEMM with the q/k norm + RoPE + cache write in its epilogue gives
     the bits of the projection followed by t2i_prefill_qk_rope_kv: q rows and both
