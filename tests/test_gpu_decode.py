@@ -320,9 +320,11 @@ def test_decode_layer_config3(gpu, dims, b, cap, positions):
     assert not failures, "; ".join(failures)
 
 
+@pytest.mark.parametrize("b", [8, 1, 24])
 @pytest.mark.parametrize("weights", ["centered", "uniform"])
-def test_greedy_decode_small_model_matches_oracle(gpu, weights):
-    """4 layers, batch 8: 32 greedy steps on the GPU (graph replays) vs the oracle.
+def test_greedy_decode_small_model_matches_oracle(gpu, weights, b):
+    """4 layers, batch 8 (and 1, 24: other linear plans and attention grids): 32
+    greedy steps on the GPU (graph replays) vs the oracle.
 
     The reference runtime computes in fp32 by default, so the tokens are held to
     the fp32 oracle.  The GPU computes in bf16, as the reference does in bf16
@@ -332,7 +334,7 @@ def test_greedy_decode_small_model_matches_oracle(gpu, weights):
     divergence from the bf16-mode oracle must be such a near-tie too."""
     cfg = gm.Qwen3Config(n_layers=4, vocab=8192)
     t = gm.random_qwen3_tensors(cfg, seed=21, weights=weights)
-    b, plen, new = 8, 24, 32
+    plen, new = 24, 32
     prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(22))
     gpu_model = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu)
     got = gpu_model.generate(prompt, new)
