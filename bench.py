@@ -74,6 +74,9 @@ def parse():
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--streams", default="1,2", help="micro-batch stream counts to measure for batch decode")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="only the decode attention at the batch-decode shape, HBM-cold (for its kernel trace and "
+                         "counters; no headline)")
     ap.add_argument("--eager", action="store_true", help="sweep launches without graphs (for counter collection)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (the reference kernel for HBM byte counters)")
@@ -429,6 +432,68 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
 # CPU baselines: the oracle on the host cores (bounded samples)
 # ---------------------------------------------------------------------------
 
+def bench_attention(dev, steps: int, warmup: int, eager: bool, calibrate: bool) -> dict:
+    """Decode attention at the batch-decode shape (16 sequences, 16 q / 8 kv heads, 577
+    cached slots each: position 576 of a 640-slot cache), HBM-cold: 28 cache pairs, one
+    per layer, cycled (1.2 GB, past the 256 MB MALL).  A step is 28 calls, one graph
+    replay (eager launches with ``eager``, for counter runs); event-timed on the stream
+    the calls launch on."""
+    import torch
+    from torch2iron_amd import ops
+    from torch2iron_amd import model as gm
+    b, hq, hkv, d, cap, pos, layers = 16, 16, 8, 128, 640, 576, 28
+    g = torch.Generator(device=dev).manual_seed(6)
+    kcs = [torch.randn(b, hkv, cap, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    vcs = [torch.randn(b, hkv, cap, d, generator=g, device=dev).to(torch.bfloat16) for _ in range(layers)]
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, generator=g, device=dev).to(torch.bfloat16)
+    qn = (torch.rand(d, generator=g, device=dev) * 0.2 + 0.9).to(torch.bfloat16)
+    kn = (torch.rand(d, generator=g, device=dev) * 0.2 + 0.9).to(torch.bfloat16)
+    rope = gm.rope_table(d, cap, 1e6, dev)
+    positions = torch.full((b,), pos, dtype=torch.int32, device=dev)
+    out = torch.empty(b, hq * d, dtype=torch.bfloat16, device=dev)
+    ws = ops.Workspace()
+
+    def step():
+        for i in range(layers):
+            ops.decode_attention(qkv, positions, hq, hkv, qn, kn, 1e-6, rope, kcs[i], vcs[i], out=out, workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    run = step
+    if not eager:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (steps * layers)
+    # algorithmic bytes of a call: the K/V rows of the 577 slots, the qkv rows read, the
+    # new k/v rows written, the context written
+    kv = b * hkv * (pos + 1) * d * 2 * 2
+    nbytes = kv + qkv.numel() * 2 + b * hkv * d * 2 * 2 + out.numel() * 2
+    if calibrate:
+        src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+    res = {"workload": f"decode attention, batch {b}, {hq} q / {hkv} kv heads, head_dim {d}, {pos + 1} cached "
+                       f"slots ({cap}-slot cache), {layers} cache pairs cycled (HBM-cold), "
+                       + ("eager launches" if eager else "graph replays"),
+           "us_per_call": round(us, 3), "algorithmic_bytes_per_call": nbytes,
+           "TBps": round(nbytes / us / 1e6, 4), "frac_of_8TBps": round(nbytes / us / 1e6 / 8.0, 4)}
+    log(f"decode attention: {us:.2f} us per call, {nbytes / us / 1e6:.3f} TB/s of {nbytes / 1e6:.1f} MB algorithmic")
+    return res
+
+
 def cpu_info() -> dict:
     import torch
     model = "unknown"
@@ -550,6 +615,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.attention_only:
+        att = bench_attention(dev, args.steps, args.warmup, args.eager, args.calibrate_copy)
+        print(json.dumps({"metric": METRIC, "value": None, "unit": "TB/s", "n_gpus": 1, "note": "attention only",
+                          "decode_attention": att}), flush=True)
+        return
     if args.decode_only:
         decode, _, _ = bench_decode(dev, args.steps, args.warmup, args.prompt, args.new_tokens, args.batch,
                                     [int(v) for v in args.streams.split(",")], teacher_forced_leg=False)
