@@ -77,6 +77,9 @@ def parse():
     ap.add_argument("--attention-only", action="store_true",
                     help="only the decode attention at the batch-decode shape, HBM-cold (for its kernel trace and "
                          "counters; no headline)")
+    ap.add_argument("--prompt-gemm-only", action="store_true",
+                    help="only the prompt GEMM at the prompt pass's shapes (16 x 512 rows; for its kernel trace and "
+                         "MFMA counters; no headline)")
     ap.add_argument("--eager", action="store_true", help="sweep launches without graphs (for counter collection)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="also run a 256 MiB device copy (the reference kernel for HBM byte counters)")
@@ -494,6 +497,61 @@ def bench_attention(dev, steps: int, warmup: int, eager: bool, calibrate: bool) 
     return res
 
 
+def bench_prompt_gemm(dev, steps: int, warmup: int, eager: bool) -> dict:
+    """The prompt pass's four W4A16 GEMMs (Qwen3-0.6B, 16 x 512 = 8192 rows) with their
+    epilogues: qkv, o_proj + residual, gate_up + SwiGLU, down + residual.  A step runs
+    each 8 times (one graph replay; eager launches with ``eager``, for counter runs);
+    the weights stay MALL-warm, as the GEMMs are bound by their k-loops, not by bytes."""
+    import torch
+    from torch2iron_amd import ops
+    from torch2iron_amd.formats import random_weight_on_device
+    m, reps = 8192, 8
+    g = torch.Generator(device=dev).manual_seed(9)
+    res = {}
+    for name, k, n in (("qkv", 1024, 4096), ("o_proj", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)):
+        w = random_weight_on_device(k, n, g, dev)
+        x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        if name == "gate_up":
+            y = torch.empty(m, n // 2, dtype=torch.bfloat16, device=dev)
+            call = lambda: ops.gate_up(x, w, swiglu=True, out=y)
+        elif name == "qkv":
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            call = lambda: ops.linear(x, w, out=y)
+        else:
+            r = torch.randn(m, n, generator=g, device=dev).to(torch.bfloat16)
+            y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
+            call = lambda: ops.linear(x, w, residual=r, out=y)
+        call()
+        torch.cuda.synchronize()
+
+        def step():
+            for _ in range(reps):
+                call()
+
+        run = step
+        if not eager:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            run = graph.replay
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (steps * reps)
+        flops = 2 * m * k * n
+        res[name] = {"M": m, "K": k, "N": n, "us_per_launch": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
+                     "frac_of_2_5PFLOPs": round(flops / us / 1e6 / 2500.0, 4)}
+        log(f"prompt GEMM {name} M={m} K={k} N={n}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s")
+        del w, x, y
+    return res
+
+
 def cpu_info() -> dict:
     import torch
     model = "unknown"
@@ -615,6 +673,11 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
 
+    if args.prompt_gemm_only:
+        gemm = bench_prompt_gemm(dev, args.steps, args.warmup, args.eager)
+        print(json.dumps({"metric": METRIC, "value": None, "unit": "TB/s", "n_gpus": 1, "note": "prompt GEMM only",
+                          "prompt_gemm": gemm}), flush=True)
+        return
     if args.attention_only:
         att = bench_attention(dev, args.steps, args.warmup, args.eager, args.calibrate_copy)
         print(json.dumps({"metric": METRIC, "value": None, "unit": "TB/s", "n_gpus": 1, "note": "attention only",
