@@ -342,7 +342,45 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                            "TBps": round(layer_bytes / (layer_us * 1e-6) / 1e12, 4),
                            "frac_of_8TBps": round(layer_bytes / (layer_us * 1e-6) / 8e12, 4)}
     log(f"decode layer (B=8, ctx 1024): {layer_us:.1f} us, {out['decode_layer']['TBps']} TB/s")
-    del g, buf, layers3, kc, vc
+    # each of the layer's five launches on its own: a graph of that launch for all 12
+    # layers (HBM-cold as above), event-timed, outside any profiler
+    from torch2iron_amd import ops
+
+    def layer_ops(lay, kc, vc):
+        c, lw = cfg, lay.w
+        return [
+            ("rmsnorm_qkv", lambda: ops.rmsnorm_linear(buf.x, lw.ln1, c.eps, lw.qkv, out=buf.qkv)),
+            ("attention", lambda: ops.decode_attention(buf.qkv, pos, c.n_heads, c.n_kv_heads, lw.q_norm, lw.k_norm,
+                                                       c.eps, lay.rope, kc, vc, rope_style=lay.rope_style,
+                                                       out=buf.ctx, workspace=buf.workspace)),
+            ("o_proj_residual", lambda: ops.linear(buf.ctx, lw.o, residual=buf.x, out=buf.x)),
+            ("rmsnorm_gate_up_swiglu", lambda: ops.rmsnorm_gate_up(buf.x, lw.ln2, c.eps, lw.gate_up, swiglu=True,
+                                                                   out=buf.hmlp)),
+            ("down_residual", lambda: ops.linear(buf.hmlp, lw.down, residual=buf.x, out=buf.x)),
+        ]
+
+    calls = [layer_ops(lay, kc, vc) for lay, kc, vc in layers3]
+    per_op = {}
+    for j, (name, _) in enumerate(calls[0]):
+        gop = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gop):
+            for lc in calls:
+                lc[j][1]()
+        for _ in range(warmup):
+            gop.replay()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            gop.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        per_op[name] = round(e0.elapsed_time(e1) * 1e3 / (reps * n3), 2)
+        del gop
+    out["decode_layer"]["per_op_us"] = per_op
+    out["decode_layer"]["per_op_sum_us"] = round(sum(per_op.values()), 2)
+    log("decode layer, each launch alone (us): " + ", ".join(f"{k} {v}" for k, v in per_op.items()))
+    buf.x.copy_(x0)
+    del g, buf, layers3, kc, vc, calls
     torch.cuda.empty_cache()
 
     # ---- config 4: full model, batch 16, prompt 512, 128 new tokens ----
