@@ -44,7 +44,6 @@ GEMV_06B = [("up_proj", 1024, 3072)]
 MALL_BYTES = 256 << 20
 COPY_BYTES = 256 << 20
 TRAFFIC_FILE = ROOT / "profiles" / "w4a16_linear_qwen3_0.6b_sweep_traffic.json"
-KERNELS_FILE = ROOT / "profiles" / "w4a16_linear_qwen3_0.6b_sweep_kernels.json"
 
 
 def _load_json(path: Path):
@@ -415,6 +414,15 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         }
         log(f"decode ({model.n_streams} streams): {runs[s]['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step; "
             f"prefill {tm['prompt_ms']:.2f} ms; end to end {runs[s]['end_to_end_tokens_per_s']} tok/s")
+    # each kernel of the step alone, event-timed outside any profiler, at position 576
+    # (the middle of the timed steps' 512..638)
+    model.set_streams(1)
+    log("decode step kernels, each alone (graphs of its launches in one step, HBM-cold, events)")
+    per_kernel = time_step_kernels(model, dev, max(steps, 10), prompt_len + new_tokens // 2)
+    kernel_sum_ms = sum(v["us_per_step"] for v in per_kernel.values() if isinstance(v, dict)) / 1e3
+    log("decode step kernels (us per launch): " + ", ".join(
+        f"{k} {v['us_per_launch'] if isinstance(v, dict) else v}" for k, v in per_kernel.items())
+        + f"; sum {kernel_sum_ms:.3f} ms per step")
     # the prompt consumed one position at a time through the decode step (the NPU runner's way)
     teacher_forced = None
     if teacher_forced_leg:
@@ -459,6 +467,12 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                     f"prompt {prompt_len} (one prefill pass), {new_tokens} new tokens",
         **best,
         "by_streams": {str(k): v for k, v in runs.items()},
+        "step_kernels": {"position": prompt_len + new_tokens // 2, "by_kernel": per_kernel,
+                         "sum_ms_per_step": round(kernel_sum_ms, 4),
+                         "method": "each kernel's launches of one step in a graph of their own (28 launches; a "
+                                   "per-step kernel 28 times), HBM-cold (a 512 MB read between replays), HIP "
+                                   "events per replay on the launch stream, no host wait between replays; wall "
+                                   "time per launch"},
         "teacher_forced_prompt": teacher_forced,
         "one_launch_step": one_launch,
         "greedy_parity": oracle,
@@ -467,6 +481,98 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     del model
     torch.cuda.empty_cache()
     return out, tensors, prompt
+
+
+def time_step_kernels(model, dev, reps: int, pos: int) -> dict:
+    """Each kernel of the batch-decode step on its own, outside any profiler: per
+    kernel a graph of its launches in one step (28 per layer kernel, one for the
+    per-step ones) over the model's own weights and caches at position ``pos`` for
+    every sequence, replayed ``reps`` times; a read of a 512 MB pool between
+    replays (untimed) leaves the MALL without any of the step's bytes, as the
+    1.6 GB step itself does, so every replay reads HBM.  HIP events bracket each
+    replay on the stream the kernels run on.  Returns microseconds per launch
+    (wall time in the graph: launch gaps included, an upper bound on the kernel's
+    own duration) and per step, with each kernel's algorithmic bytes."""
+    import torch
+    from torch2iron_amd import ops
+    from torch2iron_amd.formats import algorithmic_bytes
+    c, b = model.cfg, model.batch
+    buf = model.micro[0].buf
+    positions = torch.full((b,), pos, dtype=torch.int32, device=dev)
+    adv_positions = positions.clone()   # advanced by every greedy_advance replay
+    pool = torch.empty(512 << 20, dtype=torch.uint8, device=dev).fill_(3)
+    sink = torch.empty(1 << 20, dtype=torch.int32, device=dev)
+    x0 = model.x.clone()
+    tokens = model.tokens.clone()
+    kv_bytes = b * c.n_kv_heads * (pos + 1) * c.head_dim * 2 * 2
+    qkv_n, hq = c.qkv_dim, c.n_heads * c.head_dim
+    per_layer = [
+        ("rmsnorm_qkv", lambda i, L: ops.rmsnorm_linear(buf.x, L.w.ln1, c.eps, L.w.qkv, out=buf.qkv),
+         algorithmic_bytes(b, c.hidden, qkv_n) + c.hidden * 2),
+        ("attention", lambda i, L: ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, L.w.q_norm,
+                                                        L.w.k_norm, c.eps, model.rope, model.k_cache[i],
+                                                        model.v_cache[i], rope_style=L.rope_style, out=buf.ctx,
+                                                        workspace=buf.workspace),
+         kv_bytes + b * qkv_n * 2 + b * c.n_kv_heads * c.head_dim * 2 * 2 + b * hq * 2),
+        ("o_proj_residual", lambda i, L: ops.linear(buf.ctx, L.w.o, residual=buf.x, out=buf.x),
+         algorithmic_bytes(b, hq, c.hidden) + b * c.hidden * 2),
+        ("rmsnorm_gate_up_swiglu", lambda i, L: ops.rmsnorm_gate_up(buf.x, L.w.ln2, c.eps, L.w.gate_up, swiglu=True,
+                                                                    out=buf.hmlp),
+         algorithmic_bytes(b, c.hidden, 2 * c.intermediate) - b * c.intermediate * 2 + c.hidden * 2),
+        ("down_residual", lambda i, L: ops.linear(buf.hmlp, L.w.down, residual=buf.x, out=buf.x),
+         algorithmic_bytes(b, c.intermediate, c.hidden) + b * c.hidden * 2),
+    ]
+    per_step = [
+        ("embedding_gather_rmsnorm", lambda: ops.rmsnorm(model.embed, model.layers[0].w.ln1, c.eps, out=buf.xn,
+                                                         tokens=model.tokens, x_out=buf.x, argmax_keys=model.keys),
+         b * c.hidden * 2 * 3 + c.hidden * 2 + b * 4),
+        ("final_rmsnorm_lm_head_argmax", lambda: model._head(False),
+         model.lm_head.numel() * 2 + b * c.hidden * 2 + c.hidden * 2 + b * 8),
+        ("greedy_advance", lambda: ops.greedy_advance(model.keys, model.tokens, adv_positions, None, model.step),
+         b * 8 + b * 4 * 3),
+    ]
+    out = {}
+    n = len(model.layers)
+    # a per-step kernel is launched n times in its graph too, so that every graph
+    # spreads its own start over the same number of launches
+    jobs = [(name, [lambda i=i, L=L, f=f: f(i, L) for i, L in enumerate(model.layers)], 1, nb)
+            for name, f, nb in per_layer]
+    jobs += [(name, [f] * n, n, nb) for name, f, nb in per_step]
+    jobs.append(("graph_floor_one_element_fill", [lambda: sink[:1].fill_(0)] * n, n, 0))
+    stream = torch.cuda.current_stream(dev)
+    for name, calls, div, nbytes in jobs:
+        for fn in calls:
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for fn in calls:
+                fn()
+        marks = []
+        for r in range(reps + 1):   # no host wait between replays: the GPU never idles
+            model.x.copy_(x0)
+            buf.x.copy_(x0)
+            model.tokens.copy_(tokens)
+            ops.stream_read(pool, out=sink)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            marks.append((e0, e1))
+        torch.cuda.synchronize()
+        total = sum(a.elapsed_time(b) for a, b in marks[1:])   # the first replay is a warm-up
+        us = total * 1e3 / (reps * len(calls))
+        per_step_launches = len(calls) // div
+        out[name] = {"launches_per_step": per_step_launches, "us_per_launch": round(us, 3),
+                     "us_per_step": round(us * per_step_launches, 1), "algorithmic_bytes_per_launch": int(nbytes),
+                     "TBps": round(nbytes / us / 1e6, 4), "frac_of_8TBps": round(nbytes / us / 1e6 / 8.0, 4)}
+        del g
+    floor = out.pop("graph_floor_one_element_fill")
+    out["graph_floor_us_per_launch"] = floor["us_per_launch"]
+    model.x.copy_(x0)
+    model.tokens.copy_(tokens)
+    del pool, sink
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -743,6 +849,7 @@ def main():
     cold_copies = cold.copies
     cold_bytes = cold.bytes_per_step
     cold_groups = [dict(label=gr["label"], bytes=gr["bytes"], launches=gr["launches"]) for gr in cold.groups]
+    cold_launches = cold.launches_per_step
 
     if args.calibrate_copy:
         src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
@@ -821,7 +928,7 @@ def main():
 
     achieved_gbps = value * 1e3
     traffic = _load_json(TRAFFIC_FILE)
-    kernels = _load_json(KERNELS_FILE)
+    bd = (decode or {}).get("batch_decode") or {}
     line = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -833,6 +940,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
+        "decode_tokens_per_s": bd.get("decode_tokens_per_s"),
+        "decode_ms_per_step": bd.get("ms_per_decode_step"),
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
@@ -855,11 +964,13 @@ def main():
             "avg_launch_us": round(avg_launch_us, 3),
             "launch_floor_us": None if floor_us is None else round(floor_us, 3),
             "read_ceiling": ceiling,
-            "kernel_time": None if not kernels else {
-                "avg_kernel_us": kernels.get("avg_kernel_us"),
-                "algorithmic_bytes_per_launch": kernels.get("algorithmic_bytes_per_launch"),
-                "frac": kernels.get("frac"),
-                "source": kernels.get("source")},
+            "kernel_time": {
+                "avg_us_per_launch": round(avg_launch_us, 3),
+                "algorithmic_bytes_per_launch": round(cold_bytes / cold_launches),
+                "frac": round(cold_bytes / cold_launches / (avg_launch_us * 1e-6) / (PEAK_GBPS * 1e9), 4),
+                "source": "HIP events around each (shape, M) group's graph of its launches (wall time per launch in "
+                          "the graph, an upper bound on the kernel's own duration); rocprofv3 traces are kept for "
+                          "kernel names and counters only: their per-dispatch signals stretch the durations"},
         },
         "cpu_baseline": cpu,
         "breakdown": breakdown,

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 3
+#define T2I_ABI_VERSION 4
 #define T2I_MAX_ROWS (65535 * 16)   /* rows of one linear call: 16-row tiles in grid.z */
 
 #define T2I_OK 0
@@ -144,6 +144,50 @@ int t2i_decode_attention(const uint16_t* qkv, const int32_t* positions, int32_t 
                          uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
                          uint16_t* ctx, void* workspace, size_t workspace_bytes,
                          void* stream);
+
+/* The same attention on q / k / v that are normalised and rotated already (the
+ * reference's runlist runs RMSNormRoPE on them first): q bf16 [B, Hq*D], k and v
+ * bf16 [B, Hkv*D].  Per sequence b: k_cache[b][h][p] <- k, v_cache[b][h][p] <- v,
+ * ctx as t2i_decode_attention; no norm weights and no RoPE table.  Workspace as
+ * t2i_decode_attention (t2i_decode_attention_workspace_bytes).
+ * Replaces: torch2iron/operators/copy_present_packet_kv (CopyPresentPacketKV) and
+ *           llama_chunked_attention (LlamaChunkedAttention), the per-row pair of
+ *           quantized_qwen3/batch_decode_fused.py:445-479 (the KV cache here is
+ *           contiguous [B, Hkv, ctx_cap, D], not the 64-slot packet layout).
+ */
+int t2i_decode_attention_prepared(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                  const int32_t* positions, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                                  uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Standalone elementwise operators of the reference's batch-decode runlist.  The
+ * decode layer folds each into a neighbouring kernel; these run a runlist written
+ * for the NPU entry for entry.  Outputs may alias inputs.
+ *
+ * t2i_rmsnorm_rope: rows of `cols` values; y = RoPE(RMSNorm(x) * weight), row r
+ * rotated by angle row r / (rows / angle_rows) of `angles` (bf16 [angle_rows,
+ * cols], cos at even, sin at odd columns), rounded as t2i_decode_attention's
+ * prologue.  rope_style 0 = halves (i, i + cols/2), 1 = interleaved.  cols even,
+ * at most 1024; angle_rows divides rows.
+ * Replaces: torch2iron/operators/rms_norm_rope (RMSNormRoPE, op.py:20-96,
+ *           kernel.cc:39-67).
+ *
+ * t2i_silu_mul: out = bf16(bf16(silu(left)) * right) over n values (n % 8 == 0),
+ * the SwiGLU epilogue's rounding.
+ * Replaces: torch2iron/operators/silu_mul (SiLUMul, op.py:20-79).
+ *
+ * t2i_residual_add_rmsnorm: x_out = bf16(x + update), y = t2i_rmsnorm(x_out,
+ * weight, eps) bit for bit; M rows of H.
+ * Replaces: torch2iron/operators/residual_add_rms_norm (ResidualAddRMSNorm,
+ *           op.py:19-93).
+ */
+int t2i_rmsnorm_rope(const uint16_t* x, int32_t rows, int32_t cols, const uint16_t* weight,
+                     const uint16_t* angles, int32_t angle_rows, float eps, int32_t rope_style,
+                     uint16_t* y, void* stream);
+int t2i_silu_mul(const uint16_t* left, const uint16_t* right, int64_t n, uint16_t* out, void* stream);
+int t2i_residual_add_rmsnorm(const uint16_t* x, const uint16_t* update, int32_t M, int32_t H,
+                             const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y, void* stream);
 
 /* ---------------------------------------------------------------------------
  * The front of the decode layer in one cooperative launch: the input RMSNorm +

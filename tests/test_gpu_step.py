@@ -166,3 +166,58 @@ def test_step_falls_back_where_no_plan(gpu):
     layers[0]["k_cache"] = m3.k_cache[0, :8]
     with pytest.raises(ValueError):
         ops.DecodeLayerTable(layers, big.n_heads, big.n_kv_heads, gpu)
+
+
+@pytest.mark.parametrize("form", ["persistent", "fused"])
+def test_error_word_set_by_the_host_gives_up_then_clears(gpu, form):
+    """A one-launch path whose error word is already set gives up every bounded
+    wait early and still returns (every kernel exits); the error is reported and
+    ``check_errors`` clears it; the next launch then gives exactly the bits of a
+    model that never failed, from the same state."""
+    print(f"error word test, {form}", flush=True)
+    cfg = gm.Qwen3Config(n_layers=2, vocab=512)
+    b, cap = 4, 128
+    t = gm.random_qwen3_tensors(cfg, seed=7, weights="centered")
+    kw = dict(persistent=True) if form == "persistent" else dict(fused=True, persistent=False)
+    m = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, **kw)
+    fresh = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, **kw)
+    g = torch.Generator().manual_seed(8)
+    kc = torch.randn(m.k_cache.shape, generator=g).to(BF16).to(gpu)
+    vc = torch.randn(m.v_cache.shape, generator=g).to(BF16).to(gpu)
+    tok = torch.randint(0, cfg.vocab, (b,), generator=g, dtype=torch.int32).to(gpu)
+    pos = torch.tensor([0, 17, 64, 127], dtype=torch.int32, device=gpu)
+
+    def reset(model):
+        model.k_cache.copy_(kc)
+        model.v_cache.copy_(vc)
+        model.tokens.copy_(tok)
+        model.positions.copy_(pos)
+
+    ws = m.micro[0].buf.workspace
+    if form == "persistent":
+        assert m.step_table is not None
+        word, off = ops._step_region(m.step_table, 4, gpu, ws)
+        errors = lambda: ops.decode_step_errors(m.step_table, gpu, workspace=ws)
+    else:
+        lib = ops._lib.load()
+        off = lib.t2i_qkv_attention_error_offset(b, cfg.n_heads, cfg.n_kv_heads)
+        nbytes = lib.t2i_qkv_attention_workspace_bytes(b, cfg.n_heads, cfg.n_kv_heads)
+        word = ws.get(("qkv_attn", b, cfg.n_heads, cfg.n_kv_heads), nbytes, gpu)
+        errors = lambda: ops.qkv_attention_errors(b, cfg.n_heads, cfg.n_kv_heads, gpu, workspace=ws)
+    reset(m)
+    word[off:off + 4].view(torch.int32).fill_(1)     # raised before the launch starts
+    m.forward_step(with_head=False)
+    torch.cuda.synchronize()
+    assert errors() != 0
+    with pytest.raises(RuntimeError, match="timed out"):
+        m.check_errors()
+    assert errors() == 0
+    reset(m)
+    reset(fresh)
+    m.forward_step(with_head=False)
+    fresh.forward_step(with_head=False)
+    torch.cuda.synchronize()
+    assert errors() == 0
+    m.check_errors()
+    assert torch.equal(m.x, fresh.x)
+    assert torch.equal(m.k_cache, fresh.k_cache) and torch.equal(m.v_cache, fresh.v_cache)

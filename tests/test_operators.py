@@ -259,3 +259,86 @@ def test_runlist_layer_matches_decode_layer(gpu, layers):
     assert torch.equal(m2.x, m1.x)
     assert torch.equal(m2.k_cache, m1.k_cache) and torch.equal(m2.v_cache, m1.v_cache)
     assert torch.equal(fused.get_buffer("x"), m1.x)
+
+
+@pytest.mark.parametrize("batch", [1, 5, 16, 32])
+def test_reference_batch_decode_runlist_constructs(batch):
+    """The reference's per-step runlist (``batch_decode_fused.py:300-539``) for
+    Qwen3-0.6B: its operators are constructed with the reference's own arguments
+    (``:336-425``), every entry's buffer count matches its operator's arg spec,
+    and the per-layer sequence is the reference's, with one attention entry per
+    sequence in place of the packet-cache pair."""
+    cfg = gm.QWEN3_0_6B
+    built = R.batch_decode_runlist(cfg, 640, batch, lm_head_out_features=152064)
+    rl, rows = built["runlist"], built["decode_rows"]
+    assert rows == next(r for r in (4, 8, 16, 32) if batch <= r)
+    assert len(rl) == 1 + cfg.n_layers * (4 + batch + 6) + 1
+    assert all(len(bufs) == len(op.get_arg_spec()) for op, *bufs in rl)
+    names = [type(op).__name__ for op, *_ in rl[:5 + batch + 6]]
+    assert names == (["RMSNorm", "W4A16KGroupGEMM", "W4A16PairedKGroupGEMM", "RMSNormRoPE", "RMSNormRoPE"]
+                     + ["CopyPresentKVAttention"] * batch
+                     + ["W4A16KGroupGEMM", "ResidualAddRMSNorm", "W4A16PairedKGroupGEMM", "SiLUMul",
+                        "W4A16KGroupGEMM", "ResidualAddRMSNorm"])
+    norm, q_gemm, kv_gemm, rope_q, rope_k = (e[0] for e in rl[:5])
+    cols = min(8, rows)
+    assert (norm.size, norm.num_aie_columns, norm.num_channels, norm.tile_size, norm.weighted, norm.epsilon) == \
+        (rows * 1024, cols, 1, 1024, True, 1e-5)
+    assert (rope_q.rows, rope_q.cols, rope_q.angle_rows, rope_q.num_aie_columns) == (rows * 16, 128, rows, cols)
+    assert (rope_k.rows, rope_k.angle_rows) == (rows * 8, rows)
+    assert (q_gemm.M, q_gemm.K, q_gemm.N, q_gemm.k_group) == (rows, 1024, 2048, 4)
+    assert (kv_gemm.N, kv_gemm.k_group, kv_gemm.tile_m) == (1024, 2, 4 if rows <= 8 else 8)
+    silu = rl[5 + batch + 3][0]
+    assert (silu.size, silu.tile_size, silu.num_aie_columns) == (rows * 3072, 384, 8)
+    head = rl[-1][0]
+    assert type(head).__name__ == "W4A16NShardGEMM" and head.num_aie_rows == _n_shard_rows(152064, 64) and rl[-1][1:] == ("hidden_out",
+                                                                                                  "W_out_head_qparam",
+                                                                                                  "logits")
+    # the last layer's residual norm writes hidden_out with the final norm weight
+    assert rl[-2][1:] == ("x", "ffn_output", "W_final_norm", "x", "hidden_out")
+    attn = rl[5]
+    assert attn[1:] == ("queries[0:4096]", "keys[0:2048]", "values[0:2048]", "positions[0:4]",
+                        f"k_cache_0[0:{8 * 640 * 128 * 2}]", f"v_cache_0[0:{8 * 640 * 128 * 2}]",
+                        "attn_context[0:4096]")
+
+
+def test_reference_batch_decode_runlist_binds_on_the_host():
+    """A two-layer runlist binds its weight names and sizes every other buffer
+    (``FusedRunlist`` with the reference's ``buffer_sizes``), without a GPU."""
+    cfg = gm.Qwen3Config(n_layers=2, vocab=512)
+    t = gm.random_qwen3_tensors(cfg, seed=3, weights="centered")
+    built = R.batch_decode_runlist(cfg, 128, 3)
+    bufs = {"x": torch.zeros(4, 1024, dtype=BF16), "rope_angles": torch.zeros(4, 128, dtype=BF16),
+            "positions": torch.zeros(3, dtype=torch.int32), **R.batch_decode_weights(t, cfg, "cpu")}
+    for i in range(2):
+        bufs[f"k_cache_{i}"] = torch.zeros(3, 8, 128, 128, dtype=BF16)
+        bufs[f"v_cache_{i}"] = torch.zeros(3, 8, 128, 128, dtype=BF16)
+    fr = R.FusedRunlist("step", built["runlist"], built["input_args"], built["output_args"], bufs, "cpu",
+                        buffer_sizes=built["buffer_sizes"])
+    assert fr.get_buffer("queries").numel() == 4 * 2048 and fr.get_buffer("ffn_hidden").numel() == 4 * 3072
+    assert fr.get_buffer("attn_context[4096:8192]").numel() == 2048
+    assert fr.get_buffer("W_attn_key_value_1_qparam").N == 2048     # k|v paired
+    with pytest.raises(ValueError, match="explicit size"):
+        R.FusedRunlist("step", built["runlist"], built["input_args"], built["output_args"], bufs, "cpu")
+    with pytest.raises(ValueError):
+        R.batch_decode_runlist(cfg, 100, 3)          # max_seq_len % 64
+    with pytest.raises(ValueError):
+        R.batch_decode_runlist(cfg, 128, 33)         # beyond the 32-row bucket
+
+
+@pytest.mark.parametrize("ctor", [
+    lambda: O.RMSNorm(size=8 * 1000, num_aie_columns=8, num_channels=1, tile_size=1024, weighted=True),
+    lambda: O.RMSNorm(size=8 * 1024, num_aie_columns=8, num_channels=1, tile_size=1024, epsilon=0.0),
+    lambda: O.RMSNormRoPE(rows=128, cols=100, angle_rows=16),
+    lambda: O.RMSNormRoPE(rows=128, cols=128, angle_rows=12),
+    lambda: O.RMSNormRoPE(rows=128, cols=128, angle_rows=4),          # angle_rows < num_aie_columns
+    lambda: O.RMSNormRoPE(rows=130, cols=128, angle_rows=13, num_aie_columns=8),
+    lambda: O.SiLUMul(size=3000, tile_size=384),
+    lambda: O.ResidualAddRMSNorm(size=8 * 1024, num_aie_columns=8, tile_size=1000),
+    lambda: O.ResidualAddRMSNorm(size=8 * 1024, num_aie_columns=8, tile_size=1024, epsilon=-1.0),
+    lambda: O.CopyPresentKVAttention(max_seq_len=100, chunk_size=64),
+    lambda: O.CopyPresentKVAttention(max_seq_len=128, head_dim=64),   # the GPU kernel's D = 128
+    lambda: O.CopyPresentKVAttention(max_seq_len=128, head_dim=128, q_heads_per_group=3),
+])
+def test_runlist_operator_checks_raise_value_error(ctor):
+    with pytest.raises(ValueError):
+        ctor()

@@ -46,6 +46,14 @@ SIGNATURES = {
     "t2i_decode_attention_noalloc": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p,
                                                c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p, c_int32,
                                                c_void_p, c_void_p]),
+    "t2i_decode_attention_prepared": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32,
+                                                c_int32, c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_size_t,
+                                                c_void_p]),
+    "t2i_rmsnorm_rope": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_int32, c_float, c_int32,
+                                   c_void_p, c_void_p]),
+    "t2i_silu_mul": (c_int32, [c_void_p, c_void_p, ctypes.c_int64, c_void_p, c_void_p]),
+    "t2i_residual_add_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_float, c_void_p,
+                                           c_void_p, c_void_p]),
     "t2i_qkv_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "t2i_qkv_attention_error_offset": (c_size_t, [c_int32, c_int32, c_int32]),
     "t2i_qkv_attention": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_int32,

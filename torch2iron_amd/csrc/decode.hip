@@ -143,7 +143,10 @@ struct AttnParams {
 // run alongside the position's.
 //   heads_     = Hq | Hkv << 15 | rope_style << 30
 //   cap_chunk_ = ctx_cap | chunk << 23   (chunk <= 256)
-template <int Q, int ROWS>
+//   PREP = false (t2i_decode_attention_prepared): q, k and v come normalised and
+//   rotated already, as three row arrays: qkv_ = q [B, Hq*D], qn_ = k [B, Hkv*D],
+//   kn_ = v [B, Hkv*D]; no norm weights and no RoPE table are read.
+template <int Q, int ROWS, bool PREP = true>
 __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int32_t* pos_, const uint16_t* qkv_,
                                                                        uint16_t* kc_, uint16_t* vc_,
                                                                        const uint16_t* qn_, const uint16_t* kn_,
@@ -193,13 +196,23 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 #pragma unroll
   for (int n = 0; n < NV; ++n) {
     const int vi = min(wv + 4 * n, Q + 1);   // waves past the last vector reload it; unused
-    const int hrow = vi < Q ? h * Q + vi : (vi == Q ? p.Hq + h : p.Hq + p.Hkv + h);
-    const uint16_t* src = p.qkv + qkv_row + (size_t)hrow * D;
-    const uint16_t* gamma = vi < Q ? p.qn : p.kn;   // v takes no gamma; loaded, unused
+    const uint16_t* src;
+    if constexpr (PREP) {
+      const int hrow = vi < Q ? h * Q + vi : (vi == Q ? p.Hq + h : p.Hq + p.Hkv + h);
+      src = p.qkv + qkv_row + (size_t)hrow * D;
+    } else {
+      src = vi < Q ? p.qkv + ((size_t)b * p.Hq + h * Q + vi) * D
+                   : (vi == Q ? p.qn : p.kn) + ((size_t)b * p.Hkv + h) * D;
+    }
     px0[n] = bf16_to_f32(src[i0]);
     px1[n] = bf16_to_f32(src[i1]);
-    pg0[n] = bf16_to_f32(gamma[i0]);
-    pg1[n] = bf16_to_f32(gamma[i1]);
+    if constexpr (PREP) {
+      const uint16_t* gamma = vi < Q ? p.qn : p.kn;   // v takes no gamma; loaded, unused
+      pg0[n] = bf16_to_f32(gamma[i0]);
+      pg1[n] = bf16_to_f32(gamma[i1]);
+    } else {
+      pg0[n] = pg1[n] = 1.0f;
+    }
   }
   __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of everything that needs pos
 
@@ -212,8 +225,8 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 
   if (t0 < t1) {
     // ---- the RoPE row, then the chunk's K / V rows ----
-    const float cs = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]);
-    const float sn = bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]);
+    const float cs = PREP ? bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]) : 1.0f;
+    const float sn = PREP ? bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]) : 0.0f;
     __builtin_amdgcn_sched_barrier(0);   // the RoPE row ahead of the K / V rows
     // slots past the chunk's end reload its first slot; masked when scored.  The
     // K/V stream is read once per step: non-temporal loads (measured 12.8 -> 12.1 us
@@ -234,14 +247,16 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
     for (int n = 0; n < NV; ++n) {
       const int vi = wv + 4 * n;
       float x0 = px0[n], x1 = px1[n];
-      const float ss = wave_sum(x0 * x0 + x1 * x1);
-      const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
-      const float n0 = round_bf16(round_bf16(x0 * inv) * pg0[n]);
-      const float n1 = round_bf16(round_bf16(x1 * inv) * pg1[n]);
-      const float y0 = round_bf16(round_bf16(n0 * cs) + round_bf16(-n1 * sn));
-      const float y1 = round_bf16(round_bf16(n1 * cs) + round_bf16(n0 * sn));
-      x0 = vi <= Q ? y0 : x0;
-      x1 = vi <= Q ? y1 : x1;
+      if constexpr (PREP) {
+        const float ss = wave_sum(x0 * x0 + x1 * x1);
+        const float inv = round_bf16(1.0f / sqrtf(ss / (float)D + p.eps));
+        const float n0 = round_bf16(round_bf16(x0 * inv) * pg0[n]);
+        const float n1 = round_bf16(round_bf16(x1 * inv) * pg1[n]);
+        const float y0 = round_bf16(round_bf16(n0 * cs) + round_bf16(-n1 * sn));
+        const float y1 = round_bf16(round_bf16(n1 * cs) + round_bf16(n0 * sn));
+        x0 = vi <= Q ? y0 : x0;
+        x1 = vi <= Q ? y1 : x1;
+      }
       if (vi >= Q + 2) continue;
       if (vi < Q) {
         s_q[vi][i0] = (uint16_t)f32_to_bf16(x0);
@@ -843,13 +858,27 @@ AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
   return pl;
 }
 
-template <int Q, int ROWS>
+template <int Q, int ROWS, bool PREP>
 hipError_t launch_attention(const AttnParams& p, dim3 grid, hipStream_t s) {
   const int heads = p.Hq | p.Hkv << 15 | p.style << 30;
   const int cap_chunk = (int)((unsigned)p.ctx_cap | (unsigned)p.chunk << 23);
-  hipLaunchKernelGGL((decode_attention_kernel<Q, ROWS>), grid, dim3(ATT_THREADS), 0, s, p.pos, p.qkv, p.kc, p.vc, p.qn,
-                     p.kn, heads, cap_chunk, p);
+  hipLaunchKernelGGL((decode_attention_kernel<Q, ROWS, PREP>), grid, dim3(ATT_THREADS), 0, s, p.pos, p.qkv, p.kc,
+                     p.vc, p.qn, p.kn, heads, cap_chunk, p);
   return hipGetLastError();
+}
+
+template <bool PREP>
+hipError_t launch_attention_plan(const AttnParams& p, int Q, int rows, dim3 grid, hipStream_t s) {
+  switch (Q * 100 + rows) {
+    case 104: return launch_attention<1, 4, PREP>(p, grid, s);
+    case 108: return launch_attention<1, 8, PREP>(p, grid, s);
+    case 116: return launch_attention<1, 16, PREP>(p, grid, s);
+    case 204: return launch_attention<2, 4, PREP>(p, grid, s);
+    case 208: return launch_attention<2, 8, PREP>(p, grid, s);
+    case 216: return launch_attention<2, 16, PREP>(p, grid, s);
+    case 404: return launch_attention<4, 4, PREP>(p, grid, s);
+    default: return launch_attention<8, 2, PREP>(p, grid, s);
+  }
 }
 
 }  // namespace
@@ -914,18 +943,9 @@ int run_attention(const AttnPlan& pl, const uint16_t* qkv, const int32_t* positi
   p.eps = eps;
   p.scale = (float)(1.0 / sqrt((double)D));
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e;
   const dim3 grid(B * Hkv, pl.splits);
-  switch (Q * 100 + pl.rows) {
-    case 104: e = launch_attention<1, 4>(p, grid, s); break;
-    case 108: e = launch_attention<1, 8>(p, grid, s); break;
-    case 116: e = launch_attention<1, 16>(p, grid, s); break;
-    case 204: e = launch_attention<2, 4>(p, grid, s); break;
-    case 208: e = launch_attention<2, 8>(p, grid, s); break;
-    case 216: e = launch_attention<2, 16>(p, grid, s); break;
-    case 404: e = launch_attention<4, 4>(p, grid, s); break;
-    default: e = launch_attention<8, 2>(p, grid, s); break;
-  }
+  const hipError_t e = rope ? launch_attention_plan<true>(p, Q, pl.rows, grid, s)
+                            : launch_attention_plan<false>(p, Q, pl.rows, grid, s);
   return t2i_host::hip_status(e, "attention launch");
 }
 
@@ -944,18 +964,29 @@ static_assert(ATT_SCRATCH_BYTES == T2I_DECODE_ATTENTION_SCRATCH_BYTES, "header a
 std::mutex g_scratch_mu;
 char* g_scratch_ptr[ATT_MAX_DEVICES];   // device address of `scratch` on each device, once known
 
-// The device address of the current device's copy of `scratch` (set up on the
-// first call on that device).  Host code uses only this address: the array's
-// own name on the host is a stand-in, not a device address.
-int scratch_for_current_device(char** out) {
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
+// The device address of the copy of `scratch` on the device that `stream`
+// belongs to (the current device for the null stream), set up on the first call
+// on that device with that device current.  Host code uses only this address:
+// the array's own name on the host is a stand-in, not a device address.
+int scratch_for_stream(hipStream_t stream, char** out) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return t2i_host::hip_status(e, "hipGetDevice");
+  int dev = cur;
+  if (stream) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) return t2i_host::hip_status(e, "hipStreamGetDevice");
+  }
   if (dev < 0 || dev >= ATT_MAX_DEVICES) return fail(T2I_ERR_VALUE, "device %d beyond %d", dev, ATT_MAX_DEVICES);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) return t2i_host::hip_status(e, "hipSetDevice");
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(t2i::scratch));
+    if (dev != cur) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess && r != hipSuccess) return t2i_host::hip_status(r, "hipSetDevice");
+    }
     if (e != hipSuccess) return t2i_host::hip_status(e, "hipGetSymbolAddress(scratch)");
     if (!ptr) return fail(T2I_ERR_NULL, "scratch has no device address");
     g_scratch_ptr[dev] = static_cast<char*>(ptr);
@@ -986,6 +1017,29 @@ extern "C" int t2i_decode_attention(const uint16_t* qkv, const int32_t* position
                        ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr, stream);
 }
 
+extern "C" int t2i_decode_attention_prepared(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                             const int32_t* positions, int32_t B, int32_t Hq, int32_t Hkv, int32_t D,
+                                             uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, uint16_t* ctx,
+                                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (!k || !v) return fail(T2I_ERR_NULL, "attention pointers must not be NULL");
+  if (!aligned16(k) || !aligned16(v)) return fail(T2I_ERR_ALIGN, "attention tensors must be 16-byte aligned");
+  // the shared checks, with k and v standing in for the norm weights and q for the table
+  int rc = check_attention(q, positions, B, Hq, Hkv, D, k, v, 1e-6f, q, 0, k_cache, v_cache, ctx_cap, ctx);
+  if (rc) return rc;
+  const AttnPlan pl = plan_attention(B, Hq, Hkv, ctx_cap);
+  if (pl.bytes) {
+    if (!workspace) return fail(T2I_ERR_WORKSPACE, "workspace of %zu bytes required", pl.bytes);
+    if (workspace_bytes < pl.bytes) return fail(T2I_ERR_WORKSPACE, "workspace %zu < required %zu", workspace_bytes, pl.bytes);
+    if (!aligned16(workspace)) return fail(T2I_ERR_ALIGN, "workspace must be 16-byte aligned");
+  }
+  char* ws = pl.bytes ? reinterpret_cast<char*>(workspace) : nullptr;
+  // rope == NULL selects the kernel form that takes q / k / v as they are
+  return run_attention(pl, q, positions, B, Hq, Hkv, D, k, v, 1e-6f, nullptr, 0, k_cache, v_cache, ctx_cap, ctx,
+                       ws ? reinterpret_cast<unsigned*>(ws) : nullptr,
+                       ws ? reinterpret_cast<float*>(ws + pl.off_ml) : nullptr,
+                       ws ? reinterpret_cast<float*>(ws + pl.off_o) : nullptr, stream);
+}
+
 extern "C" int t2i_decode_attention_noalloc(const uint16_t* qkv, const int32_t* positions, int32_t B, int32_t Hq,
                                             int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
                                             float eps, const uint16_t* rope, int32_t rope_style, uint16_t* k_cache,
@@ -1001,7 +1055,7 @@ extern "C" int t2i_decode_attention_noalloc(const uint16_t* qkv, const int32_t* 
                 "library's scratch", units, ATT_SCRATCH_UNITS, states, ATT_SCRATCH_BYTES - ATT_SCRATCH_COUNTERS);
   char* base = nullptr;
   if (pl.bytes) {
-    rc = scratch_for_current_device(&base);
+    rc = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &base);
     if (rc) return rc;
   }
   return run_attention(pl, qkv, positions, B, Hq, Hkv, D, q_norm, k_norm, eps, rope, rope_style, k_cache, v_cache,

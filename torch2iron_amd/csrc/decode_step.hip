@@ -13,9 +13,19 @@
 // its input, so the weight stream overlaps the hand-off; the K / V prefetch of
 // a layer's attention item goes out before the layer's qkv projection reads
 // its input.  No buffer is rewritten within a launch before everything that
-// reads it is done: layer l + 1's qkv words (the only reused buffer) are
-// written once all of layer l's residual stream exists, which needs every
-// context row of layer l, which needs every read of layer l's qkv words.
+// reads it is done.  Two buffers are reused by every layer:
+//   * the qkv words: layer l + 1's are written once all of layer l's residual
+//     stream exists, which needs every context row of layer l, which needs
+//     every read of layer l's qkv words;
+//   * the attention split states st ([B*Hkv][S-1][Q][D+2], written by splits
+//     1 .. S-1 of each (b, h) item and read by its split 0, the merger): a
+//     split of layer l + 1 writes its state only after it has read its q/k/v
+//     words of layer l + 1 for row b, which exist only once row b's residual
+//     stream of layer l exists, which needs row b's whole context row of layer
+//     l (o_proj reads every head), which each merger of (b, h) writes only
+//     after it has read every split state of layer l.  The states also carry
+//     the layer's tag, so a merger never takes another layer's state: it would
+//     wait instead, and a wait that gives up raises the error word.
 //
 // The linear phases run the decode linear's tiles (linear_phase, with
 // linear_tile's chunk ranges, arithmetic and reduction order) on the plans

@@ -43,6 +43,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
 }
 
+// silu(g) = g / (1 + e^-g) in fp32 (libm exponential, IEEE division); the decode
+// SwiGLU epilogue and the standalone SiLU-multiply round it to bf16 right after.
+__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
+
 __device__ __forceinline__ float f16_to_f32(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
 }

@@ -116,7 +116,6 @@ __device__ __forceinline__ bf16x8 ones_operand() {
   return __builtin_bit_cast(bf16x8, d);
 }
 
-__device__ __forceinline__ float silu_f32(float g) { return g / (1.0f + expf(-g)); }
 // g * sigmoid(g) on v_exp_f32 and v_rcp_f32: a few ulp of fp32 from silu_f32 (the
 // result is rounded to bf16 right after).  For the prompt GEMM's epilogue, where
 // the libm exponential and the IEEE division cost more than its k-loop's last steps.

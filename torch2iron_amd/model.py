@@ -269,8 +269,13 @@ class Qwen3Model:
     one micro-batch's small launches overlaps with another's work on the other
     hardware queues.  The streams join once per step for the final RMSNorm and
     the tied lm_head with its argmax, which read the embedding table once for
-    the whole batch.  Sequences never interact, so the tokens do not depend on
-    the split.
+    the whole batch.  Sequences never interact, and a linear's K split depends
+    on its shape alone up to 16 rows, so the tokens do not depend on the split
+    while every micro-batch has at most 16 rows (as does a batch of 16 or fewer
+    in one stream).  Above 16 rows the linears split K another way (16 waves,
+    or 32-column blocks), so a batch of 32 in one stream and the same batch as
+    two 16-row streams sum their fp32 partials in different orders, and a
+    near-tie can then pick another token.
 
     Two one-launch alternatives, both off by default because they measured
     slower than the separate kernels (Qwen3-0.6B, batch 16, context 576):
@@ -358,15 +363,24 @@ class Qwen3Model:
         return table if table.workspace_bytes() > 0 else None
 
     def check_errors(self) -> None:
-        """Raise if a wait inside a one-launch path timed out (synchronises)."""
+        """Raise if a wait inside a one-launch path timed out (synchronises).
+
+        The error word is cleared before raising: a launch that finds it set gives
+        up every wait early, so it would otherwise spoil every later step."""
         c = self.cfg
         if self.step_table is not None:
-            if ops.decode_step_errors(self.step_table, self.device, workspace=self.micro[0].buf.workspace):
-                raise RuntimeError("t2i_decode_step: a wait inside the launch timed out (error word set)")
+            ws = self.micro[0].buf.workspace
+            if ops.decode_step_errors(self.step_table, self.device, workspace=ws):
+                ops.clear_decode_step_errors(self.step_table, self.device, workspace=ws)
+                raise RuntimeError("t2i_decode_step: a wait inside the launch timed out (error word set, now "
+                                   "cleared)")
         elif self.layers and self.layers[0].fused:
             m = self.micro[0]
             if ops.qkv_attention_errors(m.b1 - m.b0, c.n_heads, c.n_kv_heads, self.device, workspace=m.buf.workspace):
-                raise RuntimeError("t2i_qkv_attention: a wait inside the launch timed out (error word set)")
+                ops.clear_qkv_attention_errors(m.b1 - m.b0, c.n_heads, c.n_kv_heads, self.device,
+                                               workspace=m.buf.workspace)
+                raise RuntimeError("t2i_qkv_attention: a wait inside the launch timed out (error word set, now "
+                                   "cleared)")
 
     @property
     def n_streams(self) -> int:

@@ -29,6 +29,18 @@ Reference operators:
 * ``Q4NXFusedLinearResidualProjection``  ``fast_qwen3/operators/q4nx_fused_linear_residual_projection/op.py:31-118``,
                                          args (ctx, residual, W, out)
 
+The standalone operators of the reference's batch-decode runlist
+(``quantized_qwen3/batch_decode_fused.py:336-425``), one kernel each:
+
+* ``RMSNorm``                ``torch2iron/operators/rms_norm/op.py:20-143``, args (x, [weight,] y)
+* ``RMSNormRoPE``            ``torch2iron/operators/rms_norm_rope/op.py:19-96``, args (x, weight, angles, y)
+* ``SiLUMul``                ``torch2iron/operators/silu_mul/op.py:20-79``, args (left, right, out)
+* ``ResidualAddRMSNorm``     ``torch2iron/operators/residual_add_rms_norm/op.py:19-93``,
+                             args (x, update, weight, x_out, y)
+* ``CopyPresentKVAttention`` the per-row pair ``CopyPresentPacketKV`` + ``LlamaChunkedAttention``
+                             (``copy_present_packet_kv/op.py:18-95``, ``llama_chunked_attention/op.py:20-150``)
+                             on the contiguous KV cache, args (q, k, v, positions, k_cache, v_cache, out)
+
 Batch-row forms of the fused projections (one call per decode batch and full
 output width, the shapes the GPU decode layer runs):
 
@@ -522,3 +534,210 @@ class Qwen3LayerFused:
         self._impl(self._buf, positions, k_cache, v_cache)
         hidden.view(self.rows, -1).copy_(self._buf.x)
         return hidden
+
+
+# ---------------------------------------------------------------------------
+# The standalone operators of the batch-decode runlist (torch2iron operators)
+# ---------------------------------------------------------------------------
+# Their NPU fields (``num_aie_columns``, ``num_channels``, ``tile_size``) keep
+# their meaning for the buffer shapes and divisibility checks; the ShimDMA
+# channel budget checks of the reference (an NPU resource) have no counterpart.
+
+@dataclass
+class RMSNorm:
+    """Row-wise RMSNorm over rows of ``tile_size`` (``rms_norm/op.py:20-143``);
+    ``weighted`` multiplies by a ``[tile_size]`` weight (the decode runlist's form)."""
+
+    size: int
+    num_aie_columns: int
+    num_channels: int
+    tile_size: int
+    weighted: bool = False
+    epsilon: float = 1e-5
+    context: object = field(default=None, repr=False)
+    _ones: object = field(default=None, repr=False)
+
+    def __post_init__(self):
+        if self.epsilon <= 0:
+            raise ValueError(f"epsilon must be positive, got {self.epsilon}")
+        max_multiple = self.num_aie_columns * self.num_channels * self.tile_size
+        if self.size % max_multiple != 0:
+            raise ValueError(f"size ({self.size}) must be a multiple of "
+                             f"num_aie_columns * num_channels * tile_size ({max_multiple})")
+        if self.tile_size % 8 != 0 or self.tile_size > 8192:
+            raise ValueError("tile_size must be a multiple of 8, at most 8192")
+
+    def get_arg_spec(self):
+        rows = (self.size // self.tile_size, self.tile_size)
+        specs = [ArgSpec("in", rows, BF16)]
+        if self.weighted:
+            specs.append(ArgSpec("in", (self.tile_size,), BF16))
+        specs.append(ArgSpec("out", rows, BF16))
+        return specs
+
+    def __call__(self, x, *rest):
+        if self.weighted:
+            weight, y = rest
+        else:
+            (y,) = rest
+            if self._ones is None or self._ones.device != x.device:
+                self._ones = torch.ones(self.tile_size, dtype=BF16, device=x.device)
+            weight = self._ones
+        return ops.rmsnorm(x.view(-1, self.tile_size), weight, self.epsilon, out=y.view(-1, self.tile_size))
+
+
+@dataclass
+class RMSNormRoPE:
+    """Weighted RMSNorm then two-halves RoPE of ``rows`` head rows of ``cols``
+    (``rms_norm_rope/op.py:19-96``, kernel ``kernel.cc:39-67``): row r takes angle
+    row ``r // (rows // angle_rows)`` (cos at even, sin at odd columns)."""
+
+    rows: int
+    cols: int
+    angle_rows: int
+    num_aie_columns: int = 8
+    epsilon: float = 1e-5
+    context: object = field(default=None, repr=False)
+
+    def __post_init__(self):
+        # the reference's checks (rms_norm_rope/op.py:35-46)
+        if self.cols % 32 != 0:
+            raise ValueError("cols must be divisible by 32")
+        if self.rows % self.num_aie_columns != 0:
+            raise ValueError("rows must be divisible by num_aie_columns")
+        if self.angle_rows > self.rows or self.rows % self.angle_rows != 0:
+            raise ValueError("angle_rows must divide rows")
+        if self.angle_rows < self.num_aie_columns or self.angle_rows % self.num_aie_columns != 0:
+            raise ValueError("angle_rows must be divisible by num_aie_columns")
+        if self.epsilon <= 0:
+            raise ValueError("epsilon must be positive")
+        if self.cols > 1024:
+            raise ValueError("cols must be at most 1024")
+
+    def get_arg_spec(self):
+        return [ArgSpec("in", (self.rows, self.cols), BF16), ArgSpec("in", (self.cols,), BF16),
+                ArgSpec("in", (self.angle_rows, self.cols), BF16), ArgSpec("out", (self.rows, self.cols), BF16)]
+
+    def __call__(self, x, weight, angles, y):
+        return ops.rmsnorm_rope(x.view(self.rows, self.cols), weight, angles.view(self.angle_rows, self.cols),
+                                self.epsilon, rope_style=ops.ROPE_HALVES, out=y.view(self.rows, self.cols))
+
+
+@dataclass
+class SiLUMul:
+    """``silu(left) * right`` elementwise (``silu_mul/op.py:20-79``)."""
+
+    size: int
+    tile_size: int
+    num_aie_columns: int = 8
+    context: object = field(default=None, repr=False)
+
+    def __post_init__(self):
+        if self.size % (self.num_aie_columns * self.tile_size) != 0:
+            raise ValueError(f"size ({self.size}) must be a multiple of "
+                             f"num_aie_columns * tile_size ({self.num_aie_columns * self.tile_size})")
+        if self.size % 8 != 0:
+            raise ValueError("size must be a multiple of 8")
+
+    def get_arg_spec(self):
+        return [ArgSpec("in", (self.size,), BF16), ArgSpec("in", (self.size,), BF16),
+                ArgSpec("out", (self.size,), BF16)]
+
+    def __call__(self, left, right, out):
+        return ops.silu_mul(left.view(-1), right.view(-1), out=out.view(-1))
+
+
+@dataclass
+class ResidualAddRMSNorm:
+    """``x_out = x + update``, then the weighted RMSNorm of ``x_out`` over rows of
+    ``tile_size`` (``residual_add_rms_norm/op.py:19-93``).  ``x_out`` may be ``x``."""
+
+    size: int
+    num_aie_columns: int
+    tile_size: int
+    epsilon: float = 1e-5
+    context: object = field(default=None, repr=False)
+
+    def __post_init__(self):
+        if self.epsilon <= 0:
+            raise ValueError("epsilon must be positive")
+        if self.size % (self.num_aie_columns * self.tile_size) != 0:
+            raise ValueError("size must be divisible by num_aie_columns * tile_size")
+        if self.tile_size % 8 != 0 or self.tile_size > 8192:
+            raise ValueError("tile_size must be a multiple of 8, at most 8192")
+
+    def get_arg_spec(self):
+        return [ArgSpec("in", (self.size,), BF16), ArgSpec("in", (self.size,), BF16),
+                ArgSpec("in", (self.tile_size,), BF16), ArgSpec("out", (self.size,), BF16),
+                ArgSpec("out", (self.size,), BF16)]
+
+    def __call__(self, x, update, weight, x_out, y):
+        ops.residual_add_rmsnorm(x.view(-1), update.view(-1), weight, self.epsilon, x_out=x_out.view(-1),
+                                 out=y.view(-1))
+        return y
+
+
+@dataclass
+class CopyPresentKVAttention:
+    """The runlist pair ``CopyPresentPacketKV`` + ``LlamaChunkedAttention``
+    (``batch_decode_fused.py:445-479``) on the contiguous KV cache: writes the
+    current k and v of ``rows`` sequences at their positions and attends (GQA)
+    over slots ``0 .. position``.  q and k arrive normalised and rotated
+    (``RMSNormRoPE``).  Constructor fields are ``LlamaChunkedAttention``'s
+    (``llama_chunked_attention/op.py:35-63``; ``chunk_size`` is the NPU packet
+    size, checked and otherwise unused) plus ``rows``.  Args ``(q [rows, Hq*D],
+    k [rows, Hkv*D], v [rows, Hkv*D], positions int32 [rows], k_cache, v_cache,
+    out [rows, Hq*D])``, caches ``[rows, Hkv, max_seq_len, D]``."""
+
+    max_seq_len: int
+    num_kv_groups: int = 8
+    q_heads_per_group: int = 4
+    head_dim: int = 64
+    chunk_size: int = 64
+    rows: int = 1
+    kernel_vector_size: int = field(default=32, repr=False)
+    context: object = field(default=None, repr=False)
+    _workspace: object = field(default=None, repr=False)
+
+    def __post_init__(self):
+        # the reference's checks (llama_chunked_attention/op.py:49-63)
+        if self.max_seq_len <= 0:
+            raise ValueError("max_seq_len must be positive")
+        if self.chunk_size <= 0:
+            raise ValueError("chunk_size must be positive")
+        if self.max_seq_len % self.chunk_size != 0:
+            raise ValueError("max_seq_len must be divisible by chunk_size")
+        if self.num_kv_groups <= 0:
+            raise ValueError("num_kv_groups must be positive")
+        if self.q_heads_per_group <= 0:
+            raise ValueError("q_heads_per_group must be positive")
+        if self.head_dim <= 0:
+            raise ValueError("head_dim must be positive")
+        if self.head_dim % self.kernel_vector_size != 0:
+            raise ValueError("head_dim must be divisible by kernel_vector_size")
+        # the GPU kernel's limits
+        if self.head_dim != 128:
+            raise ValueError("head_dim must be 128")
+        if self.q_heads_per_group not in (1, 2, 4, 8):
+            raise ValueError("q_heads_per_group must be 1, 2, 4 or 8")
+        if self.rows < 1:
+            raise ValueError("rows must be positive")
+        self._workspace = ops.Workspace()
+
+    def get_arg_spec(self):
+        hq = self.num_kv_groups * self.q_heads_per_group
+        cache = (self.rows, self.num_kv_groups, self.max_seq_len, self.head_dim)
+        return [ArgSpec("in", (self.rows, hq * self.head_dim), BF16),
+                ArgSpec("in", (self.rows, self.num_kv_groups * self.head_dim), BF16),
+                ArgSpec("in", (self.rows, self.num_kv_groups * self.head_dim), BF16),
+                ArgSpec("in", (self.rows,), torch.int32),
+                ArgSpec("inout", cache, BF16), ArgSpec("inout", cache, BF16),
+                ArgSpec("out", (self.rows, hq * self.head_dim), BF16)]
+
+    def __call__(self, q, k, v, positions, k_cache, v_cache, out):
+        hq = self.num_kv_groups * self.q_heads_per_group
+        cache = (self.rows, self.num_kv_groups, self.max_seq_len, self.head_dim)
+        return ops.decode_attention_prepared(q.view(self.rows, -1), k.view(self.rows, -1), v.view(self.rows, -1),
+                                             positions.view(-1), hq, self.num_kv_groups, k_cache.view(cache),
+                                             v_cache.view(cache), out=out.view(self.rows, -1),
+                                             workspace=self._workspace)

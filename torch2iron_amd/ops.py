@@ -276,6 +276,104 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, n_heads: int, n
     return out
 
 
+def decode_attention_prepared(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+                              n_heads: int, n_kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                              out: torch.Tensor | None = None, workspace: Workspace | None = None) -> torch.Tensor:
+    """KV write + GQA attention of one token per sequence whose q and k are
+    normalised and rotated already (``rmsnorm_rope``): ``q`` bf16 ``[B, Hq * D]``,
+    ``k`` / ``v`` bf16 ``[B, Hkv * D]``, caches ``[B, Hkv, ctx_cap, D]``.  Writes
+    k and v at ``positions`` and returns the context ``[B, Hq * D]``."""
+    for n, t in (("q", q), ("k", k), ("v", v), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _check_dev(n, t, BF16)
+    _check_dev("positions", positions, torch.int32)
+    b = positions.numel()
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must be [B, Hkv, ctx_cap, D] of equal shape")
+    d = k_cache.shape[3]
+    if tuple(k_cache.shape[:2]) != (b, n_kv_heads):
+        raise ValueError(f"cache shape {tuple(k_cache.shape)} does not match B={b}, Hkv={n_kv_heads}")
+    if q.numel() != b * n_heads * d or k.numel() != b * n_kv_heads * d or v.numel() != b * n_kv_heads * d:
+        raise ValueError("q must be [B, Hq * D] and k, v [B, Hkv * D]")
+    ctx_cap = k_cache.shape[2]
+    if out is None:
+        out = torch.empty(b, n_heads * d, dtype=BF16, device=q.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != b * n_heads * d:
+        raise ValueError(f"out must hold {b}x{n_heads * d} elements")
+    lib = _lib.load()
+    nbytes = lib.t2i_decode_attention_workspace_bytes(b, n_heads, n_kv_heads, ctx_cap)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("attn", b, n_kv_heads, ctx_cap), nbytes, q.device)
+    rc = lib.t2i_decode_attention_prepared(q.data_ptr(), k.data_ptr(), v.data_ptr(), positions.data_ptr(), b,
+                                           n_heads, n_kv_heads, d, k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap,
+                                           out.data_ptr(), _lib.ptr(ws), nbytes, _lib.stream_handle(q.device))
+    _lib.check(rc, "t2i_decode_attention_prepared")
+    return out
+
+
+def rmsnorm_rope(x: torch.Tensor, weight: torch.Tensor, angles: torch.Tensor, eps: float,
+                 rope_style: int = ROPE_HALVES, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-row weighted RMSNorm then RoPE: ``x`` bf16 ``[rows, cols]``, ``weight``
+    ``[cols]``, ``angles`` ``[angle_rows, cols]`` (cos even / sin odd); row r takes
+    angle row ``r // (rows // angle_rows)``.  ``out`` may be ``x``."""
+    for n, t in (("x", x), ("weight", weight), ("angles", angles)):
+        _check_dev(n, t, BF16)
+    cols = weight.numel()
+    if x.numel() % cols or angles.numel() % cols:
+        raise ValueError("x and angles must hold whole rows of len(weight) values")
+    rows, angle_rows = x.numel() // cols, angles.numel() // cols
+    if out is None:
+        out = torch.empty_like(x)
+    _check_dev("out", out, BF16)
+    if out.numel() != x.numel():
+        raise ValueError("out must match x")
+    lib = _lib.load()
+    rc = lib.t2i_rmsnorm_rope(x.data_ptr(), rows, cols, weight.data_ptr(), angles.data_ptr(), angle_rows,
+                              float(eps), int(rope_style), out.data_ptr(), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_rmsnorm_rope")
+    return out
+
+
+def silu_mul(left: torch.Tensor, right: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``bf16(bf16(silu(left)) * right)`` elementwise (bf16 tensors of equal size)."""
+    _check_dev("left", left, BF16)
+    _check_dev("right", right, BF16)
+    if left.numel() != right.numel():
+        raise ValueError("left and right must hold the same number of values")
+    if out is None:
+        out = torch.empty_like(left)
+    _check_dev("out", out, BF16)
+    if out.numel() != left.numel():
+        raise ValueError("out must match left")
+    lib = _lib.load()
+    rc = lib.t2i_silu_mul(left.data_ptr(), right.data_ptr(), left.numel(), out.data_ptr(),
+                          _lib.stream_handle(left.device))
+    _lib.check(rc, "t2i_silu_mul")
+    return out
+
+
+def residual_add_rmsnorm(x: torch.Tensor, update: torch.Tensor, weight: torch.Tensor, eps: float,
+                         x_out: torch.Tensor | None = None, out: torch.Tensor | None = None):
+    """``x_out = bf16(x + update)`` and ``out = rmsnorm(x_out) * weight`` over rows of
+    ``len(weight)`` (``x_out`` may be ``x``).  Returns ``(x_out, out)``."""
+    for n, t in (("x", x), ("update", update), ("weight", weight)):
+        _check_dev(n, t, BF16)
+    h = weight.numel()
+    if x.numel() % h or update.numel() != x.numel():
+        raise ValueError("x and update must be whole rows of len(weight) values, of equal size")
+    m = x.numel() // h
+    x_out = torch.empty_like(x) if x_out is None else x_out
+    out = torch.empty_like(x) if out is None else out
+    for n, t in (("x_out", x_out), ("out", out)):
+        _check_dev(n, t, BF16)
+        if t.numel() != x.numel():
+            raise ValueError(f"{n} must match x")
+    lib = _lib.load()
+    rc = lib.t2i_residual_add_rmsnorm(x.data_ptr(), update.data_ptr(), m, h, weight.data_ptr(), float(eps),
+                                      x_out.data_ptr(), out.data_ptr(), _lib.stream_handle(x.device))
+    _lib.check(rc, "t2i_residual_add_rmsnorm")
+    return x_out, out
+
+
 def qkv_attention(x: torch.Tensor, norm_weight: torch.Tensor | None, eps: float, w_qkv: W4A16Weight,
                   positions: torch.Tensor, n_heads: int, n_kv_heads: int, q_norm: torch.Tensor, k_norm: torch.Tensor,
                   rope: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
@@ -335,6 +433,17 @@ def qkv_attention_errors(b: int, n_heads: int, n_kv_heads: int, device, workspac
     nbytes = lib.t2i_qkv_attention_workspace_bytes(b, n_heads, n_kv_heads)
     ws = (workspace or DEFAULT_WORKSPACE).get(("qkv_attn", b, n_heads, n_kv_heads), nbytes, device)
     return int(ws[off:off + 4].view(torch.int32).item())
+
+
+def clear_qkv_attention_errors(b: int, n_heads: int, n_kv_heads: int, device,
+                               workspace: Workspace | None = None) -> None:
+    """Zero the fused launch's error word (a fill kernel on torch's current
+    stream), so that later launches wait normally again."""
+    lib = _lib.load()
+    off = lib.t2i_qkv_attention_error_offset(b, n_heads, n_kv_heads)
+    nbytes = lib.t2i_qkv_attention_workspace_bytes(b, n_heads, n_kv_heads)
+    ws = (workspace or DEFAULT_WORKSPACE).get(("qkv_attn", b, n_heads, n_kv_heads), nbytes, device)
+    ws[off:off + 4].zero_()
 
 
 class DecodeLayerTable:
@@ -444,6 +553,13 @@ def decode_step_errors(table: DecodeLayerTable, device, workspace: Workspace | N
     out).  Synchronises with the device."""
     ws, off = _step_region(table, 4, device, workspace)
     return int(ws[off:off + 4].view(torch.int32).item())
+
+
+def clear_decode_step_errors(table: DecodeLayerTable, device, workspace: Workspace | None = None) -> None:
+    """Zero the one-launch step's error word (a fill kernel on torch's current
+    stream), so that later launches wait normally again."""
+    ws, off = _step_region(table, 4, device, workspace)
+    ws[off:off + 4].zero_()
 
 
 def decode_step_intermediates(table: DecodeLayerTable, device, workspace: Workspace | None = None) -> dict:
