@@ -469,10 +469,10 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         "by_streams": {str(k): v for k, v in runs.items()},
         "step_kernels": {"position": prompt_len + new_tokens // 2, "by_kernel": per_kernel,
                          "sum_ms_per_step": round(kernel_sum_ms, 4),
-                         "method": "each kernel's launches of one step in a graph of their own (28 launches; a "
-                                   "per-step kernel 28 times), HBM-cold (a 512 MB read between replays), HIP "
-                                   "events per replay on the launch stream, no host wait between replays; wall "
-                                   "time per launch"},
+                         "method": "each kernel's launches of 5 steps in a graph of their own (140 launches, "
+                                   "each round on its own weight copies; a per-step kernel 140 times), HBM-cold "
+                                   "(a 512 MB read between replays), HIP events per replay on the launch stream, "
+                                   "no host wait between replays; wall time per launch"},
         "teacher_forced_prompt": teacher_forced,
         "one_launch_step": one_launch,
         "greedy_parity": oracle,
@@ -483,11 +483,11 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     return out, tensors, prompt
 
 
-def time_step_kernels(model, dev, reps: int, pos: int) -> dict:
+def time_step_kernels(model, dev, reps: int, pos: int, passes: int = 5) -> dict:
     """Each kernel of the batch-decode step on its own, outside any profiler: per
-    kernel a graph of its launches in one step (28 per layer kernel, one for the
-    per-step ones) over the model's own weights and caches at position ``pos`` for
-    every sequence, replayed ``reps`` times; a read of a 512 MB pool between
+    kernel a graph of its launches in ``passes`` steps (28 per layer kernel and
+    step, a per-step kernel as often) over the model's own weights and caches at
+    position ``pos`` for every sequence, replayed ``reps`` times; a read of a 512 MB pool between
     replays (untimed) leaves the MALL without any of the step's bytes, as the
     1.6 GB step itself does, so every replay reads HBM.  HIP events bracket each
     replay on the stream the kernels run on.  Returns microseconds per launch
@@ -506,20 +506,34 @@ def time_step_kernels(model, dev, reps: int, pos: int) -> dict:
     tokens = model.tokens.clone()
     kv_bytes = b * c.n_kv_heads * (pos + 1) * c.head_dim * 2 * 2
     qkv_n, hq = c.qkv_dim, c.n_heads * c.head_dim
+    # ``passes`` rounds over the layers per graph, so that a graph's own start is
+    # spread over about as many launches as the step's graph has (143).  Each round
+    # reads its own copy of the linear weights (the 28 layers' qkv weights alone,
+    # 61 MB, would stay in the 256 MB MALL from one round to the next); the KV
+    # caches (1.2 GB) and the 311 MB lm_head table leave it anyway.
+    from torch2iron_amd.formats import W4A16Weight
+
+    def copies(get):
+        return [[get(L.w) if r == 0 else W4A16Weight(get(L.w).qweight.clone(), get(L.w).qzeros.clone(),
+                                                      get(L.w).scales.clone()) for L in model.layers]
+                for r in range(passes)]
+
+    wq, wo = copies(lambda w: w.qkv), copies(lambda w: w.o)
+    wgu, wd = copies(lambda w: w.gate_up), copies(lambda w: w.down)
     per_layer = [
-        ("rmsnorm_qkv", lambda i, L: ops.rmsnorm_linear(buf.x, L.w.ln1, c.eps, L.w.qkv, out=buf.qkv),
+        ("rmsnorm_qkv", lambda r, i, L: ops.rmsnorm_linear(buf.x, L.w.ln1, c.eps, wq[r][i], out=buf.qkv),
          algorithmic_bytes(b, c.hidden, qkv_n) + c.hidden * 2),
-        ("attention", lambda i, L: ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, L.w.q_norm,
-                                                        L.w.k_norm, c.eps, model.rope, model.k_cache[i],
-                                                        model.v_cache[i], rope_style=L.rope_style, out=buf.ctx,
-                                                        workspace=buf.workspace),
+        ("attention", lambda r, i, L: ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, L.w.q_norm,
+                                                           L.w.k_norm, c.eps, model.rope, model.k_cache[i],
+                                                           model.v_cache[i], rope_style=L.rope_style, out=buf.ctx,
+                                                           workspace=buf.workspace),
          kv_bytes + b * qkv_n * 2 + b * c.n_kv_heads * c.head_dim * 2 * 2 + b * hq * 2),
-        ("o_proj_residual", lambda i, L: ops.linear(buf.ctx, L.w.o, residual=buf.x, out=buf.x),
+        ("o_proj_residual", lambda r, i, L: ops.linear(buf.ctx, wo[r][i], residual=buf.x, out=buf.x),
          algorithmic_bytes(b, hq, c.hidden) + b * c.hidden * 2),
-        ("rmsnorm_gate_up_swiglu", lambda i, L: ops.rmsnorm_gate_up(buf.x, L.w.ln2, c.eps, L.w.gate_up, swiglu=True,
-                                                                    out=buf.hmlp),
+        ("rmsnorm_gate_up_swiglu", lambda r, i, L: ops.rmsnorm_gate_up(buf.x, L.w.ln2, c.eps, wgu[r][i],
+                                                                       swiglu=True, out=buf.hmlp),
          algorithmic_bytes(b, c.hidden, 2 * c.intermediate) - b * c.intermediate * 2 + c.hidden * 2),
-        ("down_residual", lambda i, L: ops.linear(buf.hmlp, L.w.down, residual=buf.x, out=buf.x),
+        ("down_residual", lambda r, i, L: ops.linear(buf.hmlp, wd[r][i], residual=buf.x, out=buf.x),
          algorithmic_bytes(b, c.intermediate, c.hidden) + b * c.hidden * 2),
     ]
     per_step = [
@@ -532,11 +546,11 @@ def time_step_kernels(model, dev, reps: int, pos: int) -> dict:
          b * 8 + b * 4 * 3),
     ]
     out = {}
-    n = len(model.layers)
+    n = len(model.layers) * passes
     # a per-step kernel is launched n times in its graph too, so that every graph
     # spreads its own start over the same number of launches
-    jobs = [(name, [lambda i=i, L=L, f=f: f(i, L) for i, L in enumerate(model.layers)], 1, nb)
-            for name, f, nb in per_layer]
+    jobs = [(name, [lambda r=r, i=i, L=L, f=f: f(r, i, L) for r in range(passes) for i, L in enumerate(model.layers)],
+             passes, nb) for name, f, nb in per_layer]
     jobs += [(name, [f] * n, n, nb) for name, f, nb in per_step]
     jobs.append(("graph_floor_one_element_fill", [lambda: sink[:1].fill_(0)] * n, n, 0))
     stream = torch.cuda.current_stream(dev)
