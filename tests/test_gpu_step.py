@@ -221,3 +221,40 @@ def test_error_word_set_by_the_host_gives_up_then_clears(gpu, form):
     m.check_errors()
     assert torch.equal(m.x, fresh.x)
     assert torch.equal(m.k_cache, fresh.k_cache) and torch.equal(m.v_cache, fresh.v_cache)
+
+
+@pytest.mark.parametrize("form", ["persistent", "fused"])
+def test_one_launch_forms_match_the_oracle(gpu, form):
+    """The one-launch forms held to the oracle directly, with the bars of the
+    separate-kernel path (``test_gpu_decode.test_greedy_decode_small_model_matches_oracle``):
+    4 layers, batch 8, 32 greedy steps; every token that differs from the fp32
+    oracle (and from the bf16-mode oracle) sits at a near-tie, and along the fp32
+    oracle's tokens the logits sit no farther from fp32 than the bf16-mode
+    oracle's, within 25 %."""
+    from oracle import qwen3 as oq
+    from test_gpu_decode import assert_logit_noise_like_bf16_oracle, assert_near_tie, oracle_cfg
+    print(f"one-launch form {form} against the oracle", flush=True)
+    cfg = gm.Qwen3Config(n_layers=4, vocab=8192)
+    t = gm.random_qwen3_tensors(cfg, seed=21, weights="centered")
+    b, plen, new = 8, 24, 32
+    prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(22))
+    kw = dict(persistent=True) if form == "persistent" else dict(fused=True, persistent=False)
+    m = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=64, device=gpu, **kw)
+    assert (m.step_table is not None) if form == "persistent" else m.layers[0].fused
+    got = m.generate(prompt, new)
+    m.check_errors()
+    o16 = oq.DenseQwen3(t, oracle_cfg(cfg), mode="bf16", ctx_cap=64)
+    o32 = oq.DenseQwen3(t, oracle_cfg(cfg), mode="fp32", ctx_cap=64)
+    ref32, margins32 = o32.generate(prompt, new, return_margins=True)
+    ref16, margins16 = o16.generate(prompt, new, return_margins=True)
+    exact = int((got == ref32).all(dim=1).sum())
+    print(f"{form}: {exact}/{b} sequences equal to the fp32 oracle on all {new} steps", flush=True)
+    for ref, margins, name in ((ref32, margins32, "fp32"), (ref16, margins16, "bf16")):
+        for i in range(b):
+            diff = (got[i] != ref[i]).nonzero()
+            if len(diff):
+                s = int(diff[0])
+                assert_near_tie(o16, o32, prompt[i:i + 1], ref[i:i + 1, :s], margins[i, s],
+                                f"{name} oracle, sequence {i} step {s}")
+    assert_logit_noise_like_bf16_oracle(m, o16, o32, prompt, ref32[:, :new - 1], "decode")
+    m.check_errors()

@@ -486,6 +486,15 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
   __syncthreads();
   if (!s_last) return;
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  // The merger's state addresses are computed from the arrival count's outcome
+  // (dep is 1 here, through an asm the compiler cannot see into), so neither the
+  // compiler nor the hardware can issue a state load before thread 0's fetch_add
+  // has returned and the barrier has passed its result on: the order holds by data
+  // dependence, whatever a compiler does with relaxed loads and fences.
+  int dep = s_last;
+  asm volatile("" : "+v"(dep));
+  const float* part_ml = p.part_ml + (dep - 1);
+  const float* part_o = p.part_o + (dep - 1);
   for (int idx = tid; idx < Q * D; idx += ATT_THREADS) {
     const int j = idx / D, d = idx - j * D;
     float M = -INFINITY, lsum = 0.0f, o = 0.0f;
@@ -495,9 +504,9 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 #pragma unroll
       for (int u = 0; u < 8; ++u) {   // unconditional loads (clamped), as above
         const size_t st = (size_t)bh * p.splits + min(s0 + u, p.splits - 1);
-        ms[u] = ld_agent(p.part_ml + (st * Q + j) * 2);
-        ls[u] = ld_agent(p.part_ml + (st * Q + j) * 2 + 1);
-        os[u] = ld_agent(p.part_o + (st * Q + j) * D + d);
+        ms[u] = ld_agent(part_ml + (st * Q + j) * 2);
+        ls[u] = ld_agent(part_ml + (st * Q + j) * 2 + 1);
+        os[u] = ld_agent(part_o + (st * Q + j) * D + d);
       }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
