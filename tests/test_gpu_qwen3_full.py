@@ -4,9 +4,15 @@ lm_head), batch 16, 512-token prompts, 32 greedy tokens.
 
 The fp32 oracle's tokens, top-2 margins and bf16 logit noise come from
 ``tests/golden/qwen3_0.6b_greedy.npz`` (written by ``make_qwen3_greedy_golden.py``
-from the same seeds), so the 28-layer fp32 model does not run here.  Both weight
+from the same seeds), so the 28-layer fp32 model does not run here.  Three weight
 draws are checked: ``uniform`` (the benchmark's draw, which collapses onto a couple
-of tokens, so every token must match) and ``centered`` (diverse tokens).
+of tokens, so every token must match), ``centered`` (diverse tokens, chaotic under
+bf16 rounding) and ``hubs`` (diverse tokens -- 2 to 32 distinct per sequence over 32
+steps, median 10 -- with 326 of 512 steps clear of near-ties: the bf16-mode oracle
+keeps 8 of 16 sequences on all 32 steps; the GPU, which rounds at the same points
+with its own fp32 summation order, must keep at least one fewer, every divergence
+must be a near-tie, and teacher-forced it must match every one of the 326 clear
+steps).
 
 Bars, per sequence, against the fp32 oracle (the reference runtime's default dtype):
 * the sequences that match all 32 tokens are counted and reported, and must reach
@@ -45,9 +51,11 @@ from torch2iron_amd import model as gm
 
 pytestmark = pytest.mark.gpu
 FIXTURE = Path(__file__).resolve().parent / "golden" / "qwen3_0.6b_greedy.npz"
-DRAWS = {"uniform": 0, "centered": 1}
-# sequences (of 16) that must match the fp32 oracle on all 32 steps
-EXACT_FLOOR = {"uniform": 16, "centered": 0}
+DRAWS = {"uniform": 0, "centered": 1, "hubs": 1}
+# sequences (of 16) that must match the fp32 oracle on all 32 steps; None: the
+# bf16-mode oracle's own count less one (which near-ties flip is chance; at the
+# first run the GPU kept 7 and the bf16-mode oracle 8)
+EXACT_FLOOR = {"uniform": 16, "centered": 0, "hubs": None}
 
 
 @pytest.fixture(scope="module")
@@ -82,8 +90,14 @@ def test_full_model_greedy_matches_oracle(gpu, golden, draw):
         if s < new:
             assert margins[i, s] <= 2.0 * noise[i, s], \
                 f"sequence {i} step {s}: margin {margins[i, s]:.3f} > 2 x bf16 noise {noise[i, s]:.3f}"
-    assert exact >= EXACT_FLOOR[draw], f"{exact} < {EXACT_FLOOR[draw]} sequences match all {new} steps"
     t16 = golden[f"{draw}_tokens16"]
+    exact16 = int((t16 == ref).all(axis=1).sum())
+    floor = exact16 - 1 if EXACT_FLOOR[draw] is None else EXACT_FLOOR[draw]
+    distinct = [len(np.unique(r)) for r in ref]
+    print(f"{draw}: {exact}/{b} sequences exact (bf16-mode oracle {exact16}/{b}; floor {floor}); distinct tokens "
+          f"per sequence min {min(distinct)} median {int(np.median(distinct))}", flush=True)
+    assert exact >= floor, f"{exact} < {floor} sequences match all {new} steps"
+
     prefix16 = sum(int(np.argmin(t16[i] == ref[i])) if (t16[i] != ref[i]).any() else new for i in range(b))
     print(f"{draw}: {sum(steps_matched)} steps matched before the first divergence (bf16-mode oracle {prefix16})",
           flush=True)

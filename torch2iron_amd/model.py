@@ -90,9 +90,26 @@ def random_qwen3_tensors(cfg: Qwen3Config, seed: int = 0, embed_std: float = 1.0
     vacuous.
     RMSNorm weights U[0.9, 1.1] (bf16 values).  Embedding (also the tied
     lm_head) N(0, embed_std) rounded to bf16.
+    ``weights="hubs"``: the centred linears with an embedding of N(0, 12) rows
+    scaled by exp(0.3 N(0, 1)) each (a few large-norm rows), final-norm weights of
+    random sign, and q/k norm weights scaled by 0.1 (near-uniform attention): the
+    draw whose greedy tokens are both diverse and least disturbed by bf16 rounding
+    among those searched for the full-model parity test.
     """
-    if weights not in ("uniform", "centered"):
-        raise ValueError("weights must be 'uniform' or 'centered'")
+    if weights not in ("uniform", "centered", "hubs"):
+        raise ValueError("weights must be 'uniform', 'centered' or 'hubs'")
+    if weights == "hubs":
+        t = random_qwen3_tensors(cfg, seed=seed, embed_std=12.0, weights="centered")
+        r = np.exp(0.3 * np.random.default_rng(seed + 2000).standard_normal(cfg.vocab)).astype(np.float32)
+        emb = t["model.embed_tokens.weight"] * r[:, None]
+        t["model.embed_tokens.weight"] = torch.from_numpy(emb).to(BF16).float().numpy()
+        sign = np.where(np.random.default_rng(seed + 1000).random(cfg.hidden) < 0.5, -1.0, 1.0).astype(np.float32)
+        t["model.norm.weight"] = t["model.norm.weight"] * sign
+        for i in range(cfg.n_layers):
+            for nm in ("q_norm", "k_norm"):
+                k = f"model.layers.{i}.self_attn.{nm}.weight"
+                t[k] = torch.from_numpy(t[k] * 0.1).to(BF16).float().numpy()
+        return t
     rng = np.random.default_rng(seed)
     g = cfg.group_size
     t = {}
@@ -494,7 +511,7 @@ class Qwen3Model:
         c = self.cfg
         b, t = prompt.shape
         pf = self._prefill_buffers(t)
-        toks = prompt.reshape(-1).to(torch.int32).to(self.device)
+        toks = prompt.reshape(-1).to(device=self.device, dtype=torch.int32)   # no copy for a device int32 prompt
         ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"])
         # Over prompt-sized batches the norms run as their own pass: the prompt GEMM
         # has no fused-norm form, and the decode kernel's would redo each row's sum
@@ -597,7 +614,9 @@ class Qwen3Model:
             raise ValueError(f"prompt {plen} + {new_tokens} tokens exceed the cache capacity {self.ctx_cap}")
         if int(prompt.min()) < 0 or int(prompt.max()) >= self.cfg.vocab:
             raise ValueError("prompt token id out of range")
-        self.reset()
+        # The KV cache is not cleared: attention reads only slots 0 .. position of a
+        # sequence, and the prompt pass (or the decode step, for the current slot)
+        # writes every one of them before it is read.
         # One prompt buffer per prompt shape: the captured prompt-bookkeeping graph
         # reads it by address (and its length), so a new shape needs a new capture
         # and a new prompt of the same shape only new contents.
@@ -621,11 +640,10 @@ class Qwen3Model:
             self.tokens.copy_(self.prompt[:, 0])
             self.positions.zero_()
             self.step.zero_()
-            self.reset()
             torch.cuda.synchronize(self.device)
         ev[0].record()
         if prompt_mode == "prefill":
-            self.prefill(prompt)
+            self.prefill(self.prompt)      # the device copy: no host transfer inside the pass
         elif use_graph:
             for _ in range(plen - 1):
                 self._replay("prompt")
