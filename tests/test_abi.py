@@ -183,3 +183,38 @@ def test_split_batch_covers_rows():
             sizes = [b1 - b0 for b0, b1 in r]
             assert min(sizes) >= 1 and max(sizes) - min(sizes) <= 1
             assert len(r) == min(parts, batch)
+
+
+def test_runlist_entry_points_validate():
+    """The reference runlist's standalone operators and the prepared attention
+    reject bad arguments on the host before any launch."""
+    lib = _lib.load()
+    rr = lib.t2i_rmsnorm_rope
+    assert rr(None, 256, 128, FAKE, FAKE, 16, 1e-5, 0, FAKE, None) == _lib.T2I_ERR_NULL
+    assert rr(FAKE, 256, 127, FAKE, FAKE, 16, 1e-5, 0, FAKE, None) == _lib.T2I_ERR_SHAPE      # odd cols
+    assert rr(FAKE, 256, 2048, FAKE, FAKE, 16, 1e-5, 0, FAKE, None) == _lib.T2I_ERR_SHAPE     # > 1024
+    assert rr(FAKE, 256, 128, FAKE, FAKE, 12, 1e-5, 0, FAKE, None) == _lib.T2I_ERR_SHAPE      # 12 does not divide 256
+    assert rr(FAKE, 256, 128, FAKE, FAKE, 16, 1e-5, 2, FAKE, None) == _lib.T2I_ERR_VALUE
+    assert rr(FAKE, 256, 128, FAKE, FAKE, 16, 0.0, 0, FAKE, None) == _lib.T2I_ERR_VALUE
+    sm = lib.t2i_silu_mul
+    assert sm(FAKE, None, 3072, FAKE, None) == _lib.T2I_ERR_NULL
+    assert sm(FAKE, FAKE, 3070, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert sm(FAKE, MISALIGNED, 3072, FAKE, None) == _lib.T2I_ERR_ALIGN
+    ra = lib.t2i_residual_add_rmsnorm
+    assert ra(FAKE, FAKE, 8, 1024, FAKE, 1e-5, FAKE, None, None) == _lib.T2I_ERR_NULL
+    assert ra(FAKE, FAKE, 8, 1020, FAKE, 1e-5, FAKE, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert ra(FAKE, FAKE, 0, 1024, FAKE, 1e-5, FAKE, FAKE, None) == _lib.T2I_ERR_SHAPE
+    assert ra(FAKE, FAKE, 8, 1024, FAKE, -1.0, FAKE, FAKE, None) == _lib.T2I_ERR_VALUE
+    assert ra(FAKE, MISALIGNED, 8, 1024, FAKE, 1e-5, FAKE, FAKE, None) == _lib.T2I_ERR_ALIGN
+    pa = lib.t2i_decode_attention_prepared
+    args = [FAKE, FAKE, FAKE, FAKE, 16, 16, 8, 128, FAKE, FAKE, 640, FAKE, FAKE, 1 << 20, None]
+    a = list(args); a[1] = None
+    assert pa(*a) == _lib.T2I_ERR_NULL
+    a = list(args); a[7] = 64
+    assert pa(*a) == _lib.T2I_ERR_SHAPE                          # head_dim 64
+    a = list(args); a[5] = 12
+    assert pa(*a) == _lib.T2I_ERR_SHAPE                          # 12 q heads over 8 kv heads
+    a = list(args); a[2] = MISALIGNED
+    assert pa(*a) == _lib.T2I_ERR_ALIGN
+    a = list(args); a[12] = None
+    assert pa(*a) == _lib.T2I_ERR_WORKSPACE                      # split context needs the workspace
