@@ -176,12 +176,10 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 
   // ---- 1. loads that do not need the position go out with it ----
   // The raw q/k/v rows of this kv head and the norm weights are loaded while
-  // the position is (a scalar load, waited for on its own counter).  Loading
-  // the chunk's K / V rows here too, clamped to the cache capacity, was
-  // measured slower (0.927 against 0.919 ms per decode step), and so was the
-  // same with the RoPE row through scalar loads, so that its wait does not
-  // cover the K / V rows (10.5 -> 11.0 us a call, 0.848 -> 0.864 ms a step): the
-  // stream is bandwidth-bound once every workgroup runs.  Every load is
+  // the position is (a scalar load, waited for on its own counter), and so are
+  // the chunk's first two passes of K / V rows (below).  The RoPE row through
+  // scalar loads, so that its wait does not cover the K / V rows, measured
+  // slower (10.5 -> 11.0 us a call, 0.848 -> 0.864 ms a step).  Every load is
   // unconditional (clamped indices, results selected after the load): a load
   // under a lane-divergent condition whose other side writes the same registers
   // makes the compiler wait for all loads in flight there.
@@ -214,6 +212,22 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
       pg0[n] = pg1[n] = 1.0f;
     }
   }
+  // The chunk's first two passes of K / V rows (slots t0 + grp and t0 + 16 + grp,
+  // clamped into the cache) go out before the position is known: every chunk that
+  // holds a valid slot starts at a valid slot, so they are wasted only for chunks
+  // wholly past the position (32 slots each).  Measured at batch 16, 577 of 640
+  // slots, HBM-cold: 11.50 -> 11.08 us a call (one pass: 11.30; three: 11.31; four:
+  // 11.48; all eight, reading past the chunk's end: 12.44), decode step 0.829 ->
+  // 0.813 ms.  Scoring masks every slot at or past the chunk's end, and the current
+  // slot's row is patched from LDS below, so these rows are used as loaded.
+  u32x4 kreg[ROWS], vreg[ROWS];
+  constexpr int SPEC = ROWS < 2 ? ROWS : 2;
+#pragma unroll
+  for (int it = 0; it < SPEC; ++it) {
+    const int ts = min(t0 + it * 16 + grp, p.ctx_cap - 1);
+    kreg[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)ts * D + 8 * c));
+    vreg[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)ts * D + 8 * c));
+  }
   __builtin_amdgcn_sched_barrier(0);   // keep these loads ahead of everything that needs pos
 
   // a position outside the cache attends to nothing and writes nothing (zero output)
@@ -228,12 +242,12 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
     const float cs = PREP ? bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane]) : 1.0f;
     const float sn = PREP ? bf16_to_f32(p.rope[(size_t)pos * D + 2 * lane + 1]) : 0.0f;
     __builtin_amdgcn_sched_barrier(0);   // the RoPE row ahead of the K / V rows
-    // slots past the chunk's end reload its first slot; masked when scored.  The
-    // K/V stream is read once per step: non-temporal loads (measured 12.8 -> 12.1 us
-    // per call at batch 16, context 577, decode step 889 -> 870 us with the lm_head's)
-    u32x4 kreg[ROWS], vreg[ROWS];
+    // the remaining passes: slots past the chunk's end reload its first slot; masked
+    // when scored.  The K/V stream is read once per step: non-temporal loads
+    // (measured 12.8 -> 12.1 us per call at batch 16, context 577, decode step 889 ->
+    // 870 us with the lm_head's)
 #pragma unroll
-    for (int it = 0; it < ROWS; ++it) {
+    for (int it = SPEC; it < ROWS; ++it) {
       const int t = t0 + it * 16 + grp;
       const int tl = t < t1 ? t : t0;
       kreg[it] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)tl * D + 8 * c));
