@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 4
+#define T2I_ABI_VERSION 5
 #define T2I_MAX_ROWS (65535 * 16)   /* rows of one linear call: 16-row tiles in grid.z */
 
 #define T2I_OK 0
@@ -338,6 +338,49 @@ int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0,
                             int32_t Hq, int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm,
                             float eps, const uint16_t* rope, int32_t rope_style, uint16_t* q_out,
                             uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Row group sums handed from the kernel that writes a prompt GEMM's input to the
+ * GEMM.  The prompt GEMM's zero-point term needs, for every row and 128-wide k
+ * group, the sum of the row's bf16 values over the group; given them, it skips
+ * the all-ones products that otherwise form them (a third of its matrix-core
+ * work).  Sums are fp32 [rows][K / 128] (sum_parts = 1), or two sums per group
+ * over its 64-wide halves, [rows][K / 64] (sum_parts = 2); every pointer to sums
+ * is 4-byte aligned.  The outputs are those of the plain entry points up to fp32
+ * rounding of the sums.  No counterpart in the reference (its NPU kernels apply
+ * the zero point per weight): they serve the prompt pass only.
+ *
+ * t2i_rmsnorm_sums: t2i_rmsnorm (no argmax keys) that also writes y_sums, the
+ *   group sums of y; H % 128 == 0.
+ * t2i_prefill_attention_sums: t2i_prefill_attention that also writes out_sums
+ *   [B * T, Hq], each head's sum of its bf16 context values (one group of the
+ *   o_proj's k when D = 128).
+ * t2i_w4a16_linear_sums / t2i_w4a16_gate_up_sums / t2i_prefill_qkv_rope_kv_sums:
+ *   the plain entry points, taking x_sums (ignored below the prompt GEMM's rows).
+ *   gate_up_sums also takes x_sums = NULL (the GEMM then forms them); with
+ *   swiglu != 0 it also writes y_sums (may be NULL), the half-group
+ *   sums of h, [M][N / 128] (sum_parts = 2 for the down projection); it needs the
+ *   prompt GEMM (M >= 512, N % 128 == 0) and fails otherwise.
+ */
+int t2i_rmsnorm_sums(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
+                     const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y, float* y_sums,
+                     void* stream);
+int t2i_prefill_attention_sums(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
+                               int32_t D, const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap,
+                               uint16_t* out, float* out_sums, void* stream);
+int t2i_w4a16_linear_sums(const uint16_t* x, const float* x_sums, int32_t sum_parts, int32_t M,
+                          const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales, int32_t K,
+                          int32_t N, int32_t group_size, const uint16_t* residual, uint16_t* y, void* stream);
+int t2i_w4a16_gate_up_sums(const uint16_t* x, const float* x_sums, int32_t sum_parts, int32_t M,
+                           const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales, int32_t K,
+                           int32_t N, int32_t group_size, int32_t swiglu, uint16_t* y0, uint16_t* y1,
+                           float* y_sums, void* stream);
+int t2i_prefill_qkv_rope_kv_sums(const uint16_t* x, const float* x_sums, int32_t B, int32_t T, int32_t p0,
+                                 const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                 int32_t K, int32_t group_size, int32_t Hq, int32_t Hkv, int32_t D,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, float eps, const uint16_t* rope,
+                                 int32_t rope_style, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                                 int32_t ctx_cap, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Tied bf16 lm_head with a fused greedy argmax.

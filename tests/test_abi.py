@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.t2i_abi_version() == 4
+    assert lib.t2i_abi_version() == 5
     assert lib.t2i_strerror(-2) == b"unsupported shape"
 
 
@@ -69,6 +69,39 @@ def test_fused_norm_entry_points_validate():
     g = lib.t2i_w4a16_rmsnorm_gate_up
     assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, None, None) == _lib.T2I_ERR_NULL
     assert g(FAKE, 16, FAKE, 1e-6, FAKE, FAKE, FAKE, 1024, 6144, 64, 1, FAKE, None, None) == _lib.T2I_ERR_GROUP
+
+
+def test_row_sum_entry_points_validate():
+    """The *_sums entry points reject bad sums arguments before launching anything."""
+    lib = _lib.load()
+    E = _lib
+    # sums pointers: NULL where required, misaligned
+    assert lib.t2i_w4a16_linear_sums(FAKE, None, 1, 600, FAKE, FAKE, FAKE, 1024, 4096, 128, None, FAKE,
+                                     None) == E.T2I_ERR_NULL
+    assert lib.t2i_w4a16_linear_sums(FAKE, FAKE + 2, 1, 600, FAKE, FAKE, FAKE, 1024, 4096, 128, None, FAKE,
+                                     None) == E.T2I_ERR_ALIGN
+    assert lib.t2i_w4a16_linear_sums(FAKE, FAKE, 3, 600, FAKE, FAKE, FAKE, 1024, 4096, 128, None, FAKE,
+                                     None) == E.T2I_ERR_VALUE
+    # y_sums needs the prompt GEMM (M >= 512) and the SwiGLU epilogue
+    assert lib.t2i_w4a16_gate_up_sums(FAKE, None, 1, 16, FAKE, FAKE, FAKE, 1024, 6144, 128, 1, FAKE, None, FAKE,
+                                      None) == E.T2I_ERR_SHAPE
+    assert lib.t2i_w4a16_gate_up_sums(FAKE, None, 1, 600, FAKE, FAKE, FAKE, 1024, 6144, 128, 0, FAKE, FAKE, FAKE,
+                                      None) == E.T2I_ERR_VALUE
+    # RMSNorm sums: H a multiple of 128, sums required
+    assert lib.t2i_rmsnorm_sums(FAKE, None, 0, 600, 1000, FAKE, 1e-6, None, FAKE, FAKE, None) == E.T2I_ERR_SHAPE
+    assert lib.t2i_rmsnorm_sums(FAKE, None, 0, 600, 1024, FAKE, 1e-6, None, FAKE, None, None) == E.T2I_ERR_NULL
+    assert lib.t2i_prefill_attention_sums(FAKE, 2, 100, 0, 16, 8, 128, FAKE, FAKE, 128, FAKE, None,
+                                          None) == E.T2I_ERR_NULL
+    assert lib.t2i_prefill_attention_sums(FAKE, 2, 100, 0, 16, 8, 128, FAKE, FAKE, 128, FAKE, FAKE + 2,
+                                          None) == E.T2I_ERR_ALIGN
+    qkv = [FAKE, FAKE, 4, 160, 0, FAKE, FAKE, FAKE, 1024, 128, 16, 8, 128, FAKE, FAKE, 1e-6, FAKE, 0, FAKE, FAKE,
+           FAKE, 192, None]
+    a = list(qkv); a[1] = None
+    assert lib.t2i_prefill_qkv_rope_kv_sums(*a) == E.T2I_ERR_NULL
+    a = list(qkv); a[1] = FAKE + 2
+    assert lib.t2i_prefill_qkv_rope_kv_sums(*a) == E.T2I_ERR_ALIGN
+    a = list(qkv); a[3] = 100                                    # B*T = 400 < 512
+    assert lib.t2i_prefill_qkv_rope_kv_sums(*a) == E.T2I_ERR_SHAPE
 
 
 def test_prefill_entry_points_validate():

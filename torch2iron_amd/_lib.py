@@ -72,6 +72,19 @@ SIGNATURES = {
     "t2i_prefill_qkv_rope_kv": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
                                           c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_float, c_void_p,
                                           c_int32, c_void_p, c_void_p, c_void_p, c_int32, c_void_p]),
+    "t2i_rmsnorm_sums": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_float, c_void_p,
+                                   c_void_p, c_void_p, c_void_p]),
+    "t2i_prefill_attention_sums": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                             c_void_p, c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_w4a16_linear_sums": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int32,
+                                        c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_w4a16_gate_up_sums": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                         c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                         c_void_p]),
+    "t2i_prefill_qkv_rope_kv_sums": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                               c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p,
+                                               c_void_p, c_float, c_void_p, c_int32, c_void_p, c_void_p, c_void_p,
+                                               c_int32, c_void_p]),
     "t2i_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
     "t2i_rmsnorm_lm_head_argmax": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_int32, c_int32,
                                              c_void_p, c_void_p, c_void_p]),

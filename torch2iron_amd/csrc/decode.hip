@@ -27,10 +27,13 @@ namespace t2i {
 constexpr int NORM_THREADS = 256;
 constexpr int NORM_MAX_CHUNKS = 4;   // 16-byte chunks per thread: H <= 8192
 
+// gsum (may be NULL): fp32 sums of each output row's bf16 values over each
+// 128-wide group, [rows][H / 128] (H a multiple of 128): sixteen lanes hold one
+// group, each sums its 8 values in order, then a 16-lane DPP sum.
 __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ tokens, int V, int H,
     const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ x_out,
-    uint16_t* __restrict__ y, unsigned long long* __restrict__ keys) {
+    uint16_t* __restrict__ y, unsigned long long* __restrict__ keys, float* __restrict__ gsum) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   int src_row = row;
@@ -73,14 +76,21 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
       const uint32_t a[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
       const uint32_t b[4] = {g.x, g.y, g.z, g.w};
       uint32_t o[4];
+      float gs = 0.0f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float lo = round_bf16(round_bf16(bf16_lo(a[j]) * inv) * bf16_lo(b[j]));
         const float hi = round_bf16(round_bf16(bf16_hi(a[j]) * inv) * bf16_hi(b[j]));
         o[j] = pack_bf16x2(lo, hi);
+        gs += lo;
+        gs += hi;
       }
       *reinterpret_cast<u32x4*>(y + (size_t)row * H + ch * 8) = u32x4{o[0], o[1], o[2], o[3]};
       if (x_out) *reinterpret_cast<u32x4*>(x_out + (size_t)row * H + ch * 8) = v[i];
+      if (gsum) {
+        gs = row_sum16(gs);
+        if ((ch & 15) == 0) gsum[(size_t)row * (H >> 7) + (ch >> 4)] = gs;
+      }
     }
   }
   if (keys && tid == 0) keys[row] = 0ull;
@@ -906,10 +916,12 @@ hipError_t launch_attention_plan(const AttnParams& p, int Q, int rows, dim3 grid
 
 }  // namespace
 
-extern "C" int t2i_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
-                           const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y,
-                           uint64_t* argmax_keys, void* stream) {
+namespace {
+int run_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H, const uint16_t* weight,
+                float eps, uint16_t* x_out, uint16_t* y, uint64_t* argmax_keys, float* y_sums, void* stream) {
   if (!x || !weight || !y) return fail(T2I_ERR_NULL, "x, weight and y must not be NULL");
+  if (y_sums && H % 128) return fail(T2I_ERR_SHAPE, "H=%d must be a multiple of 128 with y_sums", H);
+  if (y_sums && ((uintptr_t)y_sums & 3u)) return fail(T2I_ERR_ALIGN, "y_sums must be 4-byte aligned");
   if (tokens && !x_out) return fail(T2I_ERR_NULL, "x_out is required with tokens");
   if (tokens && V < 1) return fail(T2I_ERR_SHAPE, "V=%d must be positive with tokens", V);
   if (M < 1) return fail(T2I_ERR_SHAPE, "M=%d must be positive", M);
@@ -919,8 +931,23 @@ extern "C" int t2i_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, 
   if (!aligned16(x) || !aligned16(weight) || !aligned16(y) || (x_out && !aligned16(x_out)))
     return fail(T2I_ERR_ALIGN, "rmsnorm pointers must be 16-byte aligned");
   hipLaunchKernelGGL(t2i::rmsnorm_kernel, dim3(M), dim3(NORM_THREADS), 0, reinterpret_cast<hipStream_t>(stream),
-                     x, tokens, V, H, weight, eps, x_out, y, reinterpret_cast<unsigned long long*>(argmax_keys));
+                     x, tokens, V, H, weight, eps, x_out, y, reinterpret_cast<unsigned long long*>(argmax_keys),
+                     y_sums);
   return t2i_host::hip_status(hipGetLastError(), "rmsnorm launch");
+}
+}  // namespace
+
+extern "C" int t2i_rmsnorm(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
+                           const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y,
+                           uint64_t* argmax_keys, void* stream) {
+  return run_rmsnorm(x, tokens, V, M, H, weight, eps, x_out, y, argmax_keys, nullptr, stream);
+}
+
+extern "C" int t2i_rmsnorm_sums(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,
+                                const uint16_t* weight, float eps, uint16_t* x_out, uint16_t* y, float* y_sums,
+                                void* stream) {
+  if (!y_sums) return fail(T2I_ERR_NULL, "y_sums must not be NULL");
+  return run_rmsnorm(x, tokens, V, M, H, weight, eps, x_out, y, nullptr, y_sums, stream);
 }
 
 extern "C" size_t t2i_decode_attention_workspace_bytes(int32_t B, int32_t Hq, int32_t Hkv, int32_t ctx_cap) {

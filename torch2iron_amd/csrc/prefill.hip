@@ -101,6 +101,7 @@ struct PrefillAttnParams {
   const uint16_t* kc;     // [B, Hkv, cap, D]
   const uint16_t* vc;
   uint16_t* out;          // [B*T, Hq * D]
+  float* out_sums;        // NULL, or [B*T, Hq]: each head's sum of its bf16 context values
   int B, T, Hq, Hkv, cap, p0;
   float scale_log2;       // D^-1/2 * log2(e)
 };
@@ -323,8 +324,18 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const Prefill
       const int head = h * Q + j / BQ;
       uint16_t* dst = p.out + ((size_t)b * p.T + t) * p.Hq * D + (size_t)head * D;
       const float inv = l[mi][i] > 0.0f ? 1.0f / l[mi][i] : 0.0f;
+      float hs = 0.0f;
 #pragma unroll
-      for (int n = 0; n < 8; ++n) dst[n * 16 + c] = (uint16_t)f32_to_bf16(o[mi][n][i] * inv);
+      for (int n = 0; n < 8; ++n) {
+        const uint32_t v = f32_to_bf16(o[mi][n][i] * inv);
+        dst[n * 16 + c] = (uint16_t)v;
+        hs += __uint_as_float(v << 16);
+      }
+      if (p.out_sums) {
+        // the head's 128 values are one quantisation group of the next product's k
+        hs = row_sum16(hs);
+        if (c == 0) p.out_sums[((size_t)b * p.T + t) * p.Hq + head] = hs;
+      }
     }
 }
 
@@ -355,10 +366,12 @@ extern "C" int t2i_prefill_qk_rope_kv(const uint16_t* qkv, int32_t B, int32_t T,
   return t2i_host::hip_status(hipGetLastError(), "prefill prep launch");
 }
 
-extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
-                                     int32_t D, const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap,
-                                     uint16_t* out, void* stream) {
+namespace {
+int run_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv, int32_t D,
+                          const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap, uint16_t* out,
+                          float* out_sums, void* stream) {
   if (!q || !k_cache || !v_cache || !out) return fail(T2I_ERR_NULL, "prefill attention pointers must not be NULL");
+  if (out_sums && ((uintptr_t)out_sums & 3u)) return fail(T2I_ERR_ALIGN, "out_sums must be 4-byte aligned");
   if (D != t2i::PF_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
   if (B < 1 || T < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv) return fail(T2I_ERR_SHAPE, "B=%d T=%d Hq=%d Hkv=%d invalid", B, T, Hq, Hkv);
   const int Q = Hq / Hkv;
@@ -369,7 +382,7 @@ extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, in
   if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
     return fail(T2I_ERR_ALIGN, "prefill attention tensors must be 16-byte aligned");
   t2i::PrefillAttnParams p{};
-  p.q = q; p.kc = k_cache; p.vc = v_cache; p.out = out;
+  p.q = q; p.kc = k_cache; p.vc = v_cache; p.out = out; p.out_sums = out_sums;
   p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.cap = ctx_cap; p.p0 = p0;
   p.scale_log2 = (float)(1.4426950408889634 / sqrt((double)D));
   const int bq = t2i::PF_ROWS / Q;
@@ -382,4 +395,18 @@ extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, in
     default: hipLaunchKernelGGL((t2i::prefill_attention_kernel<8>), grid, dim3(256), 0, s, p); break;
   }
   return t2i_host::hip_status(hipGetLastError(), "prefill attention launch");
+}
+}  // namespace
+
+extern "C" int t2i_prefill_attention(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq, int32_t Hkv,
+                                     int32_t D, const uint16_t* k_cache, const uint16_t* v_cache, int32_t ctx_cap,
+                                     uint16_t* out, void* stream) {
+  return run_prefill_attention(q, B, T, p0, Hq, Hkv, D, k_cache, v_cache, ctx_cap, out, nullptr, stream);
+}
+
+extern "C" int t2i_prefill_attention_sums(const uint16_t* q, int32_t B, int32_t T, int32_t p0, int32_t Hq,
+                                          int32_t Hkv, int32_t D, const uint16_t* k_cache, const uint16_t* v_cache,
+                                          int32_t ctx_cap, uint16_t* out, float* out_sums, void* stream) {
+  if (!out_sums) return fail(T2I_ERR_NULL, "out_sums must not be NULL");
+  return run_prefill_attention(q, B, T, p0, Hq, Hkv, D, k_cache, v_cache, ctx_cap, out, out_sums, stream);
 }

@@ -78,8 +78,14 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
 //     the packed weights as the k-tile's 16 qweight rows in pairs (one 1 KB load
 //     per pair, 128 bytes of padding between pairs: the four rows of a fragment
 //     read meet two-way bank conflicts at most).
-//   * Arithmetic as the decode kernel: MFMA over bf16(128 + q), an all-ones MFMA
-//     for the row sums, per group and column total += scale * (dot + zb * rowsum).
+//   * Arithmetic as the decode kernel: MFMA over bf16(128 + q), per group and
+//     column total += scale * (dot + zb * rowsum).  The row sums come either from
+//     an all-ones MFMA per row fragment (XSP = 0: a third of the matrix-core work,
+//     since every wave sums all 64 rows), or precomputed by the kernel that wrote
+//     x (XSP = 1: one fp32 sum a row and group; XSP = 2: two half-group sums),
+//     loaded into LDS with the k-tile (16 of 48 MFMAs a wave per k-tile go): at
+//     8192 rows qkv 110 -> 104 us, o_proj 55.7 -> 53.1 us, gate_up with SwiGLU
+//     152 -> 144 us, down 77.4 -> 76.8 us (same box, interleaved rounds).
 // ============================================================================
 constexpr int GM_BM = 64, GM_BN = 128;
 constexpr int GM_WAVES = 4;
@@ -106,6 +112,7 @@ struct GemmStage {
   uint32_t b[GM_BPAIR * GM_BPAIR_W];
   uint32_t qs[64];          // fp16 scales of the tile's 128 columns, two per word
   uint32_t qz[64];          // qzeros words of the tile's columns (16 used)
+  float xs[2 * GM_BM];      // precomputed row sums of the k-tile (XSP > 0): part u of row i at 64 u + i
 };
 static_assert(GM_WAVES * GM_EP_WAVE * 2 <= (int)sizeof(GemmStage) * GM_STAGES, "epilogue fits in the stages");
 
@@ -151,9 +158,17 @@ __device__ __forceinline__ void wait_vm() {
 
 // k-tile kt into stage st (rows past M reload row M - 1; their outputs are never
 // stored).  Each wave loads its A fragments and weight row pairs; wave 0 also the
-// scale and zero words.
+// scale and zero words, wave 1 the precomputed row sums (XSP > 0).
+template <int XSP>
 __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0, int kt, int wave, int lane,
                                            GemmStage& st) {
+  if constexpr (XSP > 0) {
+    if (wave == 1) {
+      const float* src = p.xs + (size_t)min(m0 + lane, p.M - 1) * p.ldxs + kt * XSP;
+#pragma unroll
+      for (int u = 0; u < XSP; ++u) lds_dma4(src + u, &st.xs[GM_BM * u]);
+    }
+  }
   const int c = lane & 15, r = lane >> 4;
 #pragma unroll
   for (int i = 0; i < GM_AF_W; ++i) {
@@ -211,8 +226,8 @@ __device__ __forceinline__ void wait_lds(GemmFrags& f) {
 }
 
 // k-step KS of a k-tile: read k-step KS + 1's fragments into nxt, then compute
-// KS from cur (read one k-step earlier).
-template <int KS>
+// KS from cur (read one k-step earlier).  OWN: the row sums by all-ones MFMAs.
+template <int KS, bool OWN>
 __device__ __forceinline__ void gemm_kstep(uint32_t abase, uint32_t bbase, GemmFrags& cur, GemmFrags& nxt,
                                            uint32_t magic, f32x4 (&P)[GM_MF][GM_NJ], f32x4 (&xs)[GM_MF]) {
   if constexpr (KS + 1 < KSG) {
@@ -228,13 +243,14 @@ __device__ __forceinline__ void gemm_kstep(uint32_t abase, uint32_t bbase, GemmF
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi) {
     const bf16x8 a = __builtin_bit_cast(bf16x8, cur.a[mi]);
-    xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
+    if constexpr (OWN) xs[mi] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, ones, xs[mi], 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < GM_NJ; ++j) P[mi][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b[j], P[mi][j], 0, 0, 0);
   }
-  if constexpr (KS + 1 < KSG) gemm_kstep<KS + 1>(abase, bbase, nxt, cur, magic, P, xs);
+  if constexpr (KS + 1 < KSG) gemm_kstep<KS + 1, OWN>(abase, bbase, nxt, cur, magic, P, xs);
 }
 
+template <int XSP>
 __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wn, int lane, int ncol0,
                                              f32x4 (&total)[GM_MF][GM_NJ]) {
   const uint32_t abase = lds_addr(&st.a[0]) + 16 * lane;
@@ -251,18 +267,48 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wn, int la
   uint32_t sw[GM_NJ], zw[GM_NJ];
   sw[0] = lds_read4<0>(sbase);  zw[0] = lds_read4<0>(zbase);
   sw[1] = lds_read4<32>(sbase); zw[1] = lds_read4<8>(zbase);
+  // precomputed row sums: rows 16 mi + 4 r .. + 3 of part u lie together at 64 u + 16 mi + 4 r
+  f32x4 xs[GM_MF], xs2[GM_MF];
+  if constexpr (XSP > 0) {
+    const uint32_t xbase = lds_addr(&st.xs[0]) + 16 * (lane >> 4);
+    xs[0] = __builtin_bit_cast(f32x4, lds_read16<0>(xbase));
+    xs[1] = __builtin_bit_cast(f32x4, lds_read16<64>(xbase));
+    xs[2] = __builtin_bit_cast(f32x4, lds_read16<128>(xbase));
+    xs[3] = __builtin_bit_cast(f32x4, lds_read16<192>(xbase));
+    if constexpr (XSP == 2) {
+      xs2[0] = __builtin_bit_cast(f32x4, lds_read16<256>(xbase));
+      xs2[1] = __builtin_bit_cast(f32x4, lds_read16<320>(xbase));
+      xs2[2] = __builtin_bit_cast(f32x4, lds_read16<384>(xbase));
+      xs2[3] = __builtin_bit_cast(f32x4, lds_read16<448>(xbase));
+    }
+  }
+  static_assert(GM_MF == 4, "four row fragments of precomputed sums");
   const uint32_t magic = magic_vgpr();
-  f32x4 P[GM_MF][GM_NJ], xs[GM_MF];
+  f32x4 P[GM_MF][GM_NJ];
 #pragma unroll
   for (int mi = 0; mi < GM_MF; ++mi) {
-    xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (XSP == 0) xs[mi] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < GM_NJ; ++j) P[mi][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   GemmFrags f0, f1;
   gemm_read<0>(abase, bbase, f0);
-  gemm_kstep<0>(abase, bbase, f0, f1, magic, P, xs);
-  // the scale and zero reads were issued first: done with the last wait
+  gemm_kstep<0, XSP == 0>(abase, bbase, f0, f1, magic, P, xs);
+  // The scale, zero and row-sum reads were issued first: done with the last wait,
+  // which the empty asm orders before their uses.
+  asm volatile("" : "+v"(sw[0]), "+v"(sw[1]), "+v"(zw[0]), "+v"(zw[1]));
+  if constexpr (XSP > 0) {
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi) asm volatile("" : "+v"(xs[mi]));
+  }
+  if constexpr (XSP == 2) {
+#pragma unroll
+    for (int mi = 0; mi < GM_MF; ++mi) {
+      asm volatile("" : "+v"(xs2[mi]));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xs[mi][i] += xs2[mi][i];
+    }
+  }
   const int zshift = (ncol0 & 7) * 4;   // the same for every fragment (16 j keeps the low bits)
   const bool odd = ncol0 & 1;
 #pragma unroll
@@ -276,6 +322,7 @@ __device__ __forceinline__ void gemm_compute(const GemmStage& st, int wn, int la
   }
 }
 
+template <int XSP>
 __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearParams p, const QkvPrepParams pp) {
   __shared__ GemmStage stg[GM_STAGES];
   const int lane = threadIdx.x & 63;
@@ -301,17 +348,17 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
   // wait until this wave's loads of kt + 1 have landed and meet the other waves
   // (then everyone's have).  The last step issues no loads, so nothing is in
   // flight when the epilogue starts.
-  gemm_issue(p, m0, n0, 0, wn, lane, stg[0]);
+  gemm_issue<XSP>(p, m0, n0, 0, wn, lane, stg[0]);
   wait_vm<0>();
   lds_barrier();
   int kt = 0;
   for (; kt + 1 < KT; ++kt) {
-    gemm_issue(p, m0, n0, kt + 1, wn, lane, stg[(kt + 1) & 1]);
-    gemm_compute(stg[kt & 1], wn, lane, ncol0, total);
+    gemm_issue<XSP>(p, m0, n0, kt + 1, wn, lane, stg[(kt + 1) & 1]);
+    gemm_compute<XSP>(stg[kt & 1], wn, lane, ncol0, total);
     wait_vm<0>();
     lds_barrier();
   }
-  gemm_compute(stg[kt & 1], wn, lane, ncol0, total);
+  gemm_compute<XSP>(stg[kt & 1], wn, lane, ncol0, total);
   lds_barrier();   // every wave is done reading the stages: they become the epilogue's tiles
 
   // ---- epilogue: total[mi][j][i] is row 16 mi + 4 r + i, column 32 wn + 16 j + c
@@ -427,6 +474,27 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
         const int m = m0 + row;
         const u32x4 v = *reinterpret_cast<const u32x4*>(ep + reg * GM_BM * GM_EP_LD + row * GM_EP_LD + 8 * ch);
         if (m < p.M) *reinterpret_cast<u32x4*>(dst + (size_t)m * p.ldy + (ncolw >> 1) + 8 * ch) = v;
+      }
+    }
+    if (p.epi == EPI_SWIGLU && p.ys) {
+      // The tile's 64 output columns are one half group of the next product's k:
+      // wave 0 sums each row (lane = row) over the four waves' regions in a fixed
+      // order, for that product's row sums.
+      __syncthreads();   // every wave's region is written
+      if (wn == 0) {
+        const uint16_t* base = reinterpret_cast<const uint16_t*>(&stg[0]) + lane * GM_EP_LD;
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < GM_WAVES; ++w) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(base + w * GM_EP_WAVE + 8 * h);
+            s += (bf16_lo(v.x) + bf16_hi(v.x)) + (bf16_lo(v.y) + bf16_hi(v.y)) + (bf16_lo(v.z) + bf16_hi(v.z)) +
+                 (bf16_lo(v.w) + bf16_hi(v.w));
+          }
+        }
+        const int m = m0 + lane;
+        if (m < p.M) p.ys[(size_t)m * p.ldys + (n0 >> 7)] = s;
       }
     }
   }
@@ -637,6 +705,15 @@ hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, h
   return hipErrorInvalidValue;
 }
 
+// The prompt GEMM over p's rows, with its own row sums or p.xs in p.xs_parts parts.
+hipError_t launch_gemm(const LinearParams& p, const QkvPrepParams& pp, hipStream_t s) {
+  const unsigned tiles = (unsigned)((p.M + GM_BM - 1) / GM_BM) * (unsigned)(p.N / GM_BN);
+  if (!p.xs) hipLaunchKernelGGL(w4a16_gemm_kernel<0>, dim3(tiles), dim3(GM_THREADS), 0, s, p, pp);
+  else if (p.xs_parts == 1) hipLaunchKernelGGL(w4a16_gemm_kernel<1>, dim3(tiles), dim3(GM_THREADS), 0, s, p, pp);
+  else hipLaunchKernelGGL(w4a16_gemm_kernel<2>, dim3(tiles), dim3(GM_THREADS), 0, s, p, pp);
+  return hipGetLastError();
+}
+
 // Rows from which the LDS-tiled GEMM replaces the 16-row-tile kernel.
 int gemm_min_rows() {
 #ifdef T2I_TUNING
@@ -657,11 +734,19 @@ int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
 }
 
 // gamma != NULL: the fused-norm variant (x is normalised with gamma, eps first).
+// xs / xs_parts: x's precomputed row sums (may be NULL: the prompt GEMM forms its
+// own; other kernels never need them); ys: the SwiGLU output's half-group sums
+// (prompt GEMM only; may be NULL).
 int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float eps, const int32_t* qweight,
                const int32_t* qzeros, const uint16_t* scales, int K, int N, int group_size,
-               const uint16_t* residual, uint16_t* y0, uint16_t* y1, void* stream) {
+               const uint16_t* residual, uint16_t* y0, uint16_t* y1, void* stream, const float* xs = nullptr,
+               int xs_parts = 1, float* ys = nullptr) {
   int rc = check_weights(qweight, qzeros, scales, K, N, group_size);
   if (rc) return rc;
+  if (xs_parts != 1 && xs_parts != 2) return fail(T2I_ERR_VALUE, "sum_parts must be 1 or 2");
+  if (ys && epi != EPI_SWIGLU) return fail(T2I_ERR_VALUE, "y_sums is only written with swiglu");
+  if ((xs && ((uintptr_t)xs & 3u)) || (ys && ((uintptr_t)ys & 3u)))
+    return fail(T2I_ERR_ALIGN, "row sums must be 4-byte aligned");
   if (!x || !y0) return fail(T2I_ERR_NULL, "x and y must not be NULL");
   if (epi == EPI_PAIRED && !y1) return fail(T2I_ERR_NULL, "y1 must not be NULL when swiglu == 0");
   if (epi == EPI_RESIDUAL && !residual) return fail(T2I_ERR_NULL, "residual must not be NULL");
@@ -688,11 +773,15 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     p.ldx = K;
     p.ldy = paired ? N / 2 : N;
     p.epi = epi;
-    const unsigned tiles = (unsigned)((M + GM_BM - 1) / GM_BM) * (unsigned)(N / GM_BN);
-    hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p,
-                       QkvPrepParams{});
-    return t2i_host::hip_status(hipGetLastError(), "w4a16 gemm launch");
+    p.xs = xs;
+    p.xs_parts = xs_parts;
+    p.ldxs = xs_parts * (K / GS);
+    p.ys = ys;
+    p.ldys = N / GM_BN;
+    return t2i_host::hip_status(launch_gemm(p, QkvPrepParams{}, reinterpret_cast<hipStream_t>(stream)),
+                                "w4a16 gemm launch");
   }
+  if (ys) return fail(T2I_ERR_SHAPE, "y_sums needs the prompt GEMM (M >= %d, N a multiple of %d)", gemm_min_rows(), GM_BN);
   const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr, false);
   LinearParams p{};
   p.x = x;
@@ -716,14 +805,15 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
 
 }  // namespace
 
-extern "C" int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0, const int32_t* qweight,
-                                       const int32_t* qzeros, const uint16_t* scales, int32_t K, int32_t group_size,
-                                       int32_t Hq, int32_t Hkv, int32_t D, const uint16_t* q_norm,
-                                       const uint16_t* k_norm, float eps, const uint16_t* rope, int32_t rope_style,
-                                       uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
-                                       void* stream) {
+namespace {
+int run_prefill_qkv(const uint16_t* x, const float* x_sums, int32_t B, int32_t T, int32_t p0, const int32_t* qweight,
+                    const int32_t* qzeros, const uint16_t* scales, int32_t K, int32_t group_size, int32_t Hq,
+                    int32_t Hkv, int32_t D, const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                    const uint16_t* rope, int32_t rope_style, uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache,
+                    int32_t ctx_cap, void* stream) {
   if (!x || !q_norm || !k_norm || !rope || !q_out || !k_cache || !v_cache)
     return fail(T2I_ERR_NULL, "prefill projection pointers must not be NULL");
+  if (x_sums && ((uintptr_t)x_sums & 3u)) return fail(T2I_ERR_ALIGN, "x_sums must be 4-byte aligned");
   if (D != ATT_D) return fail(T2I_ERR_SHAPE, "head_dim %d unsupported (only 128)", D);
   if (B < 1 || T < 1 || Hkv < 1 || Hq < Hkv || Hq % Hkv || Hq + 2 * Hkv > 0x3FFF)
     return fail(T2I_ERR_SHAPE, "B=%d T=%d Hq=%d Hkv=%d invalid", B, T, Hq, Hkv);
@@ -753,10 +843,32 @@ extern "C" int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, 
   pp.qn = q_norm; pp.kn = k_norm; pp.rope = rope; pp.q = q_out; pp.kc = k_cache; pp.vc = v_cache;
   pp.T = T; pp.Hq = Hq; pp.Hkv = Hkv; pp.cap = ctx_cap; pp.p0 = p0; pp.style = rope_style; pp.eps = eps;
   static_assert(GM_BN == ATT_D, "one prompt-GEMM column tile is one head");
-  const unsigned tiles = (unsigned)((M + GM_BM - 1) / GM_BM) * (unsigned)(N / GM_BN);
-  hipLaunchKernelGGL(w4a16_gemm_kernel, dim3(tiles), dim3(GM_THREADS), 0, reinterpret_cast<hipStream_t>(stream), p,
-                     pp);
-  return t2i_host::hip_status(hipGetLastError(), "prefill projection launch");
+  p.xs = x_sums;
+  p.xs_parts = 1;
+  p.ldxs = K / GS;
+  return t2i_host::hip_status(launch_gemm(p, pp, reinterpret_cast<hipStream_t>(stream)), "prefill projection launch");
+}
+}  // namespace
+
+extern "C" int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0, const int32_t* qweight,
+                                       const int32_t* qzeros, const uint16_t* scales, int32_t K, int32_t group_size,
+                                       int32_t Hq, int32_t Hkv, int32_t D, const uint16_t* q_norm,
+                                       const uint16_t* k_norm, float eps, const uint16_t* rope, int32_t rope_style,
+                                       uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap,
+                                       void* stream) {
+  return run_prefill_qkv(x, nullptr, B, T, p0, qweight, qzeros, scales, K, group_size, Hq, Hkv, D, q_norm, k_norm,
+                         eps, rope, rope_style, q_out, k_cache, v_cache, ctx_cap, stream);
+}
+
+extern "C" int t2i_prefill_qkv_rope_kv_sums(const uint16_t* x, const float* x_sums, int32_t B, int32_t T, int32_t p0,
+                                            const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                            int32_t K, int32_t group_size, int32_t Hq, int32_t Hkv, int32_t D,
+                                            const uint16_t* q_norm, const uint16_t* k_norm, float eps,
+                                            const uint16_t* rope, int32_t rope_style, uint16_t* q_out,
+                                            uint16_t* k_cache, uint16_t* v_cache, int32_t ctx_cap, void* stream) {
+  if (!x_sums) return fail(T2I_ERR_NULL, "x_sums must not be NULL");
+  return run_prefill_qkv(x, x_sums, B, T, p0, qweight, qzeros, scales, K, group_size, Hq, Hkv, D, q_norm, k_norm,
+                         eps, rope, rope_style, q_out, k_cache, v_cache, ctx_cap, stream);
 }
 
 extern "C" int t2i_w4a16_linear(const uint16_t* x, int32_t M, const int32_t* qweight,
@@ -773,6 +885,23 @@ extern "C" int t2i_w4a16_gate_up(const uint16_t* x, int32_t M, const int32_t* qw
                                  uint16_t* y1, void* stream) {
   return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, nullptr, 0.0f, qweight, qzeros, scales, K, N,
                     group_size, nullptr, y0, y1, stream);
+}
+
+extern "C" int t2i_w4a16_linear_sums(const uint16_t* x, const float* x_sums, int32_t sum_parts, int32_t M,
+                                     const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                     int32_t K, int32_t N, int32_t group_size, const uint16_t* residual, uint16_t* y,
+                                     void* stream) {
+  if (!x_sums) return fail(T2I_ERR_NULL, "x_sums must not be NULL");
+  return run_linear(residual ? EPI_RESIDUAL : EPI_STORE, x, M, nullptr, 0.0f, qweight, qzeros, scales, K, N,
+                    group_size, residual, y, nullptr, stream, x_sums, sum_parts);
+}
+
+extern "C" int t2i_w4a16_gate_up_sums(const uint16_t* x, const float* x_sums, int32_t sum_parts, int32_t M,
+                                      const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
+                                      int32_t K, int32_t N, int32_t group_size, int32_t swiglu, uint16_t* y0,
+                                      uint16_t* y1, float* y_sums, void* stream) {
+  return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, nullptr, 0.0f, qweight, qzeros, scales, K, N,
+                    group_size, nullptr, y0, y1, stream, x_sums, sum_parts, y_sums);
 }
 
 extern "C" int t2i_w4a16_rmsnorm_linear(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,

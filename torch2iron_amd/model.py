@@ -498,7 +498,19 @@ class Qwen3Model:
             "h": torch.empty(r, c.intermediate, dtype=BF16, device=dev),
             "last": (torch.arange(self.batch, dtype=torch.int32) * t + (t - 1)).to(dev),
         }
+        if self._prefill_sums(r):
+            # row group sums that each producer hands to the next prompt GEMM
+            self._pf["xn_sums"] = torch.empty(r, c.hidden // 128, dtype=torch.float32, device=dev)
+            self._pf["ctx_sums"] = torch.empty(r, c.n_heads, dtype=torch.float32, device=dev)
+            self._pf["h_sums"] = torch.empty(r, c.intermediate // 64, dtype=torch.float32, device=dev)
         return self._pf
+
+    def _prefill_sums(self, rows: int) -> bool:
+        """Whether the prompt pass hands row group sums to its GEMMs: every GEMM of
+        the pass is the prompt GEMM (rows and widths) and a head is one group."""
+        c = self.cfg
+        return (rows >= ops.PROMPT_GEMM_ROWS and c.head_dim == 128 and c.hidden % 128 == 0
+                and (2 * c.intermediate) % 128 == 0 and (c.n_heads * c.head_dim) % 128 == 0)
 
     def prefill(self, prompt: torch.Tensor, want_logits: bool = False):
         """Consume ``prompt [B, T]`` from position 0 in one pass over all ``B * T`` rows
@@ -512,29 +524,35 @@ class Qwen3Model:
         b, t = prompt.shape
         pf = self._prefill_buffers(t)
         toks = prompt.reshape(-1).to(device=self.device, dtype=torch.int32)   # no copy for a device int32 prompt
-        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"])
+        # Each prompt GEMM's input comes with its row group sums from the kernel that
+        # wrote it (the norm, the attention, the SwiGLU epilogue), so the GEMM does
+        # not form them itself.
+        xs_n, xs_ctx, xs_h = pf.get("xn_sums"), pf.get("ctx_sums"), pf.get("h_sums")
+        ops.rmsnorm(self.embed, self.layers[0].w.ln1, c.eps, out=pf["xn"], tokens=toks, x_out=pf["x"],
+                    out_sums=xs_n)
         # Over prompt-sized batches the norms run as their own pass: the prompt GEMM
         # has no fused-norm form, and the decode kernel's would redo each row's sum
         # of squares once per column block.
         for i, layer in enumerate(self.layers):
             w = layer.w
             if i > 0:
-                ops.rmsnorm(pf["x"], w.ln1, c.eps, out=pf["xn"])
+                ops.rmsnorm(pf["x"], w.ln1, c.eps, out=pf["xn"], out_sums=xs_n)
             if b * t >= ops.PROMPT_GEMM_ROWS:
                 # the projection's epilogue does the q/k norm, RoPE and cache write
                 ops.prefill_qkv_rope_kv(pf["xn"], w.qkv, b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps,
                                         self.rope, self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style,
-                                        q_out=pf["q"])
+                                        q_out=pf["q"], x_sums=xs_n)
             else:
                 ops.linear(pf["xn"], w.qkv, out=pf["qkv"])
                 ops.prefill_qk_rope_kv(pf["qkv"], b, 0, c.n_heads, c.n_kv_heads, w.q_norm, w.k_norm, c.eps,
                                        self.rope, self.k_cache[i], self.v_cache[i], rope_style=layer.rope_style,
                                        q_out=pf["q"])
-            ops.prefill_attention(pf["q"], 0, c.n_kv_heads, self.k_cache[i], self.v_cache[i], out=pf["ctx"])
-            ops.linear(pf["ctx"], w.o, residual=pf["x"], out=pf["x"])
-            ops.rmsnorm(pf["x"], w.ln2, c.eps, out=pf["xn"])
-            ops.gate_up(pf["xn"], w.gate_up, swiglu=True, out=pf["h"])
-            ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"])
+            ops.prefill_attention(pf["q"], 0, c.n_kv_heads, self.k_cache[i], self.v_cache[i], out=pf["ctx"],
+                                  out_sums=xs_ctx)
+            ops.linear(pf["ctx"], w.o, residual=pf["x"], out=pf["x"], x_sums=xs_ctx)
+            ops.rmsnorm(pf["x"], w.ln2, c.eps, out=pf["xn"], out_sums=xs_n)
+            ops.gate_up(pf["xn"], w.gate_up, swiglu=True, out=pf["h"], x_sums=xs_n, out_sums=xs_h)
+            ops.linear(pf["h"], w.down, residual=pf["x"], out=pf["x"], x_sums=xs_h, sum_parts=2)
         # final norm of each sequence's last prompt row, then the tied lm_head + argmax
         ops.rmsnorm(pf["x"], self.norm, c.eps, out=self.xn, tokens=pf["last"], x_out=self.x, argmax_keys=self.keys)
         logits = self._logits_out(want_logits)

@@ -53,6 +53,13 @@ def _check_dev(name: str, t: torch.Tensor, dtype=None):
         raise ValueError(f"{name} must be contiguous")
 
 
+def _check_sums(name: str, t: torch.Tensor, rows: int, per_row: int):
+    """fp32 row group sums ``[rows, per_row]`` (see ``rmsnorm(out_sums=...)``)."""
+    _check_dev(name, t, torch.float32)
+    if t.numel() != rows * per_row:
+        raise ValueError(f"{name} must hold {rows}x{per_row} sums")
+
+
 def _check_weight(w: W4A16Weight):
     if not isinstance(w, W4A16Weight):
         raise ValueError("weight must be a W4A16Weight")
@@ -72,11 +79,15 @@ def dequantize(w: W4A16Weight) -> torch.Tensor:
 
 
 def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
+           out: torch.Tensor | None = None, x_sums: torch.Tensor | None = None,
+           sum_parts: int = 1) -> torch.Tensor:
     """``y = x @ W^T`` (+ residual, rounded as bf16(bf16(x W^T) + residual)).
 
     ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case): M = 1 is the GEMV,
-    M <= 64 a decode batch, more rows a prompt batch.
+    M <= 64 a decode batch, more rows a prompt batch.  ``x_sums``: fp32 sums of
+    each row of ``x`` over each 128-wide k group (``sum_parts=1``, ``[M, K/128]``)
+    or 64-wide half group (``sum_parts=2``, ``[M, K/64]``), as the kernel that
+    wrote ``x`` emits them; the prompt GEMM then skips forming them itself.
     """
     _check_weight(w)
     _check_dev("x", x, BF16)
@@ -95,19 +106,30 @@ def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None
         if residual.numel() != m * w.N:
             raise ValueError(f"residual must hold {m}x{w.N} elements")
     lib = _lib.load()
-    rc = lib.t2i_w4a16_linear(x2.data_ptr(), m, w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(),
-                              w.K, w.N, w.group_size, _lib.ptr(residual), out.data_ptr(),
-                              _lib.stream_handle(x.device))
-    _lib.check(rc, "t2i_w4a16_linear")
+    if x_sums is not None:
+        _check_sums("x_sums", x_sums, m, sum_parts * (w.K // w.group_size))
+        rc = lib.t2i_w4a16_linear_sums(x2.data_ptr(), x_sums.data_ptr(), int(sum_parts), m, w.qweight.data_ptr(),
+                                       w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N, w.group_size,
+                                       _lib.ptr(residual), out.data_ptr(), _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_linear_sums")
+    else:
+        rc = lib.t2i_w4a16_linear(x2.data_ptr(), m, w.qweight.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(),
+                                  w.K, w.N, w.group_size, _lib.ptr(residual), out.data_ptr(),
+                                  _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_linear")
     return out.view(-1) if squeeze else out.view(m, w.N)
 
 
 def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torch.Tensor | None = None,
-            out_up: torch.Tensor | None = None):
+            out_up: torch.Tensor | None = None, x_sums: torch.Tensor | None = None, sum_parts: int = 1,
+            out_sums: torch.Tensor | None = None):
     """Paired gate/up projection over an ``interleave_gate_up`` weight.
 
     ``swiglu=True``: returns ``h = silu(gate) * up`` bf16 ``[M, N/2]``.
     ``swiglu=False``: returns ``(gate, up)``, each ``[M, N/2]``.
+    ``x_sums`` / ``sum_parts`` as ``linear``.  ``out_sums`` (SwiGLU, prompt rows
+    only): fp32 ``[M, N/128]`` receives each row of ``h`` summed over its 64-wide
+    half groups, the down projection's ``x_sums`` with ``sum_parts=2``.
     """
     _check_weight(w_pair)
     _check_dev("x", x, BF16)
@@ -127,10 +149,21 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
         if out_up.numel() != m * inter:
             raise ValueError(f"out_up must hold {m}x{inter} elements")
     lib = _lib.load()
-    rc = lib.t2i_w4a16_gate_up(x2.data_ptr(), m, w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
-                               w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)),
-                               out.data_ptr(), _lib.ptr(out_up), _lib.stream_handle(x.device))
-    _lib.check(rc, "t2i_w4a16_gate_up")
+    if x_sums is not None or out_sums is not None:
+        if x_sums is not None:
+            _check_sums("x_sums", x_sums, m, sum_parts * (w_pair.K // w_pair.group_size))
+        if out_sums is not None:
+            _check_sums("out_sums", out_sums, m, w_pair.N // 128)
+        rc = lib.t2i_w4a16_gate_up_sums(x2.data_ptr(), _lib.ptr(x_sums), int(sum_parts), m,
+                                        w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(), w_pair.scales.data_ptr(),
+                                        w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)), out.data_ptr(),
+                                        _lib.ptr(out_up), _lib.ptr(out_sums), _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_gate_up_sums")
+    else:
+        rc = lib.t2i_w4a16_gate_up(x2.data_ptr(), m, w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
+                                   w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size,
+                                   int(bool(swiglu)), out.data_ptr(), _lib.ptr(out_up), _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_gate_up")
     return out if swiglu else (out, out_up)
 
 
@@ -192,11 +225,13 @@ def rmsnorm_gate_up(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_pa
 
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
             tokens: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
-            argmax_keys: torch.Tensor | None = None) -> torch.Tensor:
+            argmax_keys: torch.Tensor | None = None, out_sums: torch.Tensor | None = None) -> torch.Tensor:
     """Weighted RMSNorm of the rows of ``x`` (bf16 rounding as the reference's bf16 path).
 
     With ``tokens`` (int32 ``[M]``), ``x`` is an embedding table ``[V, H]`` and
-    the gathered rows are also written to ``x_out``.
+    the gathered rows are also written to ``x_out``.  ``out_sums`` (fp32
+    ``[M, H/128]``, not with ``argmax_keys``): each output row's sums over its
+    128-wide groups, for a prompt GEMM that takes the output as ``x``.
     """
     _check_dev("x", x, BF16)
     _check_dev("weight", weight, BF16)
@@ -226,6 +261,15 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor
         if argmax_keys.numel() < m:
             raise ValueError(f"argmax_keys must hold at least {m} entries")
     lib = _lib.load()
+    if out_sums is not None:
+        if argmax_keys is not None:
+            raise ValueError("out_sums and argmax_keys are not taken together")
+        _check_sums("out_sums", out_sums, m, h // 128)
+        rc = lib.t2i_rmsnorm_sums(x.data_ptr(), _lib.ptr(tokens), x.shape[0] if tokens is not None else 0, m, h,
+                                  weight.data_ptr(), float(eps), _lib.ptr(x_out), out.data_ptr(),
+                                  out_sums.data_ptr(), _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_rmsnorm_sums")
+        return out
     rc = lib.t2i_rmsnorm(x.data_ptr(), _lib.ptr(tokens), x.shape[0] if tokens is not None else 0, m, h,
                          weight.data_ptr(), float(eps), _lib.ptr(x_out),
                          out.data_ptr(), _lib.ptr(argmax_keys), _lib.stream_handle(x.device))
@@ -630,11 +674,12 @@ def prefill_qk_rope_kv(qkv: torch.Tensor, batch: int, p0: int, n_heads: int, n_k
 def prefill_qkv_rope_kv(x: torch.Tensor, w_qkv: W4A16Weight, batch: int, p0: int, n_heads: int, n_kv_heads: int,
                         q_norm: torch.Tensor, k_norm: torch.Tensor, eps: float, rope: torch.Tensor,
                         k_cache: torch.Tensor, v_cache: torch.Tensor, rope_style: int = ROPE_HALVES,
-                        q_out: torch.Tensor | None = None) -> torch.Tensor:
+                        q_out: torch.Tensor | None = None, x_sums: torch.Tensor | None = None) -> torch.Tensor:
     """``prefill_qk_rope_kv(linear(x, w_qkv), ...)`` in one launch, with the same bits:
     the prompt GEMM's epilogue normalises and rotates each q/k head and writes q
     and the caches, and the projection is never stored.  ``x`` bf16 ``[B * T, K]``
-    with ``B * T >= 512`` (the prompt GEMM's rows); returns q bf16 ``[B, Hq, T, D]``."""
+    with ``B * T >= 512`` (the prompt GEMM's rows); returns q bf16 ``[B, Hq, T, D]``.
+    ``x_sums`` as ``linear`` (``sum_parts=1``)."""
     _check_dev("x", x, BF16)
     _check_weight(w_qkv)
     for n, t in (("q_norm", q_norm), ("k_norm", k_norm), ("rope", rope), ("k_cache", k_cache), ("v_cache", v_cache)):
@@ -659,6 +704,17 @@ def prefill_qkv_rope_kv(x: torch.Tensor, w_qkv: W4A16Weight, batch: int, p0: int
     if q_out.numel() != batch * n_heads * t * d:
         raise ValueError("q_out must be [B, Hq, T, D]")
     lib = _lib.load()
+    if x_sums is not None:
+        _check_sums("x_sums", x_sums, x.shape[0], w_qkv.K // w_qkv.group_size)
+        rc = lib.t2i_prefill_qkv_rope_kv_sums(x.data_ptr(), x_sums.data_ptr(), batch, t, p0,
+                                              w_qkv.qweight.data_ptr(), w_qkv.qzeros.data_ptr(),
+                                              w_qkv.scales.data_ptr(), w_qkv.K, w_qkv.group_size, n_heads,
+                                              n_kv_heads, d, q_norm.data_ptr(), k_norm.data_ptr(), float(eps),
+                                              rope.data_ptr(), int(rope_style), q_out.data_ptr(),
+                                              k_cache.data_ptr(), v_cache.data_ptr(), ctx_cap,
+                                              _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_prefill_qkv_rope_kv_sums")
+        return q_out
     rc = lib.t2i_prefill_qkv_rope_kv(x.data_ptr(), batch, t, p0, w_qkv.qweight.data_ptr(), w_qkv.qzeros.data_ptr(),
                                      w_qkv.scales.data_ptr(), w_qkv.K, w_qkv.group_size, n_heads, n_kv_heads, d,
                                      q_norm.data_ptr(), k_norm.data_ptr(), float(eps), rope.data_ptr(),
@@ -669,9 +725,11 @@ def prefill_qkv_rope_kv(x: torch.Tensor, w_qkv: W4A16Weight, batch: int, p0: int
 
 
 def prefill_attention(q: torch.Tensor, p0: int, n_kv_heads: int, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                      out: torch.Tensor | None = None) -> torch.Tensor:
+                      out: torch.Tensor | None = None, out_sums: torch.Tensor | None = None) -> torch.Tensor:
     """Causal GQA attention of prompt rows ``q [B, Hq, T, D]`` (positions p0..p0+T-1)
-    over cache slots ``0..p0+t``; returns bf16 ``[B * T, Hq * D]``."""
+    over cache slots ``0..p0+t``; returns bf16 ``[B * T, Hq * D]``.  ``out_sums``
+    (fp32 ``[B * T, Hq]``) receives each head's sum of its bf16 context values,
+    the o_proj's ``x_sums`` when ``D = 128``."""
     _check_dev("q", q, BF16)
     _check_dev("k_cache", k_cache, BF16)
     _check_dev("v_cache", v_cache, BF16)
@@ -687,6 +745,13 @@ def prefill_attention(q: torch.Tensor, p0: int, n_kv_heads: int, k_cache: torch.
     if out.numel() != b * t * hq * d:
         raise ValueError("out must be [B * T, Hq * D]")
     lib = _lib.load()
+    if out_sums is not None:
+        _check_sums("out_sums", out_sums, b * t, hq)
+        rc = lib.t2i_prefill_attention_sums(q.data_ptr(), b, t, p0, hq, n_kv_heads, d, k_cache.data_ptr(),
+                                            v_cache.data_ptr(), k_cache.shape[2], out.data_ptr(),
+                                            out_sums.data_ptr(), _lib.stream_handle(q.device))
+        _lib.check(rc, "t2i_prefill_attention_sums")
+        return out
     rc = lib.t2i_prefill_attention(q.data_ptr(), b, t, p0, hq, n_kv_heads, d, k_cache.data_ptr(),
                                    v_cache.data_ptr(), k_cache.shape[2], out.data_ptr(),
                                    _lib.stream_handle(q.device))
