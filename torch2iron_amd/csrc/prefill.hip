@@ -90,11 +90,13 @@ __global__ __launch_bounds__(256) void prefill_prep_kernel(const PrefillPrepPara
 // causal GQA flash attention over the cache
 // ============================================================================
 constexpr int PF_ROWS = 64;                 // query rows per workgroup (over the kv head's q heads)
-constexpr int PF_MF = 1;                    // 16-row fragments per wave (4 waves x 16 rows)
 constexpr int PF_KEYS = 64;                 // keys per block
 constexpr int PF_KLD = PF_D + 8;            // K tile row stride (bf16): 272 bytes
-constexpr int PF_VLD = PF_KEYS + 8;         // transposed V tile row stride: 144 bytes
-constexpr int PF_PLD = PF_KEYS + 8;         // P tile row stride
+// Transposed V tile row stride: 136 bytes = 34 banks, so the 16 rows (dims) of an
+// 8-byte A-operand read fall on 16 distinct bank pairs (a 144-byte stride put dims
+// c and c + 8 on one pair, and the staging stores of 16 dims 8 apart on one bank:
+// 69 against 62 us a layer, with 5x the LDS bank conflicts).
+constexpr int PF_VLD = PF_KEYS + 4;
 
 struct PrefillAttnParams {
   const uint16_t* q;      // [B, Hq, T, D]
@@ -106,19 +108,26 @@ struct PrefillAttnParams {
   float scale_log2;       // D^-1/2 * log2(e)
 };
 
-// One workgroup per (sequence b, kv head h, query block); 4 waves of PF_MF
-// 16-row MFMA fragments.  Row j of the PF_ROWS is q head h * Q + j / BQ at
-// prompt row t0 + j % BQ (BQ = PF_ROWS / Q), so the q heads sharing kv head h
-// share every K / V block.  Measured slower at 16 sequences x 512 rows: two
-// fragments a wave (128 rows a workgroup: 141 against 121 us a layer), and P
-// written as 32-bit words of key pairs swapped between neighbouring lanes.
-//   S = Q K^T: A = q rows (registers, 4 k-steps of 32 dims), B = K from LDS;
-//   online softmax per row in fp32 (rows 4r + i of the lane's MFMA output);
-//   O += P V: P goes to A layout through a per-wave LDS tile, B = V^T from LDS.
+// One workgroup per (sequence b, kv head h, query block); 4 waves of 16 query
+// rows.  Row j of the PF_ROWS is q head h * Q + j / BQ at prompt row
+// t0 + j % BQ (BQ = PF_ROWS / Q), so the q heads sharing kv head h share every
+// K / V block.  Everything runs transposed, so that a lane holds one query row:
+//   S^T = K Q^T: A = K from LDS (lane (c, r): key c, dims 8 r ..), B = the
+//     wave's q rows (registers); the output gives lane (c, r) row 16 w + c's
+//     scores for keys 4 r .. 4 r + 3 of each 16-key tile;
+//   online softmax per lane (the row's max and sum over the four lanes of the
+//     row with two exchanges), rescaling the lane's own outputs;
+//   O^T += V^T P^T: B = P^T straight from the softmax registers (a k-step's 32
+//     keys in the order tile 2 ks keys 4 r ..+3, tile 2 ks + 1 keys 4 r ..+3 --
+//     any order works as long as A uses the same), A = V^T from LDS read in that
+//     order; the output gives lane (c, r) row c's dims 16 n + 4 r .. + 3.
+// V is transposed in registers on its way into LDS (four keys x eight dims a
+// thread, byte permutes, 8-byte stores).  Against the untransposed form (S = Q K^T
+// with rows spread over lanes, P through a per-wave LDS tile, V stored as 2-byte
+// pieces): 66.0 -> 47.7 us a layer at 16 sequences x 512 rows (same box).
 template <int Q>
-__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const PrefillAttnParams p) {
+__global__ __launch_bounds__(256, 3) void prefill_attention_kernel(const PrefillAttnParams p) {
   constexpr int D = PF_D;
-  constexpr int MF = PF_MF;
   constexpr int BQ = PF_ROWS / Q;           // prompt rows per q head in the tile
   // Query blocks are dealt last block first (grid.y counts down): the causal
   // work of a block grows with its position, so the longest go out first and
@@ -128,215 +137,169 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(const Prefill
   const int b = blockIdx.x / p.Hkv;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15;
   const int r = lane >> 4;
 
   __shared__ __align__(16) uint16_t s_k[PF_KEYS * PF_KLD];     // [key][dim]
   __shared__ __align__(16) uint16_t s_vt[D * PF_VLD];          // [dim][key]
-  __shared__ __align__(16) uint16_t s_p[4][MF * 16 * PF_PLD];  // per wave [row][key]
 
-  // ---- the wave's query rows as A operands (fragment mi: row c) ----
-  u32x4 qa[MF][4];
+  // ---- this lane's query row j = 16 wave + c, as the B operand (dims 32 ks + 8 r ..) ----
+  const int jrow = wave * 16 + c;
+  const int t_row = t0 + jrow % BQ;
+  const int head = h * Q + jrow / BQ;
+  const int qpos = p.p0 + t_row;             // keys beyond it are masked
+  u32x4 qb[4];
+  {
+    const uint16_t* src = p.q + (((size_t)b * p.Hq + head) * p.T + min(t_row, p.T - 1)) * D + 8 * r;
 #pragma unroll
-  for (int mi = 0; mi < MF; ++mi) {
-    const int jrow = wave * 16 * MF + mi * 16 + c;
-    const int t_a = t0 + jrow % BQ;
-    const int head_a = h * Q + jrow / BQ;
-    const uint16_t* src = p.q + (((size_t)b * p.Hq + head_a) * p.T + min(t_a, p.T - 1)) * D + 8 * r;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) qa[mi][ks] = *reinterpret_cast<const u32x4*>(src + ks * 32);
+    for (int ks = 0; ks < 4; ++ks) qb[ks] = *reinterpret_cast<const u32x4*>(src + ks * 32);
   }
-  // the rows this lane holds in MFMA outputs: 4r + i of each fragment
-  int qpos[MF][4];
-#pragma unroll
-  for (int mi = 0; mi < MF; ++mi)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = wave * 16 * MF + mi * 16 + 4 * r + i;
-      qpos[mi][i] = p.p0 + t0 + j % BQ;        // absolute query position (masks keys beyond it)
-    }
   // the smallest query position of the wave's rows (wave-uniform): rows j0 ..
-  // j0 + 16 MF - 1 of the tile are prompt rows t0 + j % BQ
-  const int j0 = __builtin_amdgcn_readfirstlane(wave) * 16 * MF;
-  const int qmin = p.p0 + t0 + ((j0 % BQ) + 16 * MF <= BQ ? j0 % BQ : 0);
+  // j0 + 15 of the tile are prompt rows t0 + j % BQ
+  const int j0 = wave * 16;
+  const int qmin = p.p0 + t0 + ((j0 % BQ) + 16 <= BQ ? j0 % BQ : 0);
   const int last_t = min(t0 + BQ, p.T) - 1;
   const int kend = p.p0 + last_t + 1;        // keys [0, kend) can be attended
   const size_t cache_base = ((size_t)b * p.Hkv + h) * (size_t)p.cap * D;
 
-  float m[MF][4], l[MF][4];
-  f32x4 o[MF][8];
+  float m = -INFINITY, l = 0.0f;
+  f32x4 o[8];
 #pragma unroll
-  for (int mi = 0; mi < MF; ++mi) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) { m[mi][i] = -INFINITY; l[mi][i] = 0.0f; }
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int n = 0; n < 8; ++n) o[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per thread.
-  // K chunk q: key q / 16, dims 8 (q % 16) (a wave stores 4 whole rows, 16 bytes a
-  // lane).  V chunk q: key q % 64, dims 8 (q / 64): the transposed store then
-  // writes 64 consecutive keys of one dim per instruction (conflict-free), where
-  // the K mapping would put the 16 lanes of a key row 8 rows of s_vt apart, all in
-  // one bank.  Loads are unconditional (keys past kend reload key kend - 1), and
-  // those keys are zeroed when the block is staged, not right after the load: a
-  // select there would make the compiler wait for the load at once, leaving
-  // nothing in flight behind the compute.
+  // K / V block staging: 64 keys x 128 dims each = 1024 chunks of 16 bytes; 4 per
+  // thread.  K chunk q: key q / 16, dims 8 (q % 16), stored as loaded.  V: thread
+  // (key group g = tid % 16, octet o = tid / 16) loads keys 4 g .. 4 g + 3 of dims
+  // 8 o .. 8 o + 7 and stores each dim's four keys as one 8-byte piece of s_vt (16
+  // lanes of a store cover one dim's 64 keys: no bank conflicts).  Loads are
+  // unconditional (keys past kend reload key kend - 1: finite values whose
+  // softmax weights are zero).
+  const int vgrp = tid & 15, voct = tid >> 4;
   auto load_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int q16 = tid + 256 * u;
-      const int kkey = kb * PF_KEYS + (q16 >> 4);
-      const int vkey = kb * PF_KEYS + (q16 & 63);
-      kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)min(kkey, kend - 1) * D + 8 * (q16 & 15));
-      vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)min(vkey, kend - 1) * D + 8 * (q16 >> 6));
+      const int kkey = min(kb * PF_KEYS + (q16 >> 4), kend - 1);
+      const int vkey = min(kb * PF_KEYS + 4 * vgrp + u, kend - 1);
+      kr[u] = *reinterpret_cast<const u32x4*>(p.kc + cache_base + (size_t)kkey * D + 8 * (q16 & 15));
+      vr[u] = *reinterpret_cast<const u32x4*>(p.vc + cache_base + (size_t)vkey * D + 8 * voct);
     }
   };
-  auto store_block = [&](int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
+  auto store_block = [&](u32x4 (&kr)[4], u32x4 (&vr)[4]) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      asm volatile("" : "+v"(kr[u]), "+v"(vr[u]));   // the loads are waited for here, not earlier
       const int q16 = tid + 256 * u;
-      const int kkey = kb * PF_KEYS + (q16 >> 4);
-      const int key = q16 & 63, d0 = 8 * (q16 >> 6);
-      const u32x4 zero4 = u32x4{0u, 0u, 0u, 0u};
-      const u32x4 kv = kkey < kend ? kr[u] : zero4;
-      const u32x4 vv = kb * PF_KEYS + key < kend ? vr[u] : zero4;
-      *reinterpret_cast<u32x4*>(s_k + (q16 >> 4) * PF_KLD + 8 * (q16 & 15)) = kv;
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+      *reinterpret_cast<u32x4*>(s_k + (q16 >> 4) * PF_KLD + 8 * (q16 & 15)) = kr[u];
+    }
+    const uint32_t w0[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w};
+    const uint32_t w1[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+    const uint32_t w2[4] = {vr[2].x, vr[2].y, vr[2].z, vr[2].w};
+    const uint32_t w3[4] = {vr[3].x, vr[3].y, vr[3].z, vr[3].w};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        s_vt[(d0 + 2 * e) * PF_VLD + key] = (uint16_t)(w[e] & 0xFFFFu);
-        s_vt[(d0 + 2 * e + 1) * PF_VLD + key] = (uint16_t)(w[e] >> 16);
-      }
+    for (int e = 0; e < 4; ++e) {
+      // dims 2 e (low halves) and 2 e + 1 (high halves) of keys 4 g .. 4 g + 3
+      const u32x2 lo = u32x2{__builtin_amdgcn_perm(w1[e], w0[e], 0x05040100u), __builtin_amdgcn_perm(w3[e], w2[e], 0x05040100u)};
+      const u32x2 hi = u32x2{__builtin_amdgcn_perm(w1[e], w0[e], 0x07060302u), __builtin_amdgcn_perm(w3[e], w2[e], 0x07060302u)};
+      *reinterpret_cast<u32x2*>(s_vt + (8 * voct + 2 * e) * PF_VLD + 4 * vgrp) = lo;
+      *reinterpret_cast<u32x2*>(s_vt + (8 * voct + 2 * e + 1) * PF_VLD + 4 * vgrp) = hi;
     }
   };
 
   const int nblocks = (kend + PF_KEYS - 1) / PF_KEYS;
-  uint16_t* pt = s_p[wave];
-  // Block kb: stage its K / V (loaded two blocks earlier) in LDS, refill the
-  // register set with block kb + 2, then compute.  Two sets in flight hide the
-  // load latency behind two blocks of compute.  Every load is issued, also past
-  // the last block (clamped: all lanes read key kend - 1), so that the compiler
-  // knows that the other set's loads are in flight behind this set's and waits
-  // for this set only; with the loads under a condition it waits for all.
-  auto step = [&](const int kb, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
+  u32x4 kr[4], vr[4];
+  load_block(0, kr, vr);
+  for (int kb = 0; kb < nblocks; ++kb) {
     __syncthreads();                          // the previous block's tiles are consumed
-    store_block(kb, kr, vr);
+    store_block(kr, vr);
     __syncthreads();
-    load_block(kb + 2, kr, vr);
-    // ---- S = Q K^T for 4 key tiles of 16; each K fragment feeds every row fragment ----
-    f32x4 s[MF][4];
+    if (kb + 1 < nblocks) load_block(kb + 1, kr, vr);
+    // ---- S^T = K Q^T: 4 key tiles of 16 ----
+    f32x4 s[4];
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-#pragma unroll
-      for (int mi = 0; mi < MF; ++mi) s[mi][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+      s[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 kb16 = *reinterpret_cast<const u32x4*>(s_k + (n * 16 + c) * PF_KLD + ks * 32 + 8 * r);
-#pragma unroll
-        for (int mi = 0; mi < MF; ++mi)
-          s[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qa[mi][ks]),
-                                                             __builtin_bit_cast(bf16x8, kb16), s[mi][n], 0, 0, 0);
+        const u32x4 ka = *reinterpret_cast<const u32x4*>(s_k + (n * 16 + c) * PF_KLD + ks * 32 + 8 * r);
+        s[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka),
+                                                       __builtin_bit_cast(bf16x8, qb[ks]), s[n], 0, 0, 0);
       }
     }
-    // ---- online softmax (log2 domain), causal mask; P into the wave's LDS tile ----
-    // Blocks that every row of the wave sees whole skip the mask and its guards.
-    auto softmax = [&](auto mask_tag) {
-      constexpr bool MASK = decltype(mask_tag)::value;
+    // ---- online softmax of the lane's row (log2 domain), causal mask ----
+    // Blocks that every row of the wave sees whole skip the mask.
+    const bool whole = kb * PF_KEYS + PF_KEYS - 1 <= qmin;
+    float mx = -INFINITY;
 #pragma unroll
-      for (int mi = 0; mi < MF; ++mi) {
-        float pv[4][4];   // [i][n]
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float mx = -INFINITY;
-#pragma unroll
-          for (int n = 0; n < 4; ++n) {
-            const int key = kb * PF_KEYS + n * 16 + c;
-            const float v = (!MASK || key <= qpos[mi][i]) ? s[mi][n][i] * p.scale_log2 : -INFINITY;
-            pv[i][n] = v;
-            mx = fmaxf(mx, v);
-          }
-          mx = row_max16(mx);
-          const float mn = fmaxf(m[mi][i], mx);
-          const float f = m[mi][i] > -INFINITY ? __builtin_amdgcn_exp2f(m[mi][i] - mn) : 0.0f;
-          float sum = 0.0f;
-#pragma unroll
-          for (int n = 0; n < 4; ++n) {
-            const float x = round_bf16(__builtin_amdgcn_exp2f(pv[i][n] - mn));
-            const float e = (!MASK || pv[i][n] > -INFINITY) ? x : 0.0f;
-            pv[i][n] = e;
-            sum += e;
-          }
-          sum = row_sum16(sum);
-          l[mi][i] = l[mi][i] * f + sum;
-          m[mi][i] = mn;
-#pragma unroll
-          for (int n = 0; n < 8; ++n) o[mi][n][i] *= f;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int n = 0; n < 4; ++n)
-            pt[(mi * 16 + 4 * r + i) * PF_PLD + n * 16 + c] = (uint16_t)f32_to_bf16(pv[i][n]);
+      for (int i = 0; i < 4; ++i) {
+        const int key = kb * PF_KEYS + n * 16 + 4 * r + i;
+        const float v = (whole || key <= qpos) ? s[n][i] * p.scale_log2 : -INFINITY;
+        s[n][i] = v;
+        mx = fmaxf(mx, v);
       }
-    };
-    if (kb * PF_KEYS + PF_KEYS - 1 <= qmin) softmax(std::false_type{});
-    else softmax(std::true_type{});
-    __builtin_amdgcn_s_waitcnt(0xc07f);       // lgkmcnt(0): the wave's P writes are done
-    __builtin_amdgcn_wave_barrier();
-    // ---- O += P V: 2 k-steps of 32 keys, 8 dim tiles; each V fragment feeds every row fragment ----
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m, mx);           // finite: every row attends key 0
+    const float f = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.0f;
+    float sum = 0.0f;
+    uint32_t pw[4][2];                        // bf16 weights, two keys a word
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      float e[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = round_bf16(__builtin_amdgcn_exp2f(s[n][i] - mn));
+        e[i] = s[n][i] > -INFINITY ? x : 0.0f;
+        sum += e[i];
+      }
+      pw[n][0] = pack_bf16x2(e[0], e[1]);
+      pw[n][1] = pack_bf16x2(e[2], e[3]);
+    }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    l = l * f + sum;
+    m = mn;
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[n][i] *= f;
+    // ---- O^T += V^T P^T: 2 k-steps of 32 keys, 8 dim tiles ----
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      u32x4 pa[MF];
-#pragma unroll
-      for (int mi = 0; mi < MF; ++mi)
-        pa[mi] = *reinterpret_cast<const u32x4*>(pt + (mi * 16 + c) * PF_PLD + ks * 32 + 8 * r);
+      const u32x4 pb = u32x4{pw[2 * ks][0], pw[2 * ks][1], pw[2 * ks + 1][0], pw[2 * ks + 1][1]};
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
-        const u32x4 vb = *reinterpret_cast<const u32x4*>(s_vt + (n * 16 + c) * PF_VLD + ks * 32 + 8 * r);
-#pragma unroll
-        for (int mi = 0; mi < MF; ++mi)
-          o[mi][n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa[mi]),
-                                                             __builtin_bit_cast(bf16x8, vb), o[mi][n], 0, 0, 0);
+        const uint16_t* vrow = s_vt + (n * 16 + c) * PF_VLD + ks * 32 + 4 * r;
+        const u32x2 v0 = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 v1 = *reinterpret_cast<const u32x2*>(vrow + 16);
+        const u32x4 va = u32x4{v0.x, v0.y, v1.x, v1.y};
+        o[n] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, va),
+                                                       __builtin_bit_cast(bf16x8, pb), o[n], 0, 0, 0);
       }
     }
-  };
-  u32x4 kr0[4], vr0[4], kr1[4], vr1[4];
-  load_block(0, kr0, vr0);
-  load_block(1, kr1, vr1);
-  int kb = 0;
-  for (; kb + 1 < nblocks; kb += 2) {
-    step(kb, kr0, vr0);
-    step(kb + 1, kr1, vr1);
   }
-  if (kb < nblocks) step(kb, kr0, vr0);
 
-  // ---- normalise and store: lane holds rows 4r + i, dims n * 16 + c ----
+  // ---- normalise and store: the lane holds row jrow's dims 16 n + 4 r .. + 3 ----
+  if (t_row < p.T) {
+    uint16_t* dst = p.out + ((size_t)b * p.T + t_row) * p.Hq * D + (size_t)head * D + 4 * r;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float hs = 0.0f;
 #pragma unroll
-  for (int mi = 0; mi < MF; ++mi)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = wave * 16 * MF + mi * 16 + 4 * r + i;
-      const int t = t0 + j % BQ;
-      if (t >= p.T) continue;
-      const int head = h * Q + j / BQ;
-      uint16_t* dst = p.out + ((size_t)b * p.T + t) * p.Hq * D + (size_t)head * D;
-      const float inv = l[mi][i] > 0.0f ? 1.0f / l[mi][i] : 0.0f;
-      float hs = 0.0f;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) {
-        const uint32_t v = f32_to_bf16(o[mi][n][i] * inv);
-        dst[n * 16 + c] = (uint16_t)v;
-        hs += __uint_as_float(v << 16);
-      }
-      if (p.out_sums) {
-        // the head's 128 values are one quantisation group of the next product's k
-        hs = row_sum16(hs);
-        if (c == 0) p.out_sums[((size_t)b * p.T + t) * p.Hq + head] = hs;
-      }
+    for (int n = 0; n < 8; ++n) {
+      const float y0 = round_bf16(o[n][0] * inv), y1 = round_bf16(o[n][1] * inv);
+      const float y2 = round_bf16(o[n][2] * inv), y3 = round_bf16(o[n][3] * inv);
+      *reinterpret_cast<u32x2*>(dst + n * 16) = u32x2{pack_bf16x2(y0, y1), pack_bf16x2(y2, y3)};
+      hs += ((y0 + y1) + (y2 + y3));
     }
+    if (p.out_sums) {
+      // the head's 128 values are one quantisation group of the next product's k
+      hs += __shfl_xor(hs, 16, 64);
+      hs += __shfl_xor(hs, 32, 64);
+      if (r == 0) p.out_sums[((size_t)b * p.T + t_row) * p.Hq + head] = hs;
+    }
+  }
 }
 
 }  // namespace t2i
