@@ -414,9 +414,22 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         }
         log(f"decode ({model.n_streams} streams): {runs[s]['decode_tokens_per_s']} tok/s, {step_ms:.3f} ms/step; "
             f"prefill {tm['prompt_ms']:.2f} ms; end to end {runs[s]['end_to_end_tokens_per_s']} tok/s")
+    # The prompt pass on its own, five passes back to back (no host wait between
+    # them), event-timed.  prompt_ms above times one pass inside generate, started
+    # from a GPU that was idle while the host prepared it (clocks still rising).
+    model.set_streams(1)
+    model.prefill(model.prompt)
+    torch.cuda.synchronize(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        model.prefill(model.prompt)
+    e1.record()
+    torch.cuda.synchronize(dev)
+    prefill_steady_ms = e0.elapsed_time(e1) / 5
+    log(f"prefill, five passes back to back: {prefill_steady_ms:.2f} ms a pass")
     # each kernel of the step alone, event-timed outside any profiler, at position 576
     # (the middle of the timed steps' 512..638)
-    model.set_streams(1)
     log("decode step kernels, each alone (graphs of its launches in one step, HBM-cold, events)")
     per_kernel = time_step_kernels(model, dev, max(steps, 10), prompt_len + new_tokens // 2)
     kernel_sum_ms = sum(v["us_per_step"] for v in per_kernel.values() if isinstance(v, dict)) / 1e3
@@ -466,6 +479,8 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         "workload": f"random-init Qwen3-0.6B (28 layers, W4A16 g128, bf16 tied lm_head), batch {batch}, "
                     f"prompt {prompt_len} (one prefill pass), {new_tokens} new tokens",
         **best,
+        "prefill_ms_steady": round(prefill_steady_ms, 2),
+        "prefill_tokens_per_s_steady": round(batch * prompt_len / (prefill_steady_ms * 1e-3), 1),
         "by_streams": {str(k): v for k, v in runs.items()},
         "step_kernels": {"position": prompt_len + new_tokens // 2, "by_kernel": per_kernel,
                          "sum_ms_per_step": round(kernel_sum_ms, 4),
@@ -657,9 +672,11 @@ def bench_attention(dev, steps: int, warmup: int, eager: bool, calibrate: bool) 
 
 def bench_prompt_gemm(dev, steps: int, warmup: int, eager: bool) -> dict:
     """The prompt pass's four W4A16 GEMMs (Qwen3-0.6B, 16 x 512 = 8192 rows) with their
-    epilogues: qkv, o_proj + residual, gate_up + SwiGLU, down + residual.  A step runs
-    each 8 times (one graph replay; eager launches with ``eager``, for counter runs);
-    the weights stay MALL-warm, as the GEMMs are bound by their k-loops, not by bytes."""
+    epilogues: qkv, o_proj + residual, gate_up + SwiGLU (and its half-group sums), down +
+    residual, each given its input's row group sums as the prompt pass hands them over
+    (``own_sums_us_per_launch``: the same GEMM forming them itself).  A step runs each 8
+    times (one graph replay; eager launches with ``eager``, for counter runs); the weights
+    stay MALL-warm, as the GEMMs are bound by their k-loops, not by bytes."""
     import torch
     from torch2iron_amd import ops
     from torch2iron_amd.formats import random_weight_on_device
@@ -669,45 +686,75 @@ def bench_prompt_gemm(dev, steps: int, warmup: int, eager: bool) -> dict:
     for name, k, n in (("qkv", 1024, 4096), ("o_proj", 2048, 1024), ("gate_up", 1024, 6144), ("down", 3072, 1024)):
         w = random_weight_on_device(k, n, g, dev)
         x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
+        parts = 2 if name == "down" else 1
+        xs = x.double().view(m, k * parts // 128, 128 // parts).sum(-1).float().contiguous()
         if name == "gate_up":
             y = torch.empty(m, n // 2, dtype=torch.bfloat16, device=dev)
-            call = lambda: ops.gate_up(x, w, swiglu=True, out=y)
+            hs = torch.empty(m, n // 128, device=dev)
+            forms = {"sums": lambda: ops.gate_up(x, w, swiglu=True, out=y, x_sums=xs, out_sums=hs),
+                     "own": lambda: ops.gate_up(x, w, swiglu=True, out=y)}
         elif name == "qkv":
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            call = lambda: ops.linear(x, w, out=y)
+            forms = {"sums": lambda: ops.linear(x, w, out=y, x_sums=xs), "own": lambda: ops.linear(x, w, out=y)}
         else:
             r = torch.randn(m, n, generator=g, device=dev).to(torch.bfloat16)
             y = torch.empty(m, n, dtype=torch.bfloat16, device=dev)
-            call = lambda: ops.linear(x, w, residual=r, out=y)
-        call()
-        torch.cuda.synchronize()
-
-        def step():
-            for _ in range(reps):
-                call()
-
-        run = step
-        if not eager:
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                step()
-            run = graph.replay
-        for _ in range(warmup):
-            run()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(steps):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (steps * reps)
+            forms = {"sums": lambda: ops.linear(x, w, residual=r, out=y, x_sums=xs, sum_parts=parts),
+                     "own": lambda: ops.linear(x, w, residual=r, out=y)}
+        us_by = {}
+        for form, call in forms.items():
+            us_by[form] = _time_prompt_gemm(call, reps, steps, warmup, eager)
+        us = us_by["sums"]
         flops = 2 * m * k * n
         res[name] = {"M": m, "K": k, "N": n, "us_per_launch": round(us, 2), "TFLOPs": round(flops / us / 1e6, 1),
-                     "frac_of_2_5PFLOPs": round(flops / us / 1e6 / 2500.0, 4)}
-        log(f"prompt GEMM {name} M={m} K={k} N={n}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s")
+                     "frac_of_2_5PFLOPs": round(flops / us / 1e6 / 2500.0, 4),
+                     "own_sums_us_per_launch": round(us_by["own"], 2)}
+        log(f"prompt GEMM {name} M={m} K={k} N={n}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s "
+            f"(forming its own row sums: {us_by['own']:.1f} us)")
         del w, x, y
+    # the prompt pass's causal attention: 16 sequences x 512 rows, 16 q / 8 kv heads,
+    # head_dim 128, with its head sums; flops 4 B Hq T^2 D / 2 (causal half of QK^T and PV)
+    b, t, hq, hkv, d = 16, 512, 16, 8, 128
+    q = torch.randn(b, hq, t, d, generator=g, device=dev).to(torch.bfloat16)
+    kc = torch.randn(b, hkv, t, d, generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn(b, hkv, t, d, generator=g, device=dev).to(torch.bfloat16)
+    out = torch.empty(b * t, hq * d, dtype=torch.bfloat16, device=dev)
+    sums = torch.empty(b * t, hq, device=dev)
+    us = _time_prompt_gemm(lambda: ops.prefill_attention(q, 0, hkv, kc, vc, out=out, out_sums=sums), reps, steps,
+                           warmup, eager)
+    flops = 4 * b * hq * t * t * d / 2
+    res["attention"] = {"B": b, "T": t, "Hq": hq, "Hkv": hkv, "D": d, "us_per_launch": round(us, 2),
+                        "TFLOPs": round(flops / us / 1e6, 1), "frac_of_2_5PFLOPs": round(flops / us / 1e6 / 2500.0, 4)}
+    log(f"prompt attention B={b} T={t} Hq={hq} Hkv={hkv}: {us:.1f} us, {flops / us / 1e6:.0f} TFLOP/s (causal)")
     return res
+
+
+def _time_prompt_gemm(call, reps: int, steps: int, warmup: int, eager: bool) -> float:
+    """Microseconds a launch of ``call``: ``steps`` replays of a graph of ``reps`` launches."""
+    import torch
+    call()
+    torch.cuda.synchronize()
+
+    def step():
+        for _ in range(reps):
+            call()
+
+    run = step
+    if not eager:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        run = graph.replay
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (steps * reps)
 
 
 def cpu_info() -> dict:

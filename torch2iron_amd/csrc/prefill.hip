@@ -227,36 +227,34 @@ __global__ __launch_bounds__(256, 3) void prefill_attention_kernel(const Prefill
       }
     }
     // ---- online softmax of the lane's row (log2 domain), causal mask ----
-    // Blocks that every row of the wave sees whole skip the mask.
-    const bool whole = kb * PF_KEYS + PF_KEYS - 1 <= qmin;
-    float mx = -INFINITY;
+    // Blocks that every row of the wave sees whole skip the mask.  The scale goes
+    // into the exponent's FMA (the max of the scaled scores is the scaled max); a
+    // masked score is -inf, whose weight 2^-inf is 0.
+    if (kb * PF_KEYS + PF_KEYS - 1 > qmin) {
 #pragma unroll
-    for (int n = 0; n < 4; ++n)
+      for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = kb * PF_KEYS + n * 16 + 4 * r + i;
-        const float v = (whole || key <= qpos) ? s[n][i] * p.scale_log2 : -INFINITY;
-        s[n][i] = v;
-        mx = fmaxf(mx, v);
-      }
+        for (int i = 0; i < 4; ++i)
+          if (kb * PF_KEYS + n * 16 + 4 * r + i > qpos) s[n][i] = -INFINITY;
+    }
+    float mx = fmaxf(fmaxf(s[0][0], s[0][1]), fmaxf(s[0][2], s[0][3]));
+#pragma unroll
+    for (int n = 1; n < 4; ++n) mx = fmaxf(mx, fmaxf(fmaxf(s[n][0], s[n][1]), fmaxf(s[n][2], s[n][3])));
     mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mn = fmaxf(m, mx);           // finite: every row attends key 0
-    const float f = m > -INFINITY ? __builtin_amdgcn_exp2f(m - mn) : 0.0f;
+    const float mn = fmaxf(m, mx * p.scale_log2);   // finite: every row attends key 0
+    const float f = __builtin_amdgcn_exp2f(m - mn);  // 0 while m is -inf
     float sum = 0.0f;
     uint32_t pw[4][2];                        // bf16 weights, two keys a word
 #pragma unroll
-    for (int n = 0; n < 4; ++n) {
-      float e[4];
+    for (int n = 0; n < 4; ++n)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = round_bf16(__builtin_amdgcn_exp2f(s[n][i] - mn));
-        e[i] = s[n][i] > -INFINITY ? x : 0.0f;
-        sum += e[i];
+      for (int i = 0; i < 4; i += 2) {
+        const uint32_t w = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[n][i], p.scale_log2, -mn)),
+                                       __builtin_amdgcn_exp2f(fmaf(s[n][i + 1], p.scale_log2, -mn)));
+        pw[n][i / 2] = w;
+        sum += __uint_as_float(w << 16) + __uint_as_float(w & 0xFFFF0000u);   // the rounded weights
       }
-      pw[n][0] = pack_bf16x2(e[0], e[1]);
-      pw[n][1] = pack_bf16x2(e[2], e[3]);
-    }
     sum += __shfl_xor(sum, 16, 64);
     sum += __shfl_xor(sum, 32, 64);
     l = l * f + sum;
