@@ -687,10 +687,10 @@ def bench_prompt_gemm(dev, steps: int, warmup: int, eager: bool) -> dict:
         w = random_weight_on_device(k, n, g, dev)
         x = torch.randn(m, k, generator=g, device=dev).to(torch.bfloat16)
         parts = 2 if name == "down" else 1
-        xs = x.double().view(m, k * parts // 128, 128 // parts).sum(-1).float().contiguous()
+        xs = x.double().view(m, k * parts // 128, 128 // parts).sum(-1).t().float().contiguous()   # group-major
         if name == "gate_up":
             y = torch.empty(m, n // 2, dtype=torch.bfloat16, device=dev)
-            hs = torch.empty(m, n // 128, device=dev)
+            hs = torch.empty(n // 128, m, device=dev)
             forms = {"sums": lambda: ops.gate_up(x, w, swiglu=True, out=y, x_sums=xs, out_sums=hs),
                      "own": lambda: ops.gate_up(x, w, swiglu=True, out=y)}
         elif name == "qkv":
@@ -719,7 +719,7 @@ def bench_prompt_gemm(dev, steps: int, warmup: int, eager: bool) -> dict:
     kc = torch.randn(b, hkv, t, d, generator=g, device=dev).to(torch.bfloat16)
     vc = torch.randn(b, hkv, t, d, generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty(b * t, hq * d, dtype=torch.bfloat16, device=dev)
-    sums = torch.empty(b * t, hq, device=dev)
+    sums = torch.empty(hq, b * t, device=dev)
     us = _time_prompt_gemm(lambda: ops.prefill_attention(q, 0, hkv, kc, vc, out=out, out_sums=sums), reps, steps,
                            warmup, eager)
     flops = 4 * b * hq * t * t * d / 2

@@ -344,22 +344,23 @@ int t2i_prefill_qkv_rope_kv(const uint16_t* x, int32_t B, int32_t T, int32_t p0,
  * GEMM.  The prompt GEMM's zero-point term needs, for every row and 128-wide k
  * group, the sum of the row's bf16 values over the group; given them, it skips
  * the all-ones products that otherwise form them (a third of its matrix-core
- * work).  Sums are fp32 [rows][K / 128] (sum_parts = 1), or two sums per group
- * over its 64-wide halves, [rows][K / 64] (sum_parts = 2); every pointer to sums
- * is 4-byte aligned.  The outputs are those of the plain entry points up to fp32
+ * work).  Sums are fp32 and group-major: [K / 128][rows] (sum_parts = 1), or two
+ * sums per group over its 64-wide halves, [K / 64][rows] (sum_parts = 2), so that
+ * one group's sums for a tile of rows are contiguous; every pointer to sums is
+ * 4-byte aligned.  The outputs are those of the plain entry points up to fp32
  * rounding of the sums.  No counterpart in the reference (its NPU kernels apply
  * the zero point per weight): they serve the prompt pass only.
  *
  * t2i_rmsnorm_sums: t2i_rmsnorm (no argmax keys) that also writes y_sums, the
  *   group sums of y; H % 128 == 0.
  * t2i_prefill_attention_sums: t2i_prefill_attention that also writes out_sums
- *   [B * T, Hq], each head's sum of its bf16 context values (one group of the
+ *   [Hq][B * T], each head's sum of its bf16 context values (one group of the
  *   o_proj's k when D = 128).
  * t2i_w4a16_linear_sums / t2i_w4a16_gate_up_sums / t2i_prefill_qkv_rope_kv_sums:
  *   the plain entry points, taking x_sums (ignored below the prompt GEMM's rows).
  *   gate_up_sums also takes x_sums = NULL (the GEMM then forms them); with
  *   swiglu != 0 it also writes y_sums (may be NULL), the half-group
- *   sums of h, [M][N / 128] (sum_parts = 2 for the down projection); it needs the
+ *   sums of h, [N / 128][M] (sum_parts = 2 for the down projection); it needs the
  *   prompt GEMM (M >= 512, N % 128 == 0) and fails otherwise.
  */
 int t2i_rmsnorm_sums(const uint16_t* x, const int32_t* tokens, int32_t V, int32_t M, int32_t H,

@@ -42,8 +42,9 @@ def group_sums(y: torch.Tensor, width: int) -> tuple[torch.Tensor, torch.Tensor]
 
 
 def check_sums(got: torch.Tensor, y: torch.Tensor, width: int):
+    """got: the group-major sums [groups, rows] a producer wrote."""
     ref, mag = group_sums(y, width)
-    err = (got.double().cpu().view_as(ref) - ref).abs()
+    err = (got.double().cpu().view(ref.shape[1], ref.shape[0]).t() - ref).abs()
     assert (err <= 1e-5 * mag + 1e-30).all(), f"worst sum error {(err / (mag + 1e-30)).max():.3e} of |y|"
 
 
@@ -65,9 +66,9 @@ def check_close_to_plain(y: torch.Tensor, plain: torch.Tensor, head_vectors: boo
 
 
 def _sums(x: torch.Tensor, parts: int) -> torch.Tensor:
-    """Exact (fp64, then fp32) group sums of x as a producer would hand them over."""
+    """Exact (fp64, then fp32) group sums of x, group-major, as a producer hands them over."""
     s, _ = group_sums(x, 128 // parts)
-    return s.float().contiguous()
+    return s.t().float().contiguous()
 
 
 @pytest.mark.parametrize("m,h", [(600, 1024), (513, 2048), (64, 3072)])
@@ -76,7 +77,7 @@ def test_rmsnorm_sums(gpu, m, h):
     x = (torch.randn(m, h, generator=g) * 3).to(BF16).to(gpu)
     w = (torch.rand(h, generator=g) * 0.2 + 0.9).to(BF16).to(gpu)
     plain = ops.rmsnorm(x, w, 1e-6)
-    sums = torch.full((m, h // 128), float("nan"), device=gpu)
+    sums = torch.full((h // 128, m), float("nan"), device=gpu)
     y = ops.rmsnorm(x, w, 1e-6, out_sums=sums)
     assert torch.equal(y, plain)
     check_sums(sums, y, 128)
@@ -90,7 +91,7 @@ def test_rmsnorm_sums_gathered_rows(gpu):
     w = (torch.rand(h, generator=g) * 0.2 + 0.9).to(BF16).to(gpu)
     tok = torch.randint(0, v, (m,), generator=g, dtype=torch.int32).to(gpu)
     x_out = torch.empty(m, h, dtype=BF16, device=gpu)
-    sums = torch.empty(m, h // 128, device=gpu)
+    sums = torch.empty(h // 128, m, device=gpu)
     y = ops.rmsnorm(table, w, 1e-6, tokens=tok, x_out=x_out, out_sums=sums)
     assert torch.equal(x_out, table[tok.long()])
     assert torch.equal(y, ops.rmsnorm(table[tok.long()].contiguous(), w, 1e-6))
@@ -105,7 +106,7 @@ def test_prefill_attention_sums(gpu, b, t, hq, hkv):
     kc = torch.randn(b, hkv, cap, d, generator=g).to(BF16).to(gpu)
     vc = torch.randn(b, hkv, cap, d, generator=g).to(BF16).to(gpu)
     plain = ops.prefill_attention(q, 0, hkv, kc, vc)
-    sums = torch.full((b * t, hq), float("nan"), device=gpu)
+    sums = torch.full((hq, b * t), float("nan"), device=gpu)
     out = ops.prefill_attention(q, 0, hkv, kc, vc, out_sums=sums)
     assert torch.equal(out, plain)
     check_sums(sums, out, 128)
@@ -151,7 +152,7 @@ def test_gate_up_with_sums(gpu):
     g, u = ops.gate_up(xd, w, swiglu=False, x_sums=xs)
     check_linear(g, ow.linear(x.float().numpy(), *gate, accumulate="fp64"))
     check_linear(u, ow.linear(x.float().numpy(), *up, accumulate="fp64"))
-    hs = torch.full((m, 2 * inter // 128), float("nan"), device=gpu)
+    hs = torch.full((2 * inter // 128, m), float("nan"), device=gpu)
     h = ops.gate_up(xd, w, swiglu=True, x_sums=xs, out_sums=hs)
     check_close_to_plain(h, ops.gate_up(xd, w, swiglu=True))
     check_sums(hs, h, 64)

@@ -28,8 +28,8 @@ constexpr int NORM_THREADS = 256;
 constexpr int NORM_MAX_CHUNKS = 4;   // 16-byte chunks per thread: H <= 8192
 
 // gsum (may be NULL): fp32 sums of each output row's bf16 values over each
-// 128-wide group, [rows][H / 128] (H a multiple of 128): sixteen lanes hold one
-// group, each sums its 8 values in order, then a 16-lane DPP sum.
+// 128-wide group, group-major [H / 128][rows] (H a multiple of 128): sixteen
+// lanes hold one group, each sums its 8 values in order, then a 16-lane DPP sum.
 __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
     const uint16_t* __restrict__ x, const int32_t* __restrict__ tokens, int V, int H,
     const uint16_t* __restrict__ w, float eps, uint16_t* __restrict__ x_out,
@@ -89,7 +89,7 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(
       if (x_out) *reinterpret_cast<u32x4*>(x_out + (size_t)row * H + ch * 8) = v[i];
       if (gsum) {
         gs = row_sum16(gs);
-        if ((ch & 15) == 0) gsum[(size_t)row * (H >> 7) + (ch >> 4)] = gs;
+        if ((ch & 15) == 0) gsum[(size_t)(ch >> 4) * gridDim.x + row] = gs;
       }
     }
   }

@@ -103,7 +103,7 @@ struct PrefillAttnParams {
   const uint16_t* kc;     // [B, Hkv, cap, D]
   const uint16_t* vc;
   uint16_t* out;          // [B*T, Hq * D]
-  float* out_sums;        // NULL, or [B*T, Hq]: each head's sum of its bf16 context values
+  float* out_sums;        // NULL, or [Hq, B*T]: each head's sum of its bf16 context values
   int B, T, Hq, Hkv, cap, p0;
   float scale_log2;       // D^-1/2 * log2(e)
 };
@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256, 3) void prefill_attention_kernel(const Prefill
       // the head's 128 values are one quantisation group of the next product's k
       hs += __shfl_xor(hs, 16, 64);
       hs += __shfl_xor(hs, 32, 64);
-      if (r == 0) p.out_sums[((size_t)b * p.T + t_row) * p.Hq + head] = hs;
+      if (r == 0) p.out_sums[(size_t)head * p.B * p.T + (size_t)b * p.T + t_row] = hs;
     }
   }
 }

@@ -164,9 +164,10 @@ __device__ __forceinline__ void gemm_issue(const LinearParams& p, int m0, int n0
                                            GemmStage& st) {
   if constexpr (XSP > 0) {
     if (wave == 1) {
-      const float* src = p.xs + (size_t)min(m0 + lane, p.M - 1) * p.ldxs + kt * XSP;
+      // group-major sums: the k-tile's 64 rows are 256 contiguous bytes a part
+      const float* src = p.xs + (size_t)(kt * XSP) * p.ldxs + min(m0 + lane, p.M - 1);
 #pragma unroll
-      for (int u = 0; u < XSP; ++u) lds_dma4(src + u, &st.xs[GM_BM * u]);
+      for (int u = 0; u < XSP; ++u) lds_dma4(src + (size_t)u * p.ldxs, &st.xs[GM_BM * u]);
     }
   }
   const int c = lane & 15, r = lane >> 4;
@@ -494,7 +495,7 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
           }
         }
         const int m = m0 + lane;
-        if (m < p.M) p.ys[(size_t)m * p.ldys + (n0 >> 7)] = s;
+        if (m < p.M) p.ys[(size_t)(n0 >> 7) * p.ldys + m] = s;
       }
     }
   }
@@ -775,9 +776,9 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
     p.epi = epi;
     p.xs = xs;
     p.xs_parts = xs_parts;
-    p.ldxs = xs_parts * (K / GS);
+    p.ldxs = M;
     p.ys = ys;
-    p.ldys = N / GM_BN;
+    p.ldys = M;
     return t2i_host::hip_status(launch_gemm(p, QkvPrepParams{}, reinterpret_cast<hipStream_t>(stream)),
                                 "w4a16 gemm launch");
   }
@@ -845,7 +846,7 @@ int run_prefill_qkv(const uint16_t* x, const float* x_sums, int32_t B, int32_t T
   static_assert(GM_BN == ATT_D, "one prompt-GEMM column tile is one head");
   p.xs = x_sums;
   p.xs_parts = 1;
-  p.ldxs = K / GS;
+  p.ldxs = p.M;
   return t2i_host::hip_status(launch_gemm(p, pp, reinterpret_cast<hipStream_t>(stream)), "prefill projection launch");
 }
 }  // namespace

@@ -62,10 +62,11 @@ struct LinearParams {
   uint32_t xtag, rtag;
   unsigned* ctl;            // ctl[2]: the launch's error word (bounded waits)
   // Prompt GEMM only.  xs: fp32 sums of each row of x over each 128-wide k group,
-  // [M][ldxs] with xs_parts = 1 (sum of group g at g), or over each 64-wide half
-  // group with xs_parts = 2 (at 2 g, 2 g + 1), taken in place of the kernel's own
-  // row-sum products.  ys (EPI_SWIGLU, may be NULL): the sums of each output row's
-  // bf16 values over each 64-wide column half group, [M][ldys].
+  // group-major: the sums of group g for rows 0 .. M - 1 at xs + g * ldxs
+  // (xs_parts = 1), or over each 64-wide half group, halves 2 g and 2 g + 1
+  // (xs_parts = 2), taken in place of the kernel's own row-sum products.  ys
+  // (EPI_SWIGLU, may be NULL): the sums of each output row's bf16 values over each
+  // 64-wide column half group, half h of row m at ys[h * ldys + m].
   const float* xs;
   float* ys;
   int ldxs, xs_parts, ldys;

@@ -500,9 +500,10 @@ class Qwen3Model:
         }
         if self._prefill_sums(r):
             # row group sums that each producer hands to the next prompt GEMM
-            self._pf["xn_sums"] = torch.empty(r, c.hidden // 128, dtype=torch.float32, device=dev)
-            self._pf["ctx_sums"] = torch.empty(r, c.n_heads, dtype=torch.float32, device=dev)
-            self._pf["h_sums"] = torch.empty(r, c.intermediate // 64, dtype=torch.float32, device=dev)
+            # (group-major: [groups, rows])
+            self._pf["xn_sums"] = torch.empty(c.hidden // 128, r, dtype=torch.float32, device=dev)
+            self._pf["ctx_sums"] = torch.empty(c.n_heads, r, dtype=torch.float32, device=dev)
+            self._pf["h_sums"] = torch.empty(c.intermediate // 64, r, dtype=torch.float32, device=dev)
         return self._pf
 
     def _prefill_sums(self, rows: int) -> bool:

@@ -54,7 +54,7 @@ def _check_dev(name: str, t: torch.Tensor, dtype=None):
 
 
 def _check_sums(name: str, t: torch.Tensor, rows: int, per_row: int):
-    """fp32 row group sums ``[rows, per_row]`` (see ``rmsnorm(out_sums=...)``)."""
+    """fp32 row group sums, group-major ``[per_row, rows]`` (see ``rmsnorm(out_sums=...)``)."""
     _check_dev(name, t, torch.float32)
     if t.numel() != rows * per_row:
         raise ValueError(f"{name} must hold {rows}x{per_row} sums")
@@ -85,9 +85,9 @@ def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None
 
     ``x`` bf16 ``[M, K]`` (or ``[K]`` for the GEMV case): M = 1 is the GEMV,
     M <= 64 a decode batch, more rows a prompt batch.  ``x_sums``: fp32 sums of
-    each row of ``x`` over each 128-wide k group (``sum_parts=1``, ``[M, K/128]``)
-    or 64-wide half group (``sum_parts=2``, ``[M, K/64]``), as the kernel that
-    wrote ``x`` emits them; the prompt GEMM then skips forming them itself.
+    each row of ``x`` over each 128-wide k group (``sum_parts=1``, group-major
+    ``[K/128, M]``) or 64-wide half group (``sum_parts=2``, ``[K/64, M]``), as the
+    kernel that wrote ``x`` emits them; the prompt GEMM then skips forming them.
     """
     _check_weight(w)
     _check_dev("x", x, BF16)
@@ -128,7 +128,7 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
     ``swiglu=True``: returns ``h = silu(gate) * up`` bf16 ``[M, N/2]``.
     ``swiglu=False``: returns ``(gate, up)``, each ``[M, N/2]``.
     ``x_sums`` / ``sum_parts`` as ``linear``.  ``out_sums`` (SwiGLU, prompt rows
-    only): fp32 ``[M, N/128]`` receives each row of ``h`` summed over its 64-wide
+    only): fp32 ``[N/128, M]`` receives each row of ``h`` summed over its 64-wide
     half groups, the down projection's ``x_sums`` with ``sum_parts=2``.
     """
     _check_weight(w_pair)
@@ -230,7 +230,7 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor
 
     With ``tokens`` (int32 ``[M]``), ``x`` is an embedding table ``[V, H]`` and
     the gathered rows are also written to ``x_out``.  ``out_sums`` (fp32
-    ``[M, H/128]``, not with ``argmax_keys``): each output row's sums over its
+    ``[H/128, M]``, not with ``argmax_keys``): each output row's sums over its
     128-wide groups, for a prompt GEMM that takes the output as ``x``.
     """
     _check_dev("x", x, BF16)
@@ -728,7 +728,7 @@ def prefill_attention(q: torch.Tensor, p0: int, n_kv_heads: int, k_cache: torch.
                       out: torch.Tensor | None = None, out_sums: torch.Tensor | None = None) -> torch.Tensor:
     """Causal GQA attention of prompt rows ``q [B, Hq, T, D]`` (positions p0..p0+T-1)
     over cache slots ``0..p0+t``; returns bf16 ``[B * T, Hq * D]``.  ``out_sums``
-    (fp32 ``[B * T, Hq]``) receives each head's sum of its bf16 context values,
+    (fp32 ``[Hq, B * T]``) receives each head's sum of its bf16 context values,
     the o_proj's ``x_sums`` when ``D = 128``."""
     _check_dev("q", q, BF16)
     _check_dev("k_cache", k_cache, BF16)
