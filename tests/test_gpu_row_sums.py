@@ -138,7 +138,12 @@ def test_prompt_linear_with_sums_residual(gpu):
     plain = ops.linear(xd, w, residual=res)
     out = res.clone()
     y = ops.linear(xd, w, residual=out, out=out, x_sums=_sums(x, 1).to(gpu))
-    check_close_to_plain(y, plain)
+    # one bf16 ulp of the product (rounded before the residual is added) and one of the sum
+    lin = ops.linear(xd, w).float().cpu()
+    a, b = y.float().cpu(), plain.float().cpu()
+    bound = 2.0 ** -7 * (lin.abs() + b.abs()) + 1e-4 * lin.abs().max()
+    assert ((a - b).abs() <= bound).all(), f"worst difference {((a - b).abs() / bound).max():.3f} of the bound"
+    assert (a == b).float().mean().item() >= 0.99
 
 
 def test_gate_up_with_sums(gpu):
@@ -152,9 +157,15 @@ def test_gate_up_with_sums(gpu):
     g, u = ops.gate_up(xd, w, swiglu=False, x_sums=xs)
     check_linear(g, ow.linear(x.float().numpy(), *gate, accumulate="fp64"))
     check_linear(u, ow.linear(x.float().numpy(), *up, accumulate="fp64"))
+    g0, u0 = ops.gate_up(xd, w, swiglu=False)
+    check_close_to_plain(g, g0)
+    check_close_to_plain(u, u0)
     hs = torch.full((2 * inter // 128, m), float("nan"), device=gpu)
-    h = ops.gate_up(xd, w, swiglu=True, x_sums=xs, out_sums=hs)
-    check_close_to_plain(h, ops.gate_up(xd, w, swiglu=True))
+    h = ops.gate_up(xd, w, swiglu=True, x_sums=xs, out_sums=hs).float().cpu()
+    # the SwiGLU epilogue on this form's own gate and up, as test_prompt_rows_gate_up
+    h_chain = (torch.nn.functional.silu(g.float().cpu()).to(BF16).float() * u.float().cpu()).to(BF16).float()
+    assert (h - h_chain).abs().max() <= 2.0 ** -7 * h_chain.abs().max()
+    assert (h == h_chain).float().mean() > 0.999
     check_sums(hs, h, 64)
     # the plain input and the sums-out form agree on h too
     hs2 = torch.empty_like(hs)
