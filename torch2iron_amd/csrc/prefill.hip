@@ -14,8 +14,6 @@
 // before that product), and each row's normaliser sums those bf16 weights.
 #include <math.h>
 
-#include <type_traits>
-
 #include "t2i_common.h"
 #include "qk_prep.h"
 
