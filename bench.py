@@ -428,6 +428,10 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     torch.cuda.synchronize(dev)
     prefill_steady_ms = e0.elapsed_time(e1) / 5
     log(f"prefill, five passes back to back: {prefill_steady_ms:.2f} ms a pass")
+    prefill_kernels = time_prefill_kernels(model, dev)
+    log("prefill kernels (us per launch): " + ", ".join(
+        f"{k} {v['us_per_launch']}" for k, v in prefill_kernels.items() if isinstance(v, dict))
+        + f"; sum {prefill_kernels['sum_ms_per_pass']:.2f} ms per pass")
     # each kernel of the step alone, event-timed outside any profiler, at position 576
     # (the middle of the timed steps' 512..638)
     log("decode step kernels, each alone (graphs of its launches in one step, HBM-cold, events)")
@@ -480,6 +484,7 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                     f"prompt {prompt_len} (one prefill pass), {new_tokens} new tokens",
         **best,
         "prefill_ms_steady": round(prefill_steady_ms, 2),
+        "prefill_kernels": prefill_kernels,
         "prefill_tokens_per_s_steady": round(batch * prompt_len / (prefill_steady_ms * 1e-3), 1),
         "by_streams": {str(k): v for k, v in runs.items()},
         "step_kernels": {"position": prompt_len + new_tokens // 2, "by_kernel": per_kernel,
@@ -601,6 +606,78 @@ def time_step_kernels(model, dev, reps: int, pos: int, passes: int = 5) -> dict:
     model.x.copy_(x0)
     model.tokens.copy_(tokens)
     del pool, sink
+    return out
+
+
+def time_prefill_kernels(model, dev, reps: int = 5) -> dict:
+    """Each kernel of the prompt pass on its own, outside any profiler: per kernel a
+    graph of its 28 launches (one per layer, the model's own weights, caches and prompt
+    buffers, as ``Qwen3Model.prefill`` last left them), replayed ``reps`` times after a
+    warm-up replay, HIP events around each replay on the launch stream.  The products'
+    outputs go to spare buffers, so that replays do not feed on themselves.  Returns
+    microseconds per launch and per pass, and TFLOP/s (matrix kernels: 2 M K N; the
+    attention: its causal half of QK^T and PV) or TB/s (the norms)."""
+    import torch
+    from torch2iron_amd import ops
+    c, b = model.cfg, model.batch
+    pf = model._pf
+    t = pf["t"]
+    r = b * t
+    xs_n, xs_ctx, xs_h = pf.get("xn_sums"), pf.get("ctx_sums"), pf.get("h_sums")
+    y_h = torch.empty(r, c.hidden, dtype=torch.bfloat16, device=dev)
+    q = pf["q"]
+    hq = c.n_heads * c.head_dim
+    jobs = [
+        ("rmsnorm", lambda i, L: ops.rmsnorm(pf["x"], L.w.ln1, c.eps, out=pf["xn"], out_sums=xs_n), 2,
+         "TB/s", r * c.hidden * 2 * 2 + (r * c.hidden // 128) * 4),
+        ("qkv_prep", lambda i, L: ops.prefill_qkv_rope_kv(pf["xn"], L.w.qkv, b, 0, c.n_heads, c.n_kv_heads,
+                                                            L.w.q_norm, L.w.k_norm, c.eps, model.rope,
+                                                            model.k_cache[i], model.v_cache[i],
+                                                            rope_style=L.rope_style, q_out=q, x_sums=xs_n), 1,
+         "TFLOP/s", 2 * r * c.hidden * c.qkv_dim),
+        ("attention", lambda i, L: ops.prefill_attention(q, 0, c.n_kv_heads, model.k_cache[i], model.v_cache[i],
+                                                         out=pf["ctx"], out_sums=xs_ctx), 1,
+         "TFLOP/s", 4 * b * c.n_heads * t * t * c.head_dim // 2),
+        ("o_proj_residual", lambda i, L: ops.linear(pf["ctx"], L.w.o, residual=pf["x"], out=y_h, x_sums=xs_ctx), 1,
+         "TFLOP/s", 2 * r * hq * c.hidden),
+        ("gate_up_swiglu", lambda i, L: ops.gate_up(pf["xn"], L.w.gate_up, swiglu=True, out=pf["h"], x_sums=xs_n,
+                                                    out_sums=xs_h), 1,
+         "TFLOP/s", 2 * r * c.hidden * 2 * c.intermediate),
+        ("down_residual", lambda i, L: ops.linear(pf["h"], L.w.down, residual=pf["x"], out=y_h, x_sums=xs_h,
+                                                  sum_parts=2), 1,
+         "TFLOP/s", 2 * r * c.intermediate * c.hidden),
+    ]
+    stream = torch.cuda.current_stream(dev)
+    out = {}
+    total_ms = 0.0
+    for name, f, per_layer, unit, work in jobs:
+        calls = [lambda i=i, L=L, f=f: f(i, L) for i, L in enumerate(model.layers)]
+        for fn in calls:
+            fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for fn in calls:
+                fn()
+        marks = []
+        for _ in range(reps + 1):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            marks.append((e0, e1))
+        torch.cuda.synchronize()
+        us = sum(a.elapsed_time(b2) for a, b2 in marks[1:]) * 1e3 / (reps * len(calls))
+        launches = per_layer * len(calls)
+        rate = work / us / 1e6
+        out[name] = {"launches_per_pass": launches, "us_per_launch": round(us, 2),
+                     "us_per_pass": round(us * launches, 1),
+                     ("TFLOPs" if unit == "TFLOP/s" else "TBps"): round(rate, 1 if unit == "TFLOP/s" else 3),
+                     ("frac_of_2_5PFLOPs" if unit == "TFLOP/s" else "frac_of_8TBps"):
+                         round(rate / (2500.0 if unit == "TFLOP/s" else 8.0), 4)}
+        total_ms += us * launches / 1e3
+        del g
+    out["sum_ms_per_pass"] = round(total_ms, 3)
     return out
 
 
