@@ -194,15 +194,20 @@ def test_fused_prompt_projection_matches_two_launches(gpu, b, t, p0, hq, hkv, k,
     assert not torch.equal(kc, kc0)   # the prompt's slots were written
 
 
-@pytest.mark.parametrize("weights", ["centered", "uniform"])
-def test_model_prefill_matches_oracle(gpu, weights):
-    """Whole prompt pass (3 layers, batch 4, 70 tokens): the KV cache and the first
-    greedy token of each sequence against the oracle's prefill."""
+@pytest.mark.parametrize("weights,plen", [("centered", 70), ("uniform", 70), ("centered", 160)],
+                         ids=["centered-280rows", "uniform-280rows", "centered-640rows"])
+def test_model_prefill_matches_oracle(gpu, weights, plen):
+    """Whole prompt pass (3 layers, batch 4): the KV cache and the first greedy token of
+    each sequence against the oracle's prefill.  280 rows run the 16-row-tile linear
+    and the separate q/k prep; 640 rows the prompt GEMM with the prep in its epilogue
+    and every GEMM's row sums handed over by the kernel that wrote its input."""
     cfg = gm.Qwen3Config(n_layers=3, vocab=4096)
     t = gm.random_qwen3_tensors(cfg, seed=41, weights=weights)
-    b, plen = 4, 70
+    b = 4
+    cap = plen + 26
     prompt = torch.randint(0, cfg.vocab, (b, plen), generator=torch.Generator().manual_seed(42))
-    m = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=96, device=gpu)
+    m = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu)
+    assert m._prefill_sums(b * plen) == (b * plen >= ops.PROMPT_GEMM_ROWS)
     m.reset()
     m.history = torch.zeros(b, 4, dtype=torch.int32, device=gpu)
     m.step.zero_()
@@ -210,8 +215,8 @@ def test_model_prefill_matches_oracle(gpu, weights):
     first = m.tokens.cpu().long()
     assert int(m.positions.min()) == plen and int(m.positions.max()) == plen
     assert torch.equal(m.history[:, 0].cpu().long(), first)
-    o32 = oq.DenseQwen3(t, _oracle_cfg(cfg), mode="fp32", ctx_cap=96)
-    o16 = oq.DenseQwen3(t, _oracle_cfg(cfg), mode="bf16", ctx_cap=96)
+    o32 = oq.DenseQwen3(t, _oracle_cfg(cfg), mode="fp32", ctx_cap=cap)
+    o16 = oq.DenseQwen3(t, _oracle_cfg(cfg), mode="bf16", ctx_cap=cap)
     l32 = o32.prefill(prompt)
     l16 = o16.prefill(prompt)
     noise = (l16 - l32).abs().amax(dim=1)
