@@ -51,10 +51,20 @@ __device__ __forceinline__ void prep_store(uint16_t* vec, int c, int style, u32x
   }
 }
 
+// Two values rounded to bf16 by one v_cvt_pk_bf16_f32 (the same bits as two
+// round_bf16 calls).
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  const uint32_t p = pack_bf16x2(a, b);
+  a = bf16_lo(p);
+  b = bf16_hi(p);
+}
+
 // The lane's piece of the normalised and rotated vector (normed: q or k; a v
 // vector passes through).  raw: the lane's piece (prep_load's layout), rp: its
 // RoPE pairs, gv: its piece of the norm weight.  The sum of squares is a 16-lane
-// DPP sum, so the 16 lanes of the row call it together.
+// DPP sum, so the 16 lanes of the row call it together.  The roundings of the
+// two elements of a pair go together, and the rotation's sums are rounded by the
+// final packing.
 __device__ __forceinline__ u32x4 prep_vector(u32x4 raw, u32x4 rp, u32x4 gv, bool normed, int style, float eps) {
   constexpr int D = ATT_D;
   const float cs[4] = {bf16_lo(rp.x), bf16_lo(rp.y), bf16_lo(rp.z), bf16_lo(rp.w)};
@@ -70,10 +80,17 @@ __device__ __forceinline__ u32x4 prep_vector(u32x4 raw, u32x4 rp, u32x4 gv, bool
   float y0[4], y1[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float n0 = round_bf16(round_bf16(x0[e] * inv) * g0[e]);
-    const float n1 = round_bf16(round_bf16(x1[e] * inv) * g1[e]);
-    y0[e] = normed ? round_bf16(round_bf16(n0 * cs[e]) + round_bf16(-n1 * sn[e])) : x0[e];
-    y1[e] = normed ? round_bf16(round_bf16(n1 * cs[e]) + round_bf16(n0 * sn[e])) : x1[e];
+    float n0 = x0[e] * inv, n1 = x1[e] * inv;
+    round_pair(n0, n1);
+    n0 *= g0[e];
+    n1 *= g1[e];
+    round_pair(n0, n1);
+    float c0 = n0 * cs[e], c1 = n1 * cs[e];
+    float s0 = -n1 * sn[e], s1 = n0 * sn[e];
+    round_pair(c0, c1);
+    round_pair(s0, s1);
+    y0[e] = normed ? c0 + s0 : x0[e];
+    y1[e] = normed ? c1 + s1 : x1[e];
   }
   return prep_pack(y0, y1, style);
 }

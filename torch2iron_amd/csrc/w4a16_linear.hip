@@ -403,8 +403,12 @@ __global__ __launch_bounds__(GM_THREADS, 3) void w4a16_gemm_kernel(const LinearP
       } else {
         raw = *reinterpret_cast<const u32x4*>(tile + (c >> 2) * GM_EP_WAVE + row * GM_EP_LD + 8 * (c & 3));
       }
-      const u32x4 rp = *reinterpret_cast<const u32x4*>(pp.rope + (size_t)pos * ATT_D + 8 * c);
-      const u32x4 y = prep_vector(raw, rp, gv, normed, pp.style, pp.eps);
+      // v heads pass through (the branch is uniform over the workgroup)
+      u32x4 y = raw;
+      if (normed) {
+        const u32x4 rp = *reinterpret_cast<const u32x4*>(pp.rope + (size_t)pos * ATT_D + 8 * c);
+        y = prep_vector(raw, rp, gv, true, pp.style, pp.eps);
+      }
       uint16_t* dst;
       if (isq) dst = pp.q + (((size_t)b * pp.Hq + head) * pp.T + t) * ATT_D;
       else if (normed) dst = pp.kc + (((size_t)b * pp.Hkv + (head - pp.Hq)) * pp.cap + pos) * ATT_D;
