@@ -559,19 +559,18 @@ __global__ __launch_bounds__(ATT_THREADS) void decode_attention_kernel(const int
 // ============================================================================
 // lm_head (bf16 tied embedding) + greedy argmax
 // ============================================================================
-// 4 waves of up to 2 16-row tiles of the vocabulary each.  The workgroup count
-// is a multiple of 256 (one equal share per CU; Qwen3's 9496 tiles: 1280
-// workgroups of 7 or 8 tiles), each workgroup taking a contiguous range: with
-// 8 tiles a workgroup (1187 workgroups) 163 CUs took a fifth one, ~8 % over an
-// even split.  64-row waves (594 workgroups: CUs with 3 against 2 set the tail)
-// and 2 or 8 waves a workgroup were slower.  So were grids whose workgroups are
-// all resident from the start (one to four a CU, up to 38 tiles a workgroup dealt
-// to its waves in a stride: 67-69 against 61 us at B = 16), and loads that take
-// 64 contiguous bytes of each row per instruction instead of 16-byte pieces 32
-// bytes apart (no change).  A read-only kernel streams at 6.7 TB/s against this
-// kernel's 5.1: every load instruction here spans 16 rows of the table 2 KB apart.
+// 4 waves of up to 5 16-row tiles of the vocabulary each.  The workgroup count
+// is a multiple of 256 (one equal share per CU; Qwen3's 9496 tiles: 512
+// workgroups of 18 or 19 tiles, two a CU; a wave's 64-deep slice of its tiles
+// is 10 KB, two slices in flight), each workgroup taking a contiguous range.  Measured at batch 16,
+// HBM-cold, final norm fused (us a call, same box): 2 tiles a wave (1280
+// workgroups, a fifth one on each CU) 56.8; 3 tiles 55.2; 4 tiles 54.3; 5 tiles
+// 52.5; 6 tiles 53.0; 8 tiles 65.9; 8 waves of 2 tiles 58.3.  Earlier forms:
+// grids whose workgroups are all resident from the start with tiles dealt to the
+// waves in a stride were slower (67-69 against 61 us), and loads of 64
+// contiguous bytes of each row no faster than 16-byte pieces.
 constexpr int LMH_WAVES = 4;
-constexpr int LMH_COLS = 32;                // vocab columns per wave
+constexpr int LMH_COLS = 80;                // vocab columns per wave
 constexpr int LMH_TILES = LMH_COLS / 16;    // MFMA n-tiles per wave
 constexpr int LMH_MAX_K = 4096;   // 16 x K bf16 of LDS (plus 8 KB of regions)
 
@@ -598,7 +597,7 @@ __device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsig
 //     MFMA operand each meet 16 distinct bank groups per 16 lanes.
 //   * The activation rows sit unpadded, 16-byte unit u of row m at u ^ (m & 15)
 //     (m & 7 when K is not a multiple of 128): conflict-free operand reads, and
-//     32 KB plus the 8 KB of regions at K = 1024, so four workgroups share a CU.
+//     32 KB plus the 8 KB of regions at K = 1024 (room for four workgroups a CU).
 //   * The MFMA pairs k-block r of the slice's first half with the activation's
 //     k-block r and the second half likewise (lane (c, r) takes k 8 r and 32 + 8 r).
 __device__ __forceinline__ int lmh_unit(int row, int kb) { return 16 * kb + (row ^ ((2 * kb) & 15)); }
