@@ -428,18 +428,22 @@ __device__ __forceinline__ void compute_loaded(Chunk<MT, LW, CK>& b, float (&tot
   compute_chunk<MT, LW, CK, NORM>(b, total, ss, zshift);
 }
 
-template <int MT, int LW, int CK, bool NORM, bool XROWS, int NC>
+// issue() runs once every chunk's loads are issued (the epilogue's own loads,
+// which then retire after the chunks').
+template <int MT, int LW, int CK, bool NORM, bool XROWS, int NC, class Issue>
 __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_begin, int ncol, int c, int r, int mbase,
                                                 Chunk<MT, LW, CK>& A, float (&total)[MT][LW][4], float& ss,
-                                                int zshift, u32x4* xreg) {
+                                                int zshift, u32x4* xreg, const Issue& issue) {
   const int lane = 16 * r + c;
   if constexpr (NC == 1) {
+    issue();
     compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
   } else {
     Chunk<MT, LW, CK> rest[NC - 1];
 #pragma unroll
     for (int i = 1; i < NC; ++i)
       load_chunk<MT, LW, CK, NORM, XROWS>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
+    issue();
     compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
 #pragma unroll
     for (int i = 1; i < NC; ++i)
@@ -635,16 +639,20 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   __shared__ u32x4 xsh[XROWS ? W * CK * 64 : 1];   // each wave's chunk region (XROWS)
   u32x4* const xreg = &xsh[XROWS ? wave * CK * 64 : 0];
   load_chunk<MT, LW, CK, NORM, XROWS>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
-  // The residual values this wave stores (residual epilogue) are fetched now, so
-  // the epilogue waits for nothing.  The load is unconditional: waves that store
-  // nothing fetch a clamped row and drop it, and without a residual the first
-  // scales row stands in (in bounds, unused).
+  // The residual values this wave stores (residual epilogue) are fetched with
+  // the chunks, so the epilogue waits for nothing: after every chunk's loads in
+  // the straight schedules (they retire last; ahead of the later chunks the sweep
+  // measured 0.5 % slower), before the loop otherwise.  The load is
+  // unconditional: waves that store nothing fetch a clamped row and drop it, and
+  // without a residual the first scales row stands in (in bounds, unused).
   const int st_mi = min(wave >> 2, MT - 1), st_i = wave & 3;
   const int st_local = st_mi * 16 + r * 4 + st_i;
   const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // the row this lane stores (M: none)
   uint32_t resv[(LW + 1) / 2];
-  load_scales<LW>(!NORM && p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
-                  ncol & 1);
+  const auto load_res = [&]() {
+    load_scales<LW>(!NORM && p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
+                    ncol & 1);
+  };
   __builtin_amdgcn_sched_barrier(0);
   after_loads();
   __builtin_amdgcn_sched_barrier(0);
@@ -658,22 +666,29 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
     constexpr bool DEEP = !NORM && CK == 2;   // 4..6 chunks in registers: 12 a chunk
     looped = false;
     if (n == 1) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else if (n == 2) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else if (n == 3) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else if (DEEP && n == 4) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else if (DEEP && n == 5) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else if (DEEP && n == 6) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg);
+      straight_chunks<MT, LW, CK, NORM, XROWS, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg,
+                                                            load_res);
     } else {
       looped = true;
     }
   }
   if (looped) {
+    load_res();
     for (int ch = c_begin; ch < c_end; ch += 2) {
       if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 1, ncol, c, r, mbase, B);
       compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt);
