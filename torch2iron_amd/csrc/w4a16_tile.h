@@ -218,9 +218,6 @@ template <int MT, int LW, int CK, bool NORM, bool XROWS = false>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
   const int ks0 = ch * CK;
-#pragma unroll
-  for (int j = 0; j < CK; ++j)
-    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
   if constexpr (XROWS) {
     static_assert(MT == 1 && (CK == 2 || CK == 4), "whole-row loads of one 16-row tile");
     const int lane = 16 * r + c;
@@ -245,6 +242,9 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
 #pragma unroll
     for (int j = 0; j < CK; ++j) b.g[j] = *reinterpret_cast<const u32x4*>(p.gamma + (ks0 + j) * 32 + r * 8);
   }
+#pragma unroll
+  for (int j = 0; j < CK; ++j)
+    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
   const int g = ks0 / KSG;
   load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
   b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
