@@ -214,6 +214,13 @@ __device__ __forceinline__ int xrow_of(int lane, int i) { return (16 / CK) * i +
 template <int CK>
 __device__ __forceinline__ int xunit(int row, int kb) { return 16 * kb + (row ^ ((kb * 4 / CK) & 15)); }
 
+// A chunk's loads go out in the order their values are used: the activations
+// (moved through LDS first), the norm weight, the packed weights (the MFMAs),
+// then the scales and zeros (the step after the MFMAs, which waits for them
+// only then).  Loads retire in issue order, so each wait also covers every load
+// issued before it.  Measured over the decode sweep against weights first:
+// activations first 0.584 -> 0.600 TB/s, the scales and zeros awaited after the
+// MFMAs 0.600 -> 0.609.
 template <int MT, int LW, int CK, bool NORM, bool XROWS = false>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
@@ -360,10 +367,6 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
     for (int mi = 0; mi < MT; ++mi) pin(b.x[mi][j]);
     if constexpr (NORM) pin(b.g[j]);
   }
-#pragma unroll
-  for (int i = 0; i < (LW + 1) / 2; ++i) pin(b.s[i]);
-  pin(b.zw);
-  const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
   const bf16x8 ones = ones_operand();
   const uint32_t magic = magic_vgpr();
   f32x4 acc[MT][LW];
@@ -402,6 +405,11 @@ __device__ __forceinline__ void compute_chunk(Chunk<MT, LW, CK>& b, float (&tota
         acc[mi][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bop[t], acc[mi][t], 0, 0, 0);
     }
   }
+  // the scales and zeros, loaded after the weights, are waited for only now
+#pragma unroll
+  for (int i = 0; i < (LW + 1) / 2; ++i) pin(b.s[i]);
+  pin(b.zw);
+  const uint32_t zw = b.zw >> zshift;   // zero nibble of column ncol + t at bits 4t
 #pragma unroll
   for (int t = 0; t < LW; ++t) {
     const float zb = -(float)(128 + 1 + ((zw >> (4 * t)) & 0xFu));
