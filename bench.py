@@ -92,7 +92,7 @@ class Sweep:
     the groups run M-major, so between two uses of one copy the whole pool is
     read (the reuse distance is the pool size)."""
 
-    def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None, eager=False):
+    def __init__(self, shapes, ms, pool_bytes, dev, seed, reps=None, eager=False, tiled=True):
         import torch
         from torch2iron_amd import ops
         from torch2iron_amd.formats import algorithmic_bytes, random_weight_on_device
@@ -102,8 +102,14 @@ class Sweep:
         per_copy = sum(k * n // 2 + (k // 128) * n * 2 + (k // 128) * (n // 8) * 4 for _, k, n in shapes)
         self.per_copy = per_copy
         self.copies = max(1, -(-pool_bytes // per_copy)) if pool_bytes else 1
+        # tiled: each copy also gets its decode-linear tiles (ops.tile_weight), which the
+        # linear then reads in place of the AutoGPTQ words, as the decode model's do
         self.weights = {name: [random_weight_on_device(k, n, gen, dev) for _ in range(self.copies)]
                         for name, k, n in shapes}
+        if tiled:
+            for copies in self.weights.values():
+                for w in copies:
+                    ops.tile_weight(w)
         # launches per graph: one per weight copy (HBM-cold), or ``reps`` of the one copy (MALL-warm)
         self.reps = reps or self.copies
         self.groups = []   # (label, M, K, N, graph, bytes, launches)
@@ -534,8 +540,10 @@ def time_step_kernels(model, dev, reps: int, pos: int, passes: int = 5) -> dict:
     from torch2iron_amd.formats import W4A16Weight
 
     def copies(get):
-        return [[get(L.w) if r == 0 else W4A16Weight(get(L.w).qweight.clone(), get(L.w).qzeros.clone(),
-                                                      get(L.w).scales.clone()) for L in model.layers]
+        # copies carry tiles like the model's own weights
+        return [[get(L.w) if r == 0 else ops.tile_weight(W4A16Weight(get(L.w).qweight.clone(),
+                                                                     get(L.w).qzeros.clone(), get(L.w).scales.clone()))
+                 for L in model.layers]
                 for r in range(passes)]
 
     wq, wo = copies(lambda w: w.qkv), copies(lambda w: w.o)
@@ -1010,6 +1018,14 @@ def main():
 
     extra = {}
     if not args.skip_extra:
+        log("HBM-cold sweep over the AutoGPTQ words (the reference-layout entry points, no tiles)")
+        flat = Sweep(QWEN3_06B, ms, args.pool_mb << 20, dev, seed=1, eager=args.eager, tiled=False)
+        f_rate, f_ms, _ = rate(flat, args.steps, args.warmup)
+        extra["autogptq_layout_sweep"] = {"TBps": round(f_rate, 4),
+                                          "avg_launch_us": round(f_ms * 1e3 / flat.launches_per_step, 3)}
+        log(f"AutoGPTQ-layout sweep: {f_rate:.3f} TB/s")
+        del flat
+        torch.cuda.empty_cache()
         log("MALL-warm sweep (one weight copy)")
         warm = Sweep(QWEN3_06B, ms, 0, dev, seed=2, reps=cold_copies)
         extra["mall_warm_TBps"] = round(rate(warm, args.steps, args.warmup)[0], 4)

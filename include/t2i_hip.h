@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 5
+#define T2I_ABI_VERSION 6
 #define T2I_MAX_ROWS (65535 * 16)   /* rows of one linear call: 16-row tiles in grid.z */
 
 #define T2I_OK 0
@@ -106,6 +106,39 @@ int t2i_w4a16_rmsnorm_gate_up(const uint16_t* x, int32_t M, const uint16_t* norm
                               const int32_t* qweight, const int32_t* qzeros, const uint16_t* scales,
                               int32_t K, int32_t N, int32_t group_size, int32_t swiglu,
                               uint16_t* y0, uint16_t* y1, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode-linear weights in tiles.  t2i_w4a16_tile_qweight writes a copy of an
+ * AutoGPTQ qweight [K/8, N] into `tiles` (K/8 * N int32, not overlapping it),
+ * grouped so that the decode linear reads each workgroup's weights as whole,
+ * contiguous lines: one 256-word tile per (16-column block cb, 128-deep group g)
+ * at word (cb * K/128 + g) * 256, holding word row 4 j + r of the group, column
+ * 16 cb + c at (16 r + c) * 4 + j (j, r < 4; c < 16).  A permutation: no value
+ * changes.  Done once per weight (like the reference's repack into its NPU
+ * layout, fast_qwen3/fast_packed_format.py:132-161), stream-ordered.
+ *
+ * t2i_w4a16_linear_tiles is t2i_w4a16_linear / t2i_w4a16_gate_up /
+ * t2i_w4a16_rmsnorm_linear / t2i_w4a16_rmsnorm_gate_up over such tiles: same
+ * kernels, same arithmetic, bit-identical outputs.  qweight (may be NULL) is the
+ * AutoGPTQ original: given, the call also serves prompt rows (M >= 512 without
+ * the fused norm, which read qweight) and reads qweight for the few decode plans
+ * that read it faster; NULL: every plan reads the tiles, and prompt rows are
+ * rejected (T2I_ERR_SHAPE).  epilogue:
+ * T2I_TILES_STORE (y0 = y, or y0 = bf16(bf16(y) + residual) with residual != NULL),
+ * T2I_TILES_SWIGLU (paired weight, y0 = h) or T2I_TILES_PAIRED (y0 = gate, y1 = up).
+ * norm_weight != NULL: the fused RMSNorm (no residual).
+ * No counterpart in the reference's call surface beyond the repack it mirrors:
+ * for callers that keep decode weights resident (the batch-decode driver).
+ */
+#define T2I_TILES_STORE 0
+#define T2I_TILES_SWIGLU 1
+#define T2I_TILES_PAIRED 2
+int t2i_w4a16_tile_qweight(const int32_t* qweight, int32_t K, int32_t N, int32_t* tiles, void* stream);
+int t2i_w4a16_linear_tiles(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                           const int32_t* qweight, const int32_t* tiles, const int32_t* qzeros,
+                           const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                           int32_t epilogue, const uint16_t* residual, uint16_t* y0, uint16_t* y1,
+                           void* stream);
 
 /* ---------------------------------------------------------------------------
  * Weighted RMSNorm over rows of H: y = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * w).

@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.t2i_abi_version() == 5
+    assert lib.t2i_abi_version() == 6
     assert lib.t2i_strerror(-2) == b"unsupported shape"
 
 
@@ -102,6 +102,35 @@ def test_row_sum_entry_points_validate():
     assert lib.t2i_prefill_qkv_rope_kv_sums(*a) == E.T2I_ERR_ALIGN
     a = list(qkv); a[3] = 100                                    # B*T = 400 < 512
     assert lib.t2i_prefill_qkv_rope_kv_sums(*a) == E.T2I_ERR_SHAPE
+
+
+def test_tile_entry_points_validate():
+    """The decode-linear tile calls reject bad arguments before launching anything."""
+    lib, E = _lib.load(), _lib
+    tile = lib.t2i_w4a16_tile_qweight
+    assert tile(None, 1024, 1024, FAKE, None) == E.T2I_ERR_NULL
+    assert tile(FAKE, 1000, 1024, FAKE + 0x100000, None) == E.T2I_ERR_SHAPE
+    assert tile(FAKE, 1024, 1000, FAKE + 0x100000, None) == E.T2I_ERR_SHAPE
+    assert tile(FAKE, 1024, 1024, MISALIGNED + 0x100000, None) == E.T2I_ERR_ALIGN
+    assert tile(FAKE, 1024, 1024, FAKE + 0x1000, None) == E.T2I_ERR_VALUE     # overlaps qweight (512 KiB)
+    lt = lib.t2i_w4a16_linear_tiles
+    args = [FAKE, 16, None, 0.0, None, FAKE, FAKE, FAKE, 1024, 4096, 128, E.T2I_TILES_STORE, None, FAKE, None, None]
+    a = list(args); a[11] = 7
+    assert lt(*a) == E.T2I_ERR_VALUE                                            # unknown epilogue
+    a = list(args); a[11] = E.T2I_TILES_SWIGLU; a[12] = FAKE
+    assert lt(*a) == E.T2I_ERR_VALUE                                            # residual with SwiGLU
+    a = list(args); a[2] = FAKE; a[3] = 1e-6; a[12] = FAKE
+    assert lt(*a) == E.T2I_ERR_VALUE                                            # residual with the fused norm
+    a = list(args); a[1] = 512
+    assert lt(*a) == E.T2I_ERR_SHAPE                                            # prompt rows without qweight
+    a = list(args); a[5] = None
+    assert lt(*a) == E.T2I_ERR_NULL                                             # no tiles
+    a = list(args); a[4] = FAKE; a[5] = MISALIGNED
+    assert lt(*a) == E.T2I_ERR_ALIGN                                            # misaligned tiles
+    a = list(args); a[11] = E.T2I_TILES_PAIRED
+    assert lt(*a) == E.T2I_ERR_NULL                                             # paired needs y1
+    a = list(args); a[10] = 64
+    assert lt(*a) == E.T2I_ERR_GROUP
 
 
 def test_prefill_entry_points_validate():

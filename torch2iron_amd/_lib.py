@@ -22,6 +22,9 @@ T2I_ERR_ALIGN = -3
 T2I_ERR_GROUP = -4
 T2I_ERR_WORKSPACE = -5
 T2I_ERR_VALUE = -6
+T2I_TILES_STORE = 0
+T2I_TILES_SWIGLU = 1
+T2I_TILES_PAIRED = 2
 
 # name -> (restype, argtypes); mirrors include/t2i_hip.h
 SIGNATURES = {
@@ -37,6 +40,10 @@ SIGNATURES = {
                                            c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "t2i_w4a16_rmsnorm_gate_up": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
                                             c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p]),
+    "t2i_w4a16_tile_qweight": (c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_void_p]),
+    "t2i_w4a16_linear_tiles": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
+                                         c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                         c_void_p, c_void_p]),
     "t2i_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_float, c_void_p,
                               c_void_p, c_void_p, c_void_p]),
     "t2i_decode_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),

@@ -27,6 +27,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "t2i_common.h"
 #include "w4a16_tile.h"
 #include "qk_prep.h"
@@ -34,8 +36,9 @@
 namespace t2i {
 
 // XROWS: the activation rows are read whole (see load_chunk); the host picks it for
-// row tiles of 8 or 16 rows.
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS>
+// row tiles of 8 or 16 rows.  TILED: qweight in the tile layout of
+// t2i_w4a16_tile_qweight.
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, const uint32_t* qw_, const uint16_t* sc_,
                                                              const uint32_t* qz_, const uint16_t* aux_, int N_, int M_,
                                                              int K_, int G_, const LinearParams p_) {
@@ -44,7 +47,25 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   p.M = M_ & 0xFFFFFF;
   p.rt = 1 << (M_ >> 24);
   if constexpr (NORM) p.gamma = aux_; else p.residual = aux_;
-  linear_tile<MT, LW, W, CK, NORM, XROWS>(p, G_, blockIdx.x, blockIdx.z);
+  linear_tile<MT, LW, W, CK, NORM, XROWS, TILED>(p, G_, blockIdx.x, blockIdx.z);
+}
+
+// qweight [K/8, N] (AutoGPTQ: word row k/8, column n) into the tile layout the
+// decode linear reads whole lines of: one 256-word tile per (16-column block cb,
+// 128-deep group g), tile cb * (K/128) + g, and in it word row 4 j + r of the
+// group, column c at (16 r + c) * 4 + j.  A lane (c, r) of the kernel then finds
+// its words of one chunk's k-steps j side by side (16 bytes for 4 k-steps), and a
+// workgroup's weights of one column block are one contiguous range.
+__global__ void tile_qweight_kernel(const uint32_t* __restrict__ qw, int K, int N, uint32_t* __restrict__ tiles) {
+  const int groups = K / GS;
+  const size_t total = (size_t)(K / 8) * N;
+  for (size_t o = (size_t)blockIdx.x * blockDim.x + threadIdx.x; o < total; o += (size_t)gridDim.x * blockDim.x) {
+    const size_t tile = o >> 8;
+    const int w = (int)(o & 255);
+    const int cb = (int)(tile / groups), g = (int)(tile - (size_t)cb * groups);
+    const int j = w & 3, c = (w >> 2) & 15, r = w >> 6;
+    tiles[o] = qw[(size_t)(g * 16 + 4 * j + r) * N + cb * 16 + c];
+  }
 }
 
 // ============================================================================
@@ -661,13 +682,13 @@ using t2i_host::fail;
 using t2i_host::LinearPlan;
 using t2i_host::plan_linear;
 
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS>
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED>
 hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   // the kernel takes x rows of K values (ldx = K) and K / (32 CK) chunks, as every plan here sets them
   if (p.ldx != p.K || p.chunks != p.K / (32 * CK)) return hipErrorInvalidValue;
   if (p.M >= (1 << 24) || p.rt < 1 || p.rt > 16 * MT || (p.rt & (p.rt - 1))) return hipErrorInvalidValue;
   const int m_rt = p.M | (__builtin_ctz((unsigned)p.rt) << 24);   // M and log2 of the row-tile height
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM, XROWS>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc,
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM, XROWS, TILED>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc,
                      p.qz, NORM ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
   return hipGetLastError();
 }
@@ -678,7 +699,7 @@ hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
 // tiles of 4 (o_proj and down at M = 16, a tile loading only the instructions that
 // hold its rows); tiles of 1 or 2 rows gain nothing, within +-0.07 us.  Not compiled
 // for 16 waves of 4-step chunks, whose registers are already at the limit.
-template <int MT, int LW, int W, int CK>
+template <int MT, int LW, int W, int CK, bool TILED>
 hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm) {
   constexpr bool XOK = MT == 1 && (CK == 2 || (CK == 4 && W < 16));
   int min_rt = 4;
@@ -688,20 +709,23 @@ hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm
 #endif
   if constexpr (MT > 1) {   // the fused norm and whole-row loads work on one 16-row tile
     (void)min_rt;
-    return norm ? hipErrorInvalidValue : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
+    return norm ? hipErrorInvalidValue : launch_t<MT, LW, W, CK, false, false, TILED>(p, grid, s);
   } else {
     if constexpr (XOK) {
       if (p.rt >= min_rt)
-        return norm ? launch_t<MT, LW, W, CK, true, true>(p, grid, s) : launch_t<MT, LW, W, CK, false, true>(p, grid, s);
+        return norm ? launch_t<MT, LW, W, CK, true, true, TILED>(p, grid, s)
+                    : launch_t<MT, LW, W, CK, false, true, TILED>(p, grid, s);
     }
-    return norm ? launch_t<MT, LW, W, CK, true, false>(p, grid, s) : launch_t<MT, LW, W, CK, false, false>(p, grid, s);
+    return norm ? launch_t<MT, LW, W, CK, true, false, TILED>(p, grid, s)
+                : launch_t<MT, LW, W, CK, false, false, TILED>(p, grid, s);
   }
 }
 
-hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, hipStream_t s) {
+hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, bool tiled, hipStream_t s) {
   const dim3 grid(pl.cbs, 1, pl.mz);
-#define T2I_LAUNCH(a, b, c, d) \
-  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d) return launch_cfg<a, b, c, d>(p, grid, s, norm);
+#define T2I_LAUNCH(a, b, c, d)                                                                 \
+  if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)                                     \
+    return tiled ? launch_cfg<a, b, c, d, true>(p, grid, s, norm) : launch_cfg<a, b, c, d, false>(p, grid, s, norm);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;
@@ -739,12 +763,27 @@ int check_weights(const int32_t* qweight, const int32_t* qzeros, const uint16_t*
 // xs / xs_parts: x's precomputed row sums (may be NULL: the prompt GEMM forms its
 // own; other kernels never need them); ys: the SwiGLU output's half-group sums
 // (prompt GEMM only; may be NULL).
+// Plans that read the AutoGPTQ words faster than the tiles, when a call has both:
+// 64-column blocks of one m-tile, whose lanes' 64 tiled bytes per chunk leave each
+// load instruction with 16-byte pieces 64 bytes apart (measured HBM-cold, us a
+// launch, AutoGPTQ -> tiles: Qwen3-0.6B gate_up-shaped N = 6144 at M = 32 4.04 ->
+// 4.16, qkv at M = 64 4.03 -> 4.10), and the fused-norm paired gate_up at
+// 32-column blocks (4.00 -> 4.03 at M = 16).  Every other decode plan reads the
+// tiles faster (down at M = 16 4.12 -> 3.68, o_proj 3.30 -> 3.19, qkv at M = 32
+// 3.45 -> 3.21).
+bool autogptq_reads_faster(const LinearPlan& pl, bool paired, bool norm) {
+  return (pl.LW == 4 && pl.MT == 1) || (paired && norm && pl.LW == 2);
+}
+
+// tiles (may be NULL): qweight's words in the tile layout of t2i_w4a16_tile_qweight,
+// read by the 16-row-tile kernel; qweight may then be NULL (no prompt-GEMM rows).
 int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float eps, const int32_t* qweight,
                const int32_t* qzeros, const uint16_t* scales, int K, int N, int group_size,
                const uint16_t* residual, uint16_t* y0, uint16_t* y1, void* stream, const float* xs = nullptr,
-               int xs_parts = 1, float* ys = nullptr) {
-  int rc = check_weights(qweight, qzeros, scales, K, N, group_size);
+               int xs_parts = 1, float* ys = nullptr, const int32_t* tiles = nullptr) {
+  int rc = check_weights(qweight ? qweight : tiles, qzeros, scales, K, N, group_size);
   if (rc) return rc;
+  if (qweight && tiles && !aligned16(tiles)) return fail(T2I_ERR_ALIGN, "tiles must be 16-byte aligned");
   if (xs_parts != 1 && xs_parts != 2) return fail(T2I_ERR_VALUE, "sum_parts must be 1 or 2");
   if (ys && epi != EPI_SWIGLU) return fail(T2I_ERR_VALUE, "y_sums is only written with swiglu");
   if ((xs && ((uintptr_t)xs & 3u)) || (ys && ((uintptr_t)ys & 3u)))
@@ -762,7 +801,9 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
   if (paired && N % 32) return fail(T2I_ERR_SHAPE, "paired N=%d must be a multiple of 32", N);
   if (!gamma && M >= gemm_min_rows() && N % GM_BN == 0) {
-    // prompt-sized: the LDS-tiled GEMM
+    // prompt-sized: the LDS-tiled GEMM, over the AutoGPTQ words
+    if (!qweight)
+      return fail(T2I_ERR_SHAPE, "M=%d: prompt rows (>= %d) read qweight, which is NULL", M, gemm_min_rows());
     LinearParams p{};
     p.x = x;
     p.qw = reinterpret_cast<const uint32_t*>(qweight);
@@ -785,9 +826,10 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   }
   if (ys) return fail(T2I_ERR_SHAPE, "y_sums needs the prompt GEMM (M >= %d, N a multiple of %d)", gemm_min_rows(), GM_BN);
   const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr, false);
+  const bool tiled = tiles && !(qweight && autogptq_reads_faster(pl, paired, gamma != nullptr));
   LinearParams p{};
   p.x = x;
-  p.qw = reinterpret_cast<const uint32_t*>(qweight);
+  p.qw = reinterpret_cast<const uint32_t*>(tiled ? tiles : qweight);
   p.qz = reinterpret_cast<const uint32_t*>(qzeros);
   p.sc = scales;
   p.residual = residual;
@@ -801,7 +843,7 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   p.chunks = pl.chunks;
   p.epi = epi;
   p.rt = pl.rt;
-  return t2i_host::hip_status(launch_plan(pl, p, gamma != nullptr, reinterpret_cast<hipStream_t>(stream)),
+  return t2i_host::hip_status(launch_plan(pl, p, gamma != nullptr, tiled, reinterpret_cast<hipStream_t>(stream)),
                               "w4a16 linear launch");
 }
 
@@ -921,6 +963,39 @@ extern "C" int t2i_w4a16_rmsnorm_gate_up(const uint16_t* x, int32_t M, const uin
   if (!norm_weight) return fail(T2I_ERR_NULL, "norm_weight must not be NULL");
   return run_linear(swiglu ? EPI_SWIGLU : EPI_PAIRED, x, M, norm_weight, eps, qweight, qzeros, scales, K, N,
                     group_size, nullptr, y0, y1, stream);
+}
+
+extern "C" int t2i_w4a16_tile_qweight(const int32_t* qweight, int32_t K, int32_t N, int32_t* tiles, void* stream) {
+  if (!qweight || !tiles) return fail(T2I_ERR_NULL, "qweight and tiles must not be NULL");
+  if (K <= 0 || K % GS) return fail(T2I_ERR_SHAPE, "K=%d must be a positive multiple of 128", K);
+  if (N <= 0 || N % 16) return fail(T2I_ERR_SHAPE, "N=%d must be a positive multiple of 16", N);
+  if (!aligned16(qweight) || !aligned16(tiles)) return fail(T2I_ERR_ALIGN, "qweight and tiles must be 16-byte aligned");
+  const size_t total = (size_t)(K / 8) * N;
+  const uintptr_t a = (uintptr_t)qweight, b = (uintptr_t)tiles, bytes = total * 4;
+  if (a < b + bytes && b < a + bytes) return fail(T2I_ERR_VALUE, "tiles must not overlap qweight");
+  const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 8192);
+  hipLaunchKernelGGL(t2i::tile_qweight_kernel, dim3(blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint32_t*>(qweight), K, N, reinterpret_cast<uint32_t*>(tiles));
+  return t2i_host::hip_status(hipGetLastError(), "tile_qweight launch");
+}
+
+extern "C" int t2i_w4a16_linear_tiles(const uint16_t* x, int32_t M, const uint16_t* norm_weight, float eps,
+                                      const int32_t* qweight, const int32_t* tiles, const int32_t* qzeros,
+                                      const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                                      int32_t epilogue, const uint16_t* residual, uint16_t* y0, uint16_t* y1,
+                                      void* stream) {
+  if (!tiles) return fail(T2I_ERR_NULL, "tiles must not be NULL");
+  int epi;
+  switch (epilogue) {
+    case T2I_TILES_STORE: epi = residual ? EPI_RESIDUAL : EPI_STORE; break;
+    case T2I_TILES_SWIGLU: epi = EPI_SWIGLU; break;
+    case T2I_TILES_PAIRED: epi = EPI_PAIRED; break;
+    default: return fail(T2I_ERR_VALUE, "epilogue %d unknown", epilogue);
+  }
+  if (epilogue != T2I_TILES_STORE && residual) return fail(T2I_ERR_VALUE, "a residual goes with the plain store only");
+  if (norm_weight && residual) return fail(T2I_ERR_VALUE, "the fused-norm form takes no residual");
+  return run_linear(epi, x, M, norm_weight, eps, qweight, qzeros, scales, K, N, group_size, residual, y0, y1, stream,
+                    nullptr, 1, nullptr, tiles);
 }
 
 extern "C" int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,

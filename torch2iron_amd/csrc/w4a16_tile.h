@@ -223,7 +223,7 @@ __device__ __forceinline__ int xunit(int row, int kb) { return 16 * kb + (row ^ 
 // issued before it.  Measured over the decode sweep against weights first:
 // activations first 0.584 -> 0.600 TB/s, the scales and zeros awaited after the
 // MFMAs 0.600 -> 0.609.
-template <int MT, int LW, int CK, bool NORM, bool XROWS = false>
+template <int MT, int LW, int CK, bool NORM, bool XROWS = false, bool TILED = false>
 __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int ncol, int c, int r, int mbase,
                                            Chunk<MT, LW, CK>& b) {
   const int ks0 = ch * CK;
@@ -249,9 +249,27 @@ __device__ __forceinline__ void load_chunk(const LinearParams& p, int ch, int nc
   }
   if constexpr (NORM)   // one load a lane: piece lane % (4 CK) of the chunk's norm weight (norm_pieces)
     b.gp = *reinterpret_cast<const u32x4*>(p.gamma + ks0 * 32 + 8 * ((16 * r + c) % (4 * CK)));
+  if constexpr (TILED) {
+    // qweight as 16-column tiles (t2i_w4a16_tile_qweight): the lane's LW columns
+    // lie in one tile, their words for this chunk's k-steps contiguous
+    static_assert(CK == 2 || CK == 4, "chunks of 2 or 4 k-steps: within one group");
+    const uint32_t* src = p.qw + (size_t)((ncol >> 4) * (p.K / GS) + ks0 / KSG) * 256 + (r * 16 + (ncol & 15)) * 4 +
+                          ks0 % KSG;
 #pragma unroll
-  for (int j = 0; j < CK; ++j)
-    load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+    for (int t = 0; t < LW; ++t) {
+      if constexpr (CK == 4) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(src + 4 * t);
+        b.w[0][t] = a.x; b.w[1][t] = a.y; b.w[2][t] = a.z; b.w[3][t] = a.w;
+      } else {
+        const u32x2 a = *reinterpret_cast<const u32x2*>(src + 4 * t);
+        b.w[0][t] = a.x; b.w[1][t] = a.y;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < CK; ++j)
+      load_words<LW>(p.qw + (size_t)((ks0 + j) * 4 + r) * p.N + ncol, b.w[j]);
+  }
   const int g = ks0 / KSG;
   load_scales<LW>(p.sc + (size_t)g * p.N + ncol, b.s, ncol & 1);
   b.zw = p.qz[(size_t)g * (p.N >> 3) + (ncol >> 3)];
@@ -451,7 +469,7 @@ __device__ __forceinline__ void compute_loaded(Chunk<MT, LW, CK>& b, float (&tot
 
 // issue() runs once every chunk's loads are issued (the epilogue's own loads,
 // which then retire after the chunks').
-template <int MT, int LW, int CK, bool NORM, bool XROWS, int NC, class Issue>
+template <int MT, int LW, int CK, bool NORM, bool XROWS, bool TILED, int NC, class Issue>
 __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_begin, int ncol, int c, int r, int mbase,
                                                 Chunk<MT, LW, CK>& A, float (&total)[MT][LW][4], float& ss,
                                                 int zshift, u32x4* xreg, u32x4* greg, const Issue& issue) {
@@ -463,7 +481,7 @@ __device__ __forceinline__ void straight_chunks(const LinearParams& p, int c_beg
     Chunk<MT, LW, CK> rest[NC - 1];
 #pragma unroll
     for (int i = 1; i < NC; ++i)
-      load_chunk<MT, LW, CK, NORM, XROWS>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
+      load_chunk<MT, LW, CK, NORM, XROWS, TILED>(p, c_begin + i, ncol, c, r, mbase, rest[i - 1]);
     issue();
     compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt, greg);
 #pragma unroll
@@ -628,10 +646,12 @@ struct NoHook {
   __device__ __forceinline__ void operator()() const {}
 };
 // XROWS: activation rows read whole (load_chunk), through a per-wave LDS region.
+// TILED: qweight in the 16-column tile layout (t2i_w4a16_tile_qweight).
 // RES: the launch may have a residual (residual epilogue); the fused-norm variant
 // has none and issues no residual load (an unused load still costs: RMSNorm +
 // gate_up + SwiGLU at batch 16 4.18 -> 4.08 us without it).
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS = false, bool RES = !NORM, class Hook = NoHook>
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS = false, bool TILED = false, bool RES = !NORM,
+          class Hook = NoHook>
 __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx, int bz,
                                             const Hook& after_loads = Hook()) {
   static_assert(!(NORM && RES), "the fused-norm variant has no residual");
@@ -665,7 +685,7 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   u32x4* const xreg = &xsh[XROWS ? wave * CK * 64 : 0];
   __shared__ u32x4 gsh[NORM ? W * 4 * CK : 1];     // each wave's norm-weight pieces (NORM)
   u32x4* const greg = &gsh[NORM ? wave * 4 * CK : 0];
-  load_chunk<MT, LW, CK, NORM, XROWS>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
+  load_chunk<MT, LW, CK, NORM, XROWS, TILED>(p, min(c_begin, p.chunks - 1), ncol, c, r, mbase, A);
   // The residual values this wave stores (residual epilogue) are fetched with
   // the chunks, so the epilogue waits for nothing: after every chunk's loads in
   // the straight schedules (they retire last; ahead of the later chunks the sweep
@@ -693,22 +713,22 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
     constexpr bool DEEP = !NORM && CK == 2;   // 4..6 chunks in registers: 12 a chunk
     looped = false;
     if (n == 1) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 1>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else if (n == 2) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 2>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else if (n == 3) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 3>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else if (DEEP && n == 4) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 4>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else if (DEEP && n == 5) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 5>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else if (DEEP && n == 6) {
-      straight_chunks<MT, LW, CK, NORM, XROWS, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
+      straight_chunks<MT, LW, CK, NORM, XROWS, TILED, 6>(p, c_begin, ncol, c, r, mbase, A, total, ss, zshift, xreg, greg,
                                                             load_res);
     } else {
       looped = true;
@@ -717,10 +737,10 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   if (looped) {
     load_res();
     for (int ch = c_begin; ch < c_end; ch += 2) {
-      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 1, ncol, c, r, mbase, B);
+      if (ch + 1 < c_end) load_chunk<MT, LW, CK, NORM, XROWS, TILED>(p, ch + 1, ncol, c, r, mbase, B);
       compute_loaded<MT, LW, CK, NORM, XROWS>(A, total, ss, zshift, xreg, lane, p.rt, greg);
       if (ch + 1 >= c_end) break;
-      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM, XROWS>(p, ch + 2, ncol, c, r, mbase, A);
+      if (ch + 2 < c_end) load_chunk<MT, LW, CK, NORM, XROWS, TILED>(p, ch + 2, ncol, c, r, mbase, A);
       compute_loaded<MT, LW, CK, NORM, XROWS>(B, total, ss, zshift, xreg, lane, p.rt, greg);
     }
   }

@@ -15,7 +15,7 @@ at the nibble level, which are exact:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 
 import numpy as np
 import torch
@@ -31,6 +31,9 @@ class W4A16Weight:
     qzeros: torch.Tensor    # int32 [K/g, N/8]
     scales: torch.Tensor    # fp16  [K/g, N]
     group_size: int = GROUP_SIZE
+    # qweight's words as decode-linear tiles (int32, K/8 * N), set by ops.tile_weight;
+    # the decode-sized linears read these instead of qweight when present
+    tiles: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     def __post_init__(self):
         if self.qweight.dtype != torch.int32 or self.qzeros.dtype != torch.int32:

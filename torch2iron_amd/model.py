@@ -166,7 +166,9 @@ def _bf16_dev(a, device) -> torch.Tensor:
 
 
 class Qwen3LayerWeights:
-    """Device weights of one layer, fused for the GPU kernels."""
+    """Device weights of one layer, fused for the GPU kernels.  On a GPU each linear
+    also gets its decode-linear tiles (``ops.tile_weight``), which the decode-sized
+    linears read; prompt batches and the one-launch forms read the AutoGPTQ words."""
 
     def __init__(self, tensors: dict, layer: int, cfg: Qwen3Config, device):
         p = f"model.layers.{layer}"
@@ -181,6 +183,9 @@ class Qwen3LayerWeights:
         self.gate_up = W4A16Weight.from_numpy(*interleave_gate_up(trip(f"{p}.mlp.gate_proj"),
                                                                  trip(f"{p}.mlp.up_proj")), device=device)
         self.down = W4A16Weight.from_numpy(*trip(f"{p}.mlp.down_proj"), device=device)
+        if torch.device(device).type == "cuda":
+            for w in (self.qkv, self.o, self.gate_up, self.down):
+                ops.tile_weight(w)
         self.ln1 = _bf16_dev(tensors[f"{p}.input_layernorm.weight"], device)
         self.ln2 = _bf16_dev(tensors[f"{p}.post_attention_layernorm.weight"], device)
         self.q_norm = _bf16_dev(tensors[f"{p}.self_attn.q_norm.weight"], device)

@@ -78,6 +78,43 @@ def dequantize(w: W4A16Weight) -> torch.Tensor:
     return out
 
 
+def tile_weight(w: W4A16Weight) -> W4A16Weight:
+    """Give ``w`` its decode-linear tiles (``w.tiles``): qweight's words regrouped so
+    that each workgroup of the decode linear reads whole, contiguous lines (a
+    permutation, see ``t2i_w4a16_tile_qweight``).  From then on the linears below
+    (without handed-over row sums) go through ``t2i_w4a16_linear_tiles``, which
+    reads the tiles for the decode plans that gain from them and qweight for the
+    rest and for prompt rows: bit-identical results.  Returns ``w``."""
+    _check_weight(w)
+    if w.tiles is None:
+        tiles = torch.empty(w.qweight.numel(), dtype=torch.int32, device=w.qweight.device)
+        lib = _lib.load()
+        rc = lib.t2i_w4a16_tile_qweight(w.qweight.data_ptr(), w.K, w.N, tiles.data_ptr(),
+                                        _lib.stream_handle(tiles.device))
+        _lib.check(rc, "t2i_w4a16_tile_qweight")
+        w.tiles = tiles
+    return w
+
+
+def _tiles_for(w: W4A16Weight):
+    """The weight's tiles, checked, or None."""
+    if w.tiles is None:
+        return None
+    _check_dev("tiles", w.tiles, torch.int32)
+    if w.tiles.numel() != w.qweight.numel():
+        raise ValueError("tiles must hold as many words as qweight")
+    return w.tiles
+
+
+def _linear_tiles(x2, m, norm_weight, eps, tiles, w, epilogue, residual, out, out_up, name):
+    lib = _lib.load()
+    rc = lib.t2i_w4a16_linear_tiles(x2.data_ptr(), m, _lib.ptr(norm_weight), float(eps), w.qweight.data_ptr(),
+                                    tiles.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N,
+                                    w.group_size, epilogue, _lib.ptr(residual), out.data_ptr(), _lib.ptr(out_up),
+                                    _lib.stream_handle(x2.device))
+    _lib.check(rc, f"t2i_w4a16_linear_tiles ({name})")
+
+
 def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None,
            out: torch.Tensor | None = None, x_sums: torch.Tensor | None = None,
            sum_parts: int = 1) -> torch.Tensor:
@@ -106,7 +143,10 @@ def linear(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor | None = None
         if residual.numel() != m * w.N:
             raise ValueError(f"residual must hold {m}x{w.N} elements")
     lib = _lib.load()
-    if x_sums is not None:
+    tiles = _tiles_for(w) if x_sums is None else None
+    if tiles is not None:
+        _linear_tiles(x2, m, None, 0.0, tiles, w, _lib.T2I_TILES_STORE, residual, out, None, "linear")
+    elif x_sums is not None:
         _check_sums("x_sums", x_sums, m, sum_parts * (w.K // w.group_size))
         rc = lib.t2i_w4a16_linear_sums(x2.data_ptr(), x_sums.data_ptr(), int(sum_parts), m, w.qweight.data_ptr(),
                                        w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N, w.group_size,
@@ -149,7 +189,11 @@ def gate_up(x: torch.Tensor, w_pair: W4A16Weight, swiglu: bool = True, out: torc
         if out_up.numel() != m * inter:
             raise ValueError(f"out_up must hold {m}x{inter} elements")
     lib = _lib.load()
-    if x_sums is not None or out_sums is not None:
+    tiles = _tiles_for(w_pair) if x_sums is None and out_sums is None else None
+    if tiles is not None:
+        _linear_tiles(x2, m, None, 0.0, tiles, w_pair, _lib.T2I_TILES_SWIGLU if swiglu else _lib.T2I_TILES_PAIRED,
+                      None, out, out_up, "gate_up")
+    elif x_sums is not None or out_sums is not None:
         if x_sums is not None:
             _check_sums("x_sums", x_sums, m, sum_parts * (w_pair.K // w_pair.group_size))
         if out_sums is not None:
@@ -185,11 +229,15 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w: W4
     _check_dev("out", out, BF16)
     if out.numel() != m * w.N:
         raise ValueError(f"out must hold {m}x{w.N} elements")
-    lib = _lib.load()
-    rc = lib.t2i_w4a16_rmsnorm_linear(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps), w.qweight.data_ptr(),
-                                      w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N, w.group_size,
-                                      out.data_ptr(), _lib.stream_handle(x.device))
-    _lib.check(rc, "t2i_w4a16_rmsnorm_linear")
+    tiles = _tiles_for(w)
+    if tiles is not None:
+        _linear_tiles(x2, m, norm_weight, eps, tiles, w, _lib.T2I_TILES_STORE, None, out, None, "rmsnorm_linear")
+    else:
+        lib = _lib.load()
+        rc = lib.t2i_w4a16_rmsnorm_linear(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps), w.qweight.data_ptr(),
+                                          w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N, w.group_size,
+                                          out.data_ptr(), _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_rmsnorm_linear")
     return out.view(m, w.N) if x.dim() != 1 else out.view(-1)
 
 
@@ -214,12 +262,19 @@ def rmsnorm_gate_up(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_pa
         _check_dev("out_up", out_up, BF16)
         if out_up.numel() != m * inter:
             raise ValueError(f"out_up must hold {m}x{inter} elements")
-    lib = _lib.load()
-    rc = lib.t2i_w4a16_rmsnorm_gate_up(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps),
-                                       w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(), w_pair.scales.data_ptr(),
-                                       w_pair.K, w_pair.N, w_pair.group_size, int(bool(swiglu)), out.data_ptr(),
-                                       _lib.ptr(out_up), _lib.stream_handle(x.device))
-    _lib.check(rc, "t2i_w4a16_rmsnorm_gate_up")
+    tiles = _tiles_for(w_pair)
+    if tiles is not None:
+        _linear_tiles(x2, m, norm_weight, eps, tiles, w_pair,
+                      _lib.T2I_TILES_SWIGLU if swiglu else _lib.T2I_TILES_PAIRED, None, out, out_up,
+                      "rmsnorm_gate_up")
+    else:
+        lib = _lib.load()
+        rc = lib.t2i_w4a16_rmsnorm_gate_up(x2.data_ptr(), m, norm_weight.data_ptr(), float(eps),
+                                           w_pair.qweight.data_ptr(), w_pair.qzeros.data_ptr(),
+                                           w_pair.scales.data_ptr(), w_pair.K, w_pair.N, w_pair.group_size,
+                                           int(bool(swiglu)), out.data_ptr(), _lib.ptr(out_up),
+                                           _lib.stream_handle(x.device))
+        _lib.check(rc, "t2i_w4a16_rmsnorm_gate_up")
     return out if swiglu else (out, out_up)
 
 
