@@ -294,7 +294,8 @@ def batch_decode_weights(tensors: dict, cfg, device, lm_head: tuple | None = Non
     """The weight buffers of ``batch_decode_runlist`` from AutoGPTQ tensors under
     HF names: q alone, k|v and gate|up paired (pair 0 = key / gate), o_proj,
     down, the norm weights; ``lm_head`` an optional AutoGPTQ triple for
-    ``W_out_head_qparam``."""
+    ``W_out_head_qparam``.  On a GPU each linear also gets its decode-linear tiles
+    (``ops.tile_weight``)."""
     from torch2iron_amd.formats import interleave_gate_up
 
     def trip(name):
@@ -321,4 +322,10 @@ def batch_decode_weights(tensors: dict, cfg, device, lm_head: tuple | None = Non
         })
     if lm_head is not None:
         out["W_out_head_qparam"] = W4A16Weight.from_numpy(*lm_head, device=device)
+    if torch.device(device).type == "cuda":
+        # resident decode weights: their decode-linear tiles too (bit-identical outputs)
+        from torch2iron_amd import ops
+        for w in out.values():
+            if isinstance(w, W4A16Weight):
+                ops.tile_weight(w)
     return out
