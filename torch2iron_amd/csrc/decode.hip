@@ -867,10 +867,14 @@ AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
   AttnPlan pl{};
   const int Q = Hq / Hkv;
   pl.rows = att_rows(Q);
+  bool tuned = false;   // tuning builds: rows given in T2I_ATTN_ROWS are kept
 #ifdef T2I_TUNING
   if (const char* env = getenv("T2I_ATTN_ROWS")) {
     const int r = atoi(env);
-    if ((r == 4 || r == 8 || r == 16) && Q <= 2) pl.rows = r;
+    if ((r == 4 || r == 8 || r == 9 || r == 16) && Q <= 2) {
+      pl.rows = r;
+      tuned = true;
+    }
   }
 #endif
   pl.chunk = 16 * pl.rows;
@@ -888,6 +892,17 @@ AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
         pl.chunk = (ctx_cap + s - 1) / s;
         break;
       }
+    }
+  }
+  // Still unbalanced: fewer, longer chunks of up to 144 slots (9 passes) when their
+  // count makes a multiple of 256 (batch 8, 1088 slots: 8 chunks of 136, 512
+  // workgroups, two a CU, instead of 9 chunks of 128, 576 workgroups).
+  if (!tuned && Q <= 2 && pl.rows == 8 && units * pl.splits >= 256 && (units * pl.splits) % 256) {
+    const int s9 = (ctx_cap + 16 * 9 - 1) / (16 * 9);
+    if (s9 < pl.splits && (units * s9) % 256 == 0) {
+      pl.rows = 9;
+      pl.splits = s9;
+      pl.chunk = (ctx_cap + s9 - 1) / s9;
     }
   }
   if (pl.splits > 1) {
@@ -912,9 +927,11 @@ hipError_t launch_attention_plan(const AttnParams& p, int Q, int rows, dim3 grid
   switch (Q * 100 + rows) {
     case 104: return launch_attention<1, 4, PREP>(p, grid, s);
     case 108: return launch_attention<1, 8, PREP>(p, grid, s);
+    case 109: return launch_attention<1, 9, PREP>(p, grid, s);
     case 116: return launch_attention<1, 16, PREP>(p, grid, s);
     case 204: return launch_attention<2, 4, PREP>(p, grid, s);
     case 208: return launch_attention<2, 8, PREP>(p, grid, s);
+    case 209: return launch_attention<2, 9, PREP>(p, grid, s);
     case 216: return launch_attention<2, 16, PREP>(p, grid, s);
     case 404: return launch_attention<4, 4, PREP>(p, grid, s);
     default: return launch_attention<8, 2, PREP>(p, grid, s);
