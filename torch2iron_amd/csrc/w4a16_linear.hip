@@ -652,19 +652,19 @@ LinearPlan plan_linear(int M, int K, int N, bool paired, bool norm, bool wide) {
 #endif
   finish_plan(pl, M, K, N);
   // 16-column blocks: 8 waves of 4-step chunks when each wave holds at most 3
-  // chunks (K <= 3072: the straight schedules), up to 16 rows and, for K <= 2048,
-  // up to 64: half the partial sums to reduce and half the waves to meet at the
-  // barrier, the same loads in flight.  The K split depends on the shape alone up
-  // to 16 rows, so a row's outputs do not depend on how many rows (up to 16)
-  // share the launch.  Measured HBM-cold with the chunk loads in use order (us a
-  // launch, the previous plan -> this one): Qwen3-0.6B qkv 2.92 -> 2.88 (M = 1),
-  // 3.09 -> 2.92 (M = 8), 3.23 -> 3.14 (M = 16), with the fused norm 3.86 -> 3.69
-  // (M = 16); o_proj 3.68 -> 3.46 (M = 32), 4.05 -> 3.88 (M = 64); Qwen3-1.7B qkv
-  // 3.91 -> 3.82 (M = 1), 4.68 -> 4.52 (M = 16), o_proj 3.78 -> 3.70 (M = 1), 4.07
-  // -> 3.91 (M = 16).  Six 4-step chunks a wave (Qwen3-1.7B down, K = 6144) lose
-  // to 16 waves of 2-step chunks (6.20 -> 6.87 us at M = 1), and so does the
-  // Qwen3-0.6B down (K = 3072) at M = 64 (4.88 -> 5.03).
-  if (!wide && !chosen && pl.LW == 1 && (M <= 16 || K <= 2048) && K / (32 * 4 * 8) <= 3) {
+  // chunks (K <= 3072: the straight schedules): half the partial sums to reduce
+  // and half the waves to meet at the barrier, the same loads in flight.  The K
+  // split then depends on the shape alone, so a row's outputs do not depend on
+  // how many rows share the launch.  Measured HBM-cold with the chunk loads in use
+  // order (us a launch, the previous plan -> this one): Qwen3-0.6B qkv 2.92 -> 2.88
+  // (M = 1), 3.09 -> 2.92 (M = 8), 3.23 -> 3.14 (M = 16), with the fused norm 3.86
+  // -> 3.69 (M = 16); o_proj 3.68 -> 3.46 (M = 32), 4.05 -> 3.88 (M = 64);
+  // Qwen3-1.7B qkv 3.91 -> 3.82 (M = 1), 4.68 -> 4.52 (M = 16), o_proj 3.78 -> 3.70
+  // (M = 1), 4.07 -> 3.91 (M = 16); with the tiled weights the Qwen3-0.6B down (K =
+  // 3072) 4.32 -> 3.92 (M = 32), 4.76 -> 4.56 (M = 64).  Six 4-step chunks a wave
+  // (Qwen3-1.7B down, K = 6144) lose to 16 waves of 2-step chunks (6.20 -> 6.87 us
+  // at M = 1).
+  if (!wide && !chosen && pl.LW == 1 && K / (32 * 4 * 8) <= 3) {
     pl.W = 8;
     pl.CK = 4;
     pl.chunks = K / (32 * 4);
