@@ -147,3 +147,51 @@ def test_tiles_entry_point_without_qweight(gpu):
                                     w.qzeros.data_ptr(), w.scales.data_ptr(), k, n, 128, _lib.T2I_TILES_STORE,
                                     None, y.data_ptr(), None, None)
     assert rc == _lib.T2I_ERR_SHAPE
+
+
+def _random_cases(n_cases: int, seed: int):
+    rs = np.random.RandomState(seed)
+    forms = ["plain", "residual", "norm", "paired", "norm_paired"]
+    cases = []
+    while len(cases) < n_cases:
+        form = forms[len(cases) % len(forms)]
+        k = 128 * int(rs.randint(1, 25))
+        m = int(rs.randint(1, 97))
+        n = 64 * int(rs.randint(1, 97)) if "paired" in form else 16 * int(rs.randint(1, 385))
+        if k * n <= 6 << 20:
+            cases.append((form, m, k, n))
+    return cases
+
+
+RANDOM_CASES = _random_cases(30, seed=77)
+
+
+@pytest.mark.parametrize("form,m,k,n", RANDOM_CASES, ids=[f"{f}-M{m}-K{k}-N{n}" for f, m, k, n in RANDOM_CASES])
+def test_random_shapes_over_tiles_are_bit_identical(gpu, form, m, k, n):
+    """Shapes off the model's list (column-block counts that are odd or not multiples of
+    8, ragged rows), every form: tiles against the AutoGPTQ words, bit for bit."""
+    seed = 5000 + m + 7 * k + 13 * n
+    x = _x(m, k, seed, gpu, scale=2.0)
+    gam = (torch.rand(k, generator=torch.Generator().manual_seed(seed + 1)) * 0.2 + 0.9).to(torch.bfloat16).to(gpu)
+    if "paired" in form:
+        gate, up = ow.synthetic_tensors(k, n // 2, seed=seed + 2), ow.synthetic_tensors(k, n // 2, seed=seed + 3)
+        w = W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu)
+        wt = _tiled(w)
+        if form == "norm_paired":
+            assert torch.equal(ops.rmsnorm_gate_up(x, gam, 1e-6, wt, swiglu=True),
+                               ops.rmsnorm_gate_up(x, gam, 1e-6, w, swiglu=True))
+        else:
+            g1, u1 = ops.gate_up(x, wt, swiglu=False)
+            g0, u0 = ops.gate_up(x, w, swiglu=False)
+            assert torch.equal(g1, g0) and torch.equal(u1, u0)
+        return
+    w = _weight(k, n, seed + 4, gpu)
+    wt = _tiled(w)
+    if form == "norm":
+        assert torch.equal(ops.rmsnorm_linear(x, gam, 1e-6, wt), ops.rmsnorm_linear(x, gam, 1e-6, w))
+    elif form == "residual":
+        res = _x(m, n, seed + 5, gpu)
+        a, b = res.clone(), res.clone()
+        assert torch.equal(ops.linear(x, wt, residual=a, out=a), ops.linear(x, w, residual=b, out=b))
+    else:
+        assert torch.equal(ops.linear(x, wt), ops.linear(x, w))
