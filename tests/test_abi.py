@@ -219,16 +219,18 @@ def test_workspace_sizes_are_consistent():
     # a context of at most one 128-slot chunk needs no workspace
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 100) == 0
     assert lib.t2i_decode_attention_workspace_bytes(8, 16, 8, 128) == 0
-    # counters + (max, sum) pairs + contexts of every chunk
-    for b, hq, hkv, cap, chunk in ((8, 16, 8, 1088, 128), (2, 16, 8, 4096, 128), (4, 16, 4, 640, 64)):
+    # counters + (max, sum) pairs + contexts of every chunk; batch 8 at 1088 slots takes
+    # 8 chunks of 136 (512 workgroups, a multiple of the 256 CUs) instead of 9 of 128
+    for b, hq, hkv, cap, chunk in ((8, 16, 8, 1088, 136), (2, 16, 8, 4096, 128), (4, 16, 4, 640, 64)):
         units, q, splits = b * hkv, hq // hkv, -(-cap // chunk)
         need = units * 4 + units * splits * q * 2 * 4 + units * splits * q * 128 * 4
         n = lib.t2i_decode_attention_workspace_bytes(b, hq, hkv, cap)
         assert need <= n <= need + 512, (b, hq, hkv, cap, n, need)
     assert lib.t2i_decode_attention_workspace_bytes(0, 16, 8, 640) == 0
     # batch 16 x 8 kv heads at 640 slots: 6 splits (768 workgroups, a multiple of the
-    # 256 CUs) instead of 5; at 1088 slots, 9 splits stay (12 would be a third more)
-    for b, cap, splits in ((16, 640, 6), (8, 1088, 9), (32, 640, 5)):
+    # 256 CUs) instead of 5; batch 8 at 1088 slots: no raise of the 9 splits reaches a
+    # multiple (12 would be a third more), so 8 longer chunks of 136 slots (512)
+    for b, cap, splits in ((16, 640, 6), (8, 1088, 8), (32, 640, 5)):
         units, q = b * 8, 2
         need = units * 4 + units * splits * q * 2 * 4 + units * splits * q * 128 * 4
         n = lib.t2i_decode_attention_workspace_bytes(b, 16, 8, cap)
