@@ -578,12 +578,18 @@ class Qwen3Model:
         torch.cuda.current_stream(self.device).wait_stream(stream)
         return g
 
+    # decode steps captured in one graph ("steps", one stream): the boundary between
+    # two graph replays costs ~6 us, paid once per this many tokens
+    STEPS_PER_GRAPH = 8
+
     def _capture(self):
         """One graph per micro-batch and kind ("prompt": layers + prompt bookkeeping;
         "layers": layers only) and one head graph (norm, lm_head, greedy bookkeeping),
         each captured on, and replayed on, its own stream.  With one stream a decode
         step is one graph ("step": layers, head and bookkeeping): no boundary between
-        two graphs in the step (0.789 -> 0.783 ms a step at batch 16)."""
+        two graphs in the step (0.789 -> 0.783 ms a step at batch 16); and
+        ``STEPS_PER_GRAPH`` steps are one more ("steps"), which ``generate`` replays
+        while that many steps remain."""
         if self._captured:
             return
 
@@ -597,6 +603,13 @@ class Qwen3Model:
                                                                           self._micro_prompt_advance(m)))
             if self.n_streams == 1:
                 m.graphs["step"] = self._capture_graph(stream, lambda m=m: (self._micro_layers(m), head()))
+
+                def steps(m=m):
+                    for _ in range(self.STEPS_PER_GRAPH):
+                        self._micro_layers(m)
+                        head()
+
+                m.graphs["steps"] = self._capture_graph(stream, steps)
             else:
                 m.graphs["layers"] = self._capture_graph(stream, lambda m=m: self._micro_layers(m))
         if self.n_streams > 1:
@@ -685,7 +698,13 @@ class Qwen3Model:
             self.forward_step(with_head=True)
             ops.greedy_advance(self.keys, self.tokens, self.positions, self.history, self.step)
         ev[1].record()
-        for _ in range(new_tokens - 1):
+        remaining = new_tokens - 1
+        if use_graph and self.n_streams == 1:
+            # whole groups of steps as one graph each (the step state lives on the GPU)
+            while remaining >= self.STEPS_PER_GRAPH:
+                self.micro[0].graphs["steps"].replay()
+                remaining -= self.STEPS_PER_GRAPH
+        for _ in range(remaining):
             if use_graph:
                 self._replay("layers")
             else:
