@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define T2I_ABI_VERSION 6
+#define T2I_ABI_VERSION 7
 #define T2I_MAX_ROWS (65535 * 16)   /* rows of one linear call: 16-row tiles in grid.z */
 
 #define T2I_OK 0
@@ -139,6 +139,34 @@ int t2i_w4a16_linear_tiles(const uint16_t* x, int32_t M, const uint16_t* norm_we
                            const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
                            int32_t epilogue, const uint16_t* residual, uint16_t* y0, uint16_t* y1,
                            void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Chained RMSNorm between decode linears over tiles (the decode layer's
+ * o_proj -> RMSNorm -> gate_up and down -> RMSNorm -> next qkv): the producer
+ * writes the next norm's input, the consumer takes it pre-multiplied.
+ *   producer: next_norm_weight, xg_out, sumsq_out given, residual epilogue
+ *     (T2I_TILES_STORE with residual): y0 as t2i_w4a16_linear_tiles, and also
+ *     xg_out[m][n] = bf16(y0[m][n] * next_norm_weight[n]) and sumsq_out[m][b] =
+ *     sum over the 16 columns of block b of y0[m][n]^2 (fp32, [M][N/16]).
+ *   consumer: x_sumsq given (no residual, no next norm): x is the producer's
+ *     xg_out and x_sumsq its sumsq_out ([M][K/16], K = 1024 or 2048); the
+ *     result is t2i_w4a16_linear_tiles with norm_weight, eps: the
+ *     products of bf16(x_raw * norm_weight) scaled by bf16(1/sqrt(mean + eps)),
+ *     the mean taken from x_sumsq (the same bits up to the order in which the
+ *     row's squares are summed).
+ * Decode row counts only; the plan must be one of the chained forms:
+ * t2i_w4a16_chain_supported(M, K, N, role) says which (role 0 producer, 1
+ * consumer, 2 paired consumer), else the call returns T2I_ERR_SHAPE.  No
+ * counterpart in the reference: its fused RMSNorm + projection operators
+ * (Q4NXFusedQKVProjection / Q4NXFusedUpGateProjection) do the norm in the consumer.
+ */
+int t2i_w4a16_linear_tiles_chain(const uint16_t* x, int32_t M, const float* x_sumsq, float eps,
+                                 const int32_t* qweight, const int32_t* tiles, const int32_t* qzeros,
+                                 const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                                 int32_t epilogue, const uint16_t* residual, uint16_t* y0, uint16_t* y1,
+                                 const uint16_t* next_norm_weight, uint16_t* xg_out, float* sumsq_out,
+                                 void* stream);
+int t2i_w4a16_chain_supported(int32_t M, int32_t K, int32_t N, int32_t role);
 
 /* ---------------------------------------------------------------------------
  * Weighted RMSNorm over rows of H: y = bf16(bf16(x * bf16(rsqrt(mean(x^2)+eps))) * w).

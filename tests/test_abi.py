@@ -28,7 +28,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), f"{name} declared in t2i_hip.h but not exported"
         assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
-    assert lib.t2i_abi_version() == 6
+    assert lib.t2i_abi_version() == 7
     assert lib.t2i_strerror(-2) == b"unsupported shape"
 
 

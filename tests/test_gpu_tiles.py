@@ -195,3 +195,61 @@ def test_random_shapes_over_tiles_are_bit_identical(gpu, form, m, k, n):
         assert torch.equal(ops.linear(x, wt, residual=a, out=a), ops.linear(x, w, residual=b, out=b))
     else:
         assert torch.equal(ops.linear(x, wt), ops.linear(x, w))
+
+
+# ---- chained RMSNorm between decode linears ----
+CHAIN_SHAPES = [(1, 2048, 1024, 1024), (16, 2048, 1024, 4096), (16, 3072, 1024, 1024), (5, 2048, 2048, 4096),
+                (13, 3072, 1024, 3072)]
+
+
+@pytest.mark.parametrize("m,kp,h,nc", CHAIN_SHAPES, ids=[f"M{m}-K{kp}-H{h}-N{nc}" for m, kp, h, nc in CHAIN_SHAPES])
+def test_chained_norm_matches_the_fused_norm(gpu, m, kp, h, nc):
+    """Producer (o_proj/down shape kp -> h, residual) then consumer (h -> nc): the
+    producer's y equals the plain residual linear bit for bit, its xg is exactly
+    bf16(y * gamma) and its block sums match y**2 (fp32, summation order aside); the
+    consumer equals rmsnorm_linear on y except where the order of the squares' sum
+    moves the bf16 1/rms by one ulp (a row scaled by 1 +- 2^-8 at most)."""
+    if not (ops.chain_supported(m, kp, h, ops.CHAIN_PRODUCER) and ops.chain_supported(m, h, nc, ops.CHAIN_CONSUMER)):
+        pytest.skip("no chained form of this plan")
+    seed = 31 * m + kp + h + nc
+    wp = ops.tile_weight(_weight(kp, h, seed, gpu))
+    wc = ops.tile_weight(_weight(h, nc, seed + 1, gpu))
+    x = _x(m, kp, seed + 2, gpu)
+    res = _x(m, h, seed + 3, gpu, scale=4.0)
+    gam = (torch.rand(h, generator=torch.Generator().manual_seed(seed + 4)) * 0.2 + 0.9).to(torch.bfloat16).to(gpu)
+    y_ref = ops.linear(x, wp, residual=res.clone(), out=torch.empty(m, h, dtype=torch.bfloat16, device=gpu))
+    y = res.clone()
+    xg = torch.empty(m, h, dtype=torch.bfloat16, device=gpu)
+    ss = torch.full((m, h // 16), float("nan"), dtype=torch.float32, device=gpu)
+    ops.linear_residual_next_norm(x, wp, y, y, gam, xg, ss)
+    assert torch.equal(y, y_ref)
+    assert torch.equal(xg, (y.float() * gam.float()).to(torch.bfloat16))
+    ref_ss = (y.double() ** 2).reshape(m, h // 16, 16).sum(-1)
+    assert torch.allclose(ss.double(), ref_ss, rtol=1e-6, atol=0)
+    z = ops.prenormed_linear(xg, ss, 1e-6, wc)
+    z_ref = ops.rmsnorm_linear(y, gam, 1e-6, wc)
+    same_rows = (z == z_ref).all(dim=1)
+    assert same_rows.float().mean() >= 0.75, f"{int(same_rows.sum())}/{m} rows identical"
+    rel = ((z.float() - z_ref.float()).abs() / z_ref.float().abs().clamp_min(1e-3)).max()
+    assert rel <= 2.0 ** -7, f"max relative difference {rel:.3e}"
+
+
+def test_chained_norm_paired_consumer(gpu):
+    m, h, inter = 16, 1024, 3072
+    if not ops.chain_supported(m, h, 2 * inter, ops.CHAIN_PAIRED_CONSUMER):
+        pytest.skip("no chained form of this plan")
+    seed = 4242
+    gate, up = ow.synthetic_tensors(h, inter, seed=seed), ow.synthetic_tensors(h, inter, seed=seed + 1)
+    w = ops.tile_weight(W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu))
+    y = _x(m, h, seed + 2, gpu, scale=3.0)
+    gam = (torch.rand(h, generator=torch.Generator().manual_seed(seed + 3)) * 0.2 + 0.9).to(torch.bfloat16).to(gpu)
+    xg = (y.float() * gam.float()).to(torch.bfloat16)
+    ss = (y.float() ** 2).reshape(m, h // 16, 16).sum(-1).contiguous()
+    for swiglu in (True, False):
+        got = ops.prenormed_gate_up(xg, ss, 1e-6, w, swiglu=swiglu)
+        ref = ops.rmsnorm_gate_up(y, gam, 1e-6, w, swiglu=swiglu)
+        pairs = [(got, ref)] if swiglu else list(zip(got, ref))
+        for a, b in pairs:
+            rel = ((a.float() - b.float()).abs() / b.float().abs().clamp_min(1e-3)).max()
+            assert rel <= 2.0 ** -6, f"swiglu={swiglu}: max relative difference {rel:.3e}"
+            assert (a == b).all(dim=1).float().mean() >= 0.75

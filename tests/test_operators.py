@@ -236,8 +236,10 @@ def test_runlist_layer_matches_decode_layer(gpu, layers):
     cfg = gm.Qwen3Config(n_layers=layers, vocab=512)
     t = gm.random_qwen3_tensors(cfg, seed=41, weights="centered")
     b, cap = 6, 96
-    # the runlist names the separate qkv linear and attention operators
-    m1 = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, fused=False)
+    # the runlist names the separate qkv linear and attention operators, each RMSNorm
+    # fused into its consumer as the reference's operators have it: the layers without
+    # the chained norm (whose sums of squares run in another order)
+    m1 = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, fused=False, chain=False)
     m2 = gm.Qwen3Model(t, cfg, batch=b, ctx_cap=cap, device=gpu, fused=False)
     g = torch.Generator().manual_seed(42)
     x0 = torch.randn(b, cfg.hidden, generator=g).to(BF16).to(gpu)

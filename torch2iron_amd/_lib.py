@@ -44,6 +44,10 @@ SIGNATURES = {
     "t2i_w4a16_linear_tiles": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
                                          c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                          c_void_p, c_void_p]),
+    "t2i_w4a16_linear_tiles_chain": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
+                                               c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                               c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "t2i_w4a16_chain_supported": (c_int32, [c_int32, c_int32, c_int32, c_int32]),
     "t2i_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p, c_float, c_void_p,
                               c_void_p, c_void_p, c_void_p]),
     "t2i_decode_attention_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32]),

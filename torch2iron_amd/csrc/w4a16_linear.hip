@@ -38,7 +38,7 @@ namespace t2i {
 // XROWS: the activation rows are read whole (see load_chunk); the host picks it for
 // row tiles of 8 or 16 rows.  TILED: qweight in the tile layout of
 // t2i_w4a16_tile_qweight.
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED>
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED, int PRE = 0, bool NXT = false>
 __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, const uint32_t* qw_, const uint16_t* sc_,
                                                              const uint32_t* qz_, const uint16_t* aux_, int N_, int M_,
                                                              int K_, int G_, const LinearParams p_) {
@@ -47,7 +47,7 @@ __global__ __launch_bounds__(64 * W) void w4a16_mfma_kernel(const uint16_t* x_, 
   p.M = M_ & 0xFFFFFF;
   p.rt = 1 << (M_ >> 24);
   if constexpr (NORM) p.gamma = aux_; else p.residual = aux_;
-  linear_tile<MT, LW, W, CK, NORM, XROWS, TILED>(p, G_, blockIdx.x, blockIdx.z);
+  linear_tile<MT, LW, W, CK, NORM, XROWS, TILED, PRE, NXT>(p, G_, blockIdx.x, blockIdx.z);
 }
 
 // qweight [K/8, N] (AutoGPTQ: word row k/8, column n) into the tile layout the
@@ -682,13 +682,13 @@ using t2i_host::fail;
 using t2i_host::LinearPlan;
 using t2i_host::plan_linear;
 
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED>
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS, bool TILED, int PRE = 0, bool NXT = false>
 hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
   // the kernel takes x rows of K values (ldx = K) and K / (32 CK) chunks, as every plan here sets them
   if (p.ldx != p.K || p.chunks != p.K / (32 * CK)) return hipErrorInvalidValue;
   if (p.M >= (1 << 24) || p.rt < 1 || p.rt > 16 * MT || (p.rt & (p.rt - 1))) return hipErrorInvalidValue;
   const int m_rt = p.M | (__builtin_ctz((unsigned)p.rt) << 24);   // M and log2 of the row-tile height
-  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM, XROWS, TILED>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc,
+  hipLaunchKernelGGL((w4a16_mfma_kernel<MT, LW, W, CK, NORM, XROWS, TILED, PRE, NXT>), grid, dim3(64 * W), 0, s, p.x, p.qw, p.sc,
                      p.qz, NORM ? p.gamma : p.residual, p.N, m_rt, p.K, (int)grid.x, p);
   return hipGetLastError();
 }
@@ -699,9 +699,29 @@ hipError_t launch_t(const LinearParams& p, dim3 grid, hipStream_t s) {
 // tiles of 4 (o_proj and down at M = 16, a tile loading only the instructions that
 // hold its rows); tiles of 1 or 2 rows gain nothing, within +-0.07 us.  Not compiled
 // for 16 waves of 4-step chunks, whose registers are already at the limit.
+// chain: 0 none, 1 the chained norm's consumer (PRE), 2 its producer (NXT); compiled
+// for the decode plans of 8 waves of 4-step chunks at 16 (both) or 32 columns (PRE).
 template <int MT, int LW, int W, int CK, bool TILED>
-hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm) {
+hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm, int chain) {
   constexpr bool XOK = MT == 1 && (CK == 2 || (CK == 4 && W < 16));
+  if (chain) {
+    constexpr bool CH = MT == 1 && W == 8 && CK == 4 && XOK;
+    if constexpr (CH && LW <= 2) {
+      const bool xr = p.rt >= 4;
+      if (chain == 1 && p.K == 1024)
+        return xr ? launch_t<MT, LW, W, CK, false, true, TILED, 1, false>(p, grid, s)
+                  : launch_t<MT, LW, W, CK, false, false, TILED, 1, false>(p, grid, s);
+      if (chain == 1 && p.K == 2048)
+        return xr ? launch_t<MT, LW, W, CK, false, true, TILED, 2, false>(p, grid, s)
+                  : launch_t<MT, LW, W, CK, false, false, TILED, 2, false>(p, grid, s);
+      if constexpr (LW == 1) {
+        if (chain == 2)
+          return xr ? launch_t<MT, LW, W, CK, false, true, TILED, 0, true>(p, grid, s)
+                    : launch_t<MT, LW, W, CK, false, false, TILED, 0, true>(p, grid, s);
+      }
+    }
+    return hipErrorInvalidValue;
+  }
   int min_rt = 4;
 #ifdef T2I_TUNING
   // tuning builds only: T2I_XROWS_MIN_RT = smallest row tile given whole-row loads (17: never)
@@ -721,11 +741,13 @@ hipError_t launch_cfg(const LinearParams& p, dim3 grid, hipStream_t s, bool norm
   }
 }
 
-hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, bool tiled, hipStream_t s) {
+hipError_t launch_plan(const LinearPlan& pl, const LinearParams& p, bool norm, bool tiled, hipStream_t s,
+                       int chain = 0) {
   const dim3 grid(pl.cbs, 1, pl.mz);
 #define T2I_LAUNCH(a, b, c, d)                                                                 \
   if (pl.MT == a && pl.LW == b && pl.W == c && pl.CK == d)                                     \
-    return tiled ? launch_cfg<a, b, c, d, true>(p, grid, s, norm) : launch_cfg<a, b, c, d, false>(p, grid, s, norm);
+    return tiled ? launch_cfg<a, b, c, d, true>(p, grid, s, norm, chain)                       \
+                 : launch_cfg<a, b, c, d, false>(p, grid, s, norm, chain);
   T2I_LINEAR_CONFIGS(T2I_LAUNCH)
 #undef T2I_LAUNCH
   return hipErrorInvalidValue;
@@ -780,7 +802,8 @@ bool autogptq_reads_faster(const LinearPlan& pl, bool paired, bool norm) {
 int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float eps, const int32_t* qweight,
                const int32_t* qzeros, const uint16_t* scales, int K, int N, int group_size,
                const uint16_t* residual, uint16_t* y0, uint16_t* y1, void* stream, const float* xs = nullptr,
-               int xs_parts = 1, float* ys = nullptr, const int32_t* tiles = nullptr) {
+               int xs_parts = 1, float* ys = nullptr, const int32_t* tiles = nullptr, const float* ss_in = nullptr,
+               const uint16_t* g_next = nullptr, uint16_t* xg = nullptr, float* ss_out = nullptr) {
   int rc = check_weights(qweight ? qweight : tiles, qzeros, scales, K, N, group_size);
   if (rc) return rc;
   if (qweight && tiles && !aligned16(tiles)) return fail(T2I_ERR_ALIGN, "tiles must be 16-byte aligned");
@@ -800,6 +823,20 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   }
   const bool paired = epi == EPI_SWIGLU || epi == EPI_PAIRED;
   if (paired && N % 32) return fail(T2I_ERR_SHAPE, "paired N=%d must be a multiple of 32", N);
+  const int chain = ss_in ? 1 : (g_next ? 2 : 0);
+  if (chain) {
+    if (gamma || xs || ys) return fail(T2I_ERR_VALUE, "the chained norm takes no norm_weight and no row sums");
+    if (chain == 1 && (epi == EPI_RESIDUAL || g_next))
+      return fail(T2I_ERR_VALUE, "the chained norm's consumer has no residual and no next norm");
+    if (chain == 1 && K != 1024 && K != 2048) return fail(T2I_ERR_SHAPE, "K=%d: the chained norm's consumer takes K = 1024 or 2048", K);
+    if (chain == 1 && !(eps > 0.0f)) return fail(T2I_ERR_VALUE, "eps must be positive");
+    if (chain == 2 && (epi != EPI_RESIDUAL || !xg || !ss_out))
+      return fail(T2I_ERR_VALUE, "the chained norm's producer needs the residual epilogue, xg and ss_out");
+    if ((ss_in && !aligned16(ss_in)) || (g_next && !aligned16(g_next)) || (xg && !aligned16(xg)) ||
+        (ss_out && ((uintptr_t)ss_out & 3u)))
+      return fail(T2I_ERR_ALIGN, "chained-norm buffers: 16-byte aligned (ss_out 4-byte)");
+    if (M >= gemm_min_rows()) return fail(T2I_ERR_SHAPE, "M=%d: the chained norm serves fewer than %d rows", M, gemm_min_rows());
+  }
   if (!gamma && M >= gemm_min_rows() && N % GM_BN == 0) {
     // prompt-sized: the LDS-tiled GEMM, over the AutoGPTQ words
     if (!qweight)
@@ -826,6 +863,8 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   }
   if (ys) return fail(T2I_ERR_SHAPE, "y_sums needs the prompt GEMM (M >= %d, N a multiple of %d)", gemm_min_rows(), GM_BN);
   const LinearPlan pl = plan_linear(M, K, N, paired, gamma != nullptr, false);
+  if (chain && !(pl.MT == 1 && pl.W == 8 && pl.CK == 4 && pl.LW <= (chain == 2 ? 1 : 2)))
+    return fail(T2I_ERR_SHAPE, "M=%d K=%d N=%d: no chained-norm form of this plan", M, K, N);
   const bool tiled = tiles && !(qweight && autogptq_reads_faster(pl, paired, gamma != nullptr));
   LinearParams p{};
   p.x = x;
@@ -843,8 +882,12 @@ int run_linear(int epi, const uint16_t* x, int M, const uint16_t* gamma, float e
   p.chunks = pl.chunks;
   p.epi = epi;
   p.rt = pl.rt;
-  return t2i_host::hip_status(launch_plan(pl, p, gamma != nullptr, tiled, reinterpret_cast<hipStream_t>(stream)),
-                              "w4a16 linear launch");
+  p.ss_in = ss_in;
+  p.g_next = g_next;
+  p.xg = xg;
+  p.ss_out = ss_out;
+  return t2i_host::hip_status(
+      launch_plan(pl, p, gamma != nullptr, tiled, reinterpret_cast<hipStream_t>(stream), chain), "w4a16 linear launch");
 }
 
 }  // namespace
@@ -996,6 +1039,35 @@ extern "C" int t2i_w4a16_linear_tiles(const uint16_t* x, int32_t M, const uint16
   if (norm_weight && residual) return fail(T2I_ERR_VALUE, "the fused-norm form takes no residual");
   return run_linear(epi, x, M, norm_weight, eps, qweight, qzeros, scales, K, N, group_size, residual, y0, y1, stream,
                     nullptr, 1, nullptr, tiles);
+}
+
+extern "C" int t2i_w4a16_linear_tiles_chain(const uint16_t* x, int32_t M, const float* x_sumsq, float eps,
+                                            const int32_t* qweight, const int32_t* tiles, const int32_t* qzeros,
+                                            const uint16_t* scales, int32_t K, int32_t N, int32_t group_size,
+                                            int32_t epilogue, const uint16_t* residual, uint16_t* y0, uint16_t* y1,
+                                            const uint16_t* next_norm_weight, uint16_t* xg_out, float* sumsq_out,
+                                            void* stream) {
+  if (!tiles) return fail(T2I_ERR_NULL, "tiles must not be NULL");
+  if (!x_sumsq && !next_norm_weight) return fail(T2I_ERR_NULL, "x_sumsq or next_norm_weight must be given");
+  int epi;
+  switch (epilogue) {
+    case T2I_TILES_STORE: epi = residual ? EPI_RESIDUAL : EPI_STORE; break;
+    case T2I_TILES_SWIGLU: epi = EPI_SWIGLU; break;
+    case T2I_TILES_PAIRED: epi = EPI_PAIRED; break;
+    default: return fail(T2I_ERR_VALUE, "epilogue %d unknown", epilogue);
+  }
+  if (epilogue != T2I_TILES_STORE && residual) return fail(T2I_ERR_VALUE, "a residual goes with the plain store only");
+  return run_linear(epi, x, M, nullptr, eps, qweight, qzeros, scales, K, N, group_size, residual, y0, y1, stream,
+                    nullptr, 1, nullptr, tiles, x_sumsq, next_norm_weight, xg_out, sumsq_out);
+}
+
+extern "C" int t2i_w4a16_chain_supported(int32_t M, int32_t K, int32_t N, int32_t role) {
+  if (M < 1 || M >= gemm_min_rows() || K <= 0 || K % GS || N <= 0 || N % 16) return 0;
+  const bool paired = role == 2;
+  if (role < 0 || role > 2 || (paired && N % 32)) return 0;
+  if (role >= 1 && K != 1024 && K != 2048) return 0;
+  const LinearPlan pl = plan_linear(M, K, N, paired, false, false);
+  return pl.MT == 1 && pl.W == 8 && pl.CK == 4 && pl.LW <= (role == 0 ? 1 : 2);
 }
 
 extern "C" int t2i_w4a16_dequant_f32(const int32_t* qweight, const int32_t* qzeros,

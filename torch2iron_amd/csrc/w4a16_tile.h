@@ -70,6 +70,16 @@ struct LinearParams {
   const float* xs;
   float* ys;
   int ldxs, xs_parts, ldys;
+  // Chained RMSNorm between decode linears.  ss_in (consumer, PRE): x holds
+  // bf16(x_raw * gamma) and ss_in [M][K/16] the sums of x_raw^2 over each 16-wide
+  // block of k; the product's fp32 sums are scaled by the row's 1 / rms.  g_next,
+  // xg, ss_out (producer, NXT, residual epilogue): besides y, the next norm's
+  // input bf16(y * g_next) [M][ldy] and the sums of y^2 over each 16-column block
+  // [M][N/16].
+  const float* ss_in;
+  const uint16_t* g_next;
+  uint16_t* xg;
+  float* ss_out;
 };
 
 // MAGIC in a VGPR.  A VALU instruction reads at most one scalar operand (SGPR or
@@ -500,11 +510,15 @@ __device__ __forceinline__ void emit_coh(const LinearParams& p, size_t idx, uint
 // Output row m of this lane's LW columns (ncol .. ncol + LW - 1) from the fp32
 // sums v; res holds the row's residual values (bf16 pairs), fetched at the start.
 // COH: agent-coherent stores (one 16-bit store a value; one or two words a lane).
-template <int LW, bool COH = false>
+// NXT (one column a lane, residual epilogue): also the next norm's input and the
+// row's sum of squares over the 16 columns of the lane's 16-lane row (gword: the
+// aligned word of g_next holding this column's weight).
+template <int LW, bool COH = false, bool NXT = false>
 __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m, const float (&v_in)[LW],
-                                          const uint32_t (&res)[(LW + 1) / 2]) {
+                                          const uint32_t (&res)[(LW + 1) / 2], uint32_t gword = 0) {
   static_assert(!COH || LW <= 2, "coherent stores: one or two words a lane");
-  if (m >= p.M) return;
+  static_assert(!NXT || (LW == 1 && !COH), "the chained norm's producer: one column a lane");
+  if (m >= p.M) return;   // uniform over the 16 lanes of a row
   if constexpr (LW == 1) {
     if (p.epi == EPI_LL) {
       const unsigned long long w = (unsigned long long)f32_to_bf16(v_in[0]) | ((unsigned long long)p.tag << 32);
@@ -525,7 +539,15 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
 #pragma unroll
       for (int t = 0; t < LW; ++t) emit_coh(p, (size_t)m * p.ldy + ncol + t, (uint16_t)f32_to_bf16(v[t]));
     } else if constexpr (LW == 1) {
-      dst[0] = (uint16_t)f32_to_bf16(v[0]);
+      const uint16_t yb = (uint16_t)f32_to_bf16(v[0]);
+      dst[0] = yb;
+      if constexpr (NXT) {
+        const float y = bf16_to_f32(yb);
+        const float g = bf16_to_f32((uint16_t)(gword >> (16 * (ncol & 1))));
+        p.xg[(size_t)m * p.ldy + ncol] = (uint16_t)f32_to_bf16(y * g);
+        const float sq = row_sum16(y * y);
+        if ((ncol & 15) == 0) p.ss_out[(size_t)m * (p.N >> 4) + (ncol >> 4)] = sq;
+      }
     } else {
       uint32_t packed[LW / 2];
 #pragma unroll
@@ -570,10 +592,14 @@ __device__ __forceinline__ void store_row(const LinearParams& p, int ncol, int m
 // every wave that had chunks (wave < nw) parks its sums (and, fused norm, its
 // rows' sums of squares) in red ([W][E][64]) and s_ss ([W][16]); then wave
 // 4 mi + i adds row i of m-tile mi over the waves in wave order and stores it.
-template <int MT, int LW, int W, bool NORM, bool COH>
+// PRE (chained norm, consumer; PRE 4-wide pieces a lane): ssq holds this lane's share
+// of its row's block sums of squares (ss_in); the row's 16 lanes add theirs.  NXT:
+// gword goes to store_row.
+template <int MT, int LW, int W, bool NORM, bool COH, int PRE = 0, bool NXT = false>
 __device__ __forceinline__ void reduce_store(const LinearParams& p, int ncol, int nw, int st_mi, int st_i,
                                              int st_local, int st_m, const float (&total)[MT][LW][4], float ss,
-                                             const uint32_t (&resv)[(LW + 1) / 2], float* red, float* s_ss) {
+                                             const uint32_t (&resv)[(LW + 1) / 2], float* red, float* s_ss,
+                                             const f32x4* ssq = nullptr, uint32_t gword = 0) {
   constexpr int E = MT * LW * 4;
   static_assert(W >= 4 * MT, "one reducing wave per (m-tile, row of the lane)");
   const int lane = threadIdx.x & 63;
@@ -606,12 +632,18 @@ __device__ __forceinline__ void reduce_store(const LinearParams& p, int ncol, in
     for (int t = 0; t < LW; ++t) v[t] += src[((st_mi * LW + t) * 4 + st_i) * 64];
     if constexpr (NORM) t_ss += s_ss[w * 16 + st_local];
   }
-  if constexpr (NORM) {
+  if constexpr (PRE > 0) {
+    float part = 0.0f;
+#pragma unroll
+    for (int q = 0; q < PRE; ++q) part += ((ssq[q][0] + ssq[q][1]) + ssq[q][2]) + ssq[q][3];
+    t_ss = row_sum16(part);   // the row's 16 lanes: every block of K
+  }
+  if constexpr (NORM || PRE > 0) {
     const float inv = round_bf16(1.0f / sqrtf(t_ss / (float)p.K + p.eps));
 #pragma unroll
     for (int t = 0; t < LW; ++t) v[t] *= inv;
   }
-  store_row<LW, COH>(p, ncol, st_m, v, resv);
+  store_row<LW, COH, NXT>(p, ncol, st_m, v, resv, gword);
 }
 
 // Workgroups are dealt to the 8 XCDs round robin by linear id, and each XCD has
@@ -650,12 +682,17 @@ struct NoHook {
 // RES: the launch may have a residual (residual epilogue); the fused-norm variant
 // has none and issues no residual load (an unused load still costs: RMSNorm +
 // gate_up + SwiGLU at batch 16 4.18 -> 4.08 us without it).
-template <int MT, int LW, int W, int CK, bool NORM, bool XROWS = false, bool TILED = false, bool RES = !NORM,
-          class Hook = NoHook>
+// PRE / NXT: the chained norm's consumer (x pre-multiplied by the norm weight, the
+// rows' sums of squares in ss_in) and producer (residual epilogue that also writes
+// the next norm's input and block sums of squares); see LinearParams.
+template <int MT, int LW, int W, int CK, bool NORM, bool XROWS = false, bool TILED = false, int PRE = 0,
+          bool NXT = false, bool RES = !NORM && PRE == 0, class Hook = NoHook>
 __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx, int bz,
                                             const Hook& after_loads = Hook()) {
   static_assert(!(NORM && RES), "the fused-norm variant has no residual");
   static_assert(!NORM || MT == 1, "the fused-norm variant works on one 16-row tile");
+  static_assert(PRE == 0 || (!NORM && !RES && MT == 1), "the chained norm's consumer: one tile, no residual");
+  static_assert(!NXT || (RES && LW == 1 && MT == 1), "the chained norm's producer: residual, one column a lane");
   constexpr int E = MT * LW * 4;      // fp32 results per lane
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar control flow
@@ -695,10 +732,18 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   const int st_local = st_mi * 16 + r * 4 + st_i;
   const int st_m = st_local < p.rt ? mbase + st_local : p.M;   // the row this lane stores (M: none)
   uint32_t resv[(LW + 1) / 2] = {};
+  f32x4 ssq[PRE > 0 ? PRE : 1] = {};   // PRE: this lane's pieces of its row's block sums of squares (K = 1024 PRE)
+  uint32_t gword[1] = {};              // NXT: the word of g_next holding this lane's column
   const auto load_res = [&]() {
     if constexpr (RES)   // (a launch without one reads the scales row instead: in bounds, unused)
       load_scales<LW>(p.residual ? p.residual + (size_t)min(st_m, p.M - 1) * p.ldy + ncol : p.sc + ncol, resv,
                       ncol & 1);
+    if constexpr (NXT) load_scales<1>(p.g_next + ncol, gword, ncol & 1);
+    if constexpr (PRE > 0) {
+      const float* src = p.ss_in + (size_t)min(st_m, p.M - 1) * (64 * PRE) + 4 * c;
+#pragma unroll
+      for (int q = 0; q < PRE; ++q) ssq[q] = *reinterpret_cast<const f32x4*>(src + 64 * q);
+    }
   };
   __builtin_amdgcn_sched_barrier(0);
   after_loads();
@@ -749,7 +794,8 @@ __device__ __forceinline__ void linear_tile(const LinearParams& p, int G, int bx
   const int nw = (p.chunks + per_wave - 1) / per_wave;   // waves that had chunks
   __shared__ float red[W * E * 64];
   __shared__ float s_ss[NORM ? W : 1][16];
-  reduce_store<MT, LW, W, NORM, false>(p, ncol, nw, st_mi, st_i, st_local, st_m, total, ss, resv, red, &s_ss[0][0]);
+  reduce_store<MT, LW, W, NORM, false, PRE, NXT>(p, ncol, nw, st_mi, st_i, st_local, st_m, total, ss, resv, red,
+                                                 &s_ss[0][0], ssq, gword[0]);
 }
 
 // One workgroup's tile of a linear phase inside a launch that runs dependent

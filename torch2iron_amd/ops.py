@@ -278,6 +278,92 @@ def rmsnorm_gate_up(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, w_pa
     return out if swiglu else (out, out_up)
 
 
+# ---- chained RMSNorm between decode linears (over tiles) ----
+CHAIN_PRODUCER, CHAIN_CONSUMER, CHAIN_PAIRED_CONSUMER = 0, 1, 2
+
+
+def chain_supported(m: int, k: int, n: int, role: int) -> bool:
+    """Whether a decode linear of ``m`` rows, K = ``k``, N = ``n`` has a chained-norm
+    form in ``role`` (``CHAIN_PRODUCER``: residual epilogue that also writes the next
+    norm's input; ``CHAIN_CONSUMER`` / ``CHAIN_PAIRED_CONSUMER``: the fused-norm linear /
+    gate_up taking that input)."""
+    return bool(_lib.load().t2i_w4a16_chain_supported(int(m), int(k), int(n), int(role)))
+
+
+def _chain_call(name, x2, m, ss_in, eps, w, epilogue, residual, out, out_up, next_norm, xg_out, ss_out):
+    tiles = _tiles_for(w)
+    if tiles is None:
+        raise ValueError("the chained norm reads the weight's tiles: call tile_weight first")
+    lib = _lib.load()
+    rc = lib.t2i_w4a16_linear_tiles_chain(x2.data_ptr(), m, _lib.ptr(ss_in), float(eps), w.qweight.data_ptr(),
+                                          tiles.data_ptr(), w.qzeros.data_ptr(), w.scales.data_ptr(), w.K, w.N,
+                                          w.group_size, epilogue, _lib.ptr(residual), out.data_ptr(),
+                                          _lib.ptr(out_up), _lib.ptr(next_norm), _lib.ptr(xg_out), _lib.ptr(ss_out),
+                                          _lib.stream_handle(x2.device))
+    _lib.check(rc, f"t2i_w4a16_linear_tiles_chain ({name})")
+
+
+def linear_residual_next_norm(x: torch.Tensor, w: W4A16Weight, residual: torch.Tensor, out: torch.Tensor,
+                              next_norm: torch.Tensor, xg_out: torch.Tensor, ss_out: torch.Tensor) -> torch.Tensor:
+    """``out = bf16(bf16(x @ W^T) + residual)`` (``linear`` with a residual) that also
+    writes the next RMSNorm's input: ``xg_out = bf16(out * next_norm)`` and ``ss_out``
+    fp32 ``[M, N/16]``, the sums of ``out**2`` over each 16-column block."""
+    _check_weight(w)
+    for n_, t in (("x", x), ("residual", residual), ("out", out), ("next_norm", next_norm), ("xg_out", xg_out)):
+        _check_dev(n_, t, BF16)
+    _check_dev("ss_out", ss_out, torch.float32)
+    m = x.shape[0]
+    if x.shape != (m, w.K) or out.numel() != m * w.N or residual.numel() != m * w.N or xg_out.numel() != m * w.N:
+        raise ValueError("x, residual, out and xg_out must be [M, K] / [M, N]")
+    if next_norm.numel() != w.N or ss_out.numel() != m * (w.N // 16):
+        raise ValueError("next_norm must hold N and ss_out M x N/16 values")
+    _chain_call("producer", x, m, None, 0.0, w, _lib.T2I_TILES_STORE, residual, out, None, next_norm, xg_out, ss_out)
+    return out
+
+
+def _consumer_checks(xg, ss, w):
+    _check_weight(w)
+    _check_dev("xg", xg, BF16)
+    _check_dev("ss", ss, torch.float32)
+    m = xg.shape[0]
+    if xg.dim() != 2 or xg.shape[1] != w.K or ss.numel() != m * (w.K // 16):
+        raise ValueError("xg must be [M, K] and ss hold M x K/16 sums")
+    return m
+
+
+def prenormed_linear(xg: torch.Tensor, ss: torch.Tensor, eps: float, w: W4A16Weight,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """``rmsnorm_linear`` of the rows a ``linear_residual_next_norm`` call produced:
+    ``xg`` is its ``xg_out`` (the rows times the norm weight) and ``ss`` its ``ss_out``."""
+    m = _consumer_checks(xg, ss, w)
+    if out is None:
+        out = torch.empty(m, w.N, dtype=BF16, device=xg.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != m * w.N:
+        raise ValueError(f"out must hold {m}x{w.N} elements")
+    _chain_call("consumer", xg, m, ss, eps, w, _lib.T2I_TILES_STORE, None, out, None, None, None, None)
+    return out
+
+
+def prenormed_gate_up(xg: torch.Tensor, ss: torch.Tensor, eps: float, w_pair: W4A16Weight, swiglu: bool = True,
+                      out: torch.Tensor | None = None, out_up: torch.Tensor | None = None):
+    """``rmsnorm_gate_up`` of the rows a ``linear_residual_next_norm`` call produced."""
+    m = _consumer_checks(xg, ss, w_pair)
+    inter = w_pair.N // 2
+    if out is None:
+        out = torch.empty(m, inter, dtype=BF16, device=xg.device)
+    _check_dev("out", out, BF16)
+    if out.numel() != m * inter:
+        raise ValueError(f"out must hold {m}x{inter} elements")
+    if not swiglu:
+        if out_up is None:
+            out_up = torch.empty(m, inter, dtype=BF16, device=xg.device)
+        _check_dev("out_up", out_up, BF16)
+    _chain_call("paired consumer", xg, m, ss, eps, w_pair, _lib.T2I_TILES_SWIGLU if swiglu else _lib.T2I_TILES_PAIRED,
+                None, out, out_up, None, None, None)
+    return out if swiglu else (out, out_up)
+
+
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor | None = None,
             tokens: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
             argmax_keys: torch.Tensor | None = None, out_sums: torch.Tensor | None = None) -> torch.Tensor:
