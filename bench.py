@@ -314,6 +314,18 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
         kc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
         vc = torch.randn(b3, cfg.n_kv_heads, cap3, cfg.head_dim, generator=gen, device=dev).to(torch.bfloat16)
         layers3.append((lay, kc, vc))
+    # the layers chained as the model chains them: each o_proj hands the MLP's RMSNorm
+    # over to gate_up, each down the next layer's to its qkv (the first layer's qkv and
+    # the last layer's down unchained)
+    from torch2iron_amd import ops as _ops
+    chain3 = (_ops.chain_supported(b3, cfg.n_heads * cfg.head_dim, cfg.hidden, _ops.CHAIN_PRODUCER)
+              and _ops.chain_supported(b3, cfg.intermediate, cfg.hidden, _ops.CHAIN_PRODUCER)
+              and _ops.chain_supported(b3, cfg.hidden, cfg.qkv_dim, _ops.CHAIN_CONSUMER)
+              and _ops.chain_supported(b3, cfg.hidden, 2 * cfg.intermediate, _ops.CHAIN_PAIRED_CONSUMER))
+    for li, (lay, _, _) in enumerate(layers3):
+        lay.chain = chain3
+        lay.chain_in = chain3 and li > 0
+        lay.next_ln1 = layers3[li + 1][0].w.ln1 if chain3 and li + 1 < n3 else None
     pos = torch.full((b3,), 1024, dtype=torch.int32, device=dev)
     x0 = torch.randn(b3, cfg.hidden, generator=gen, device=dev).to(torch.bfloat16)
     buf.x.copy_(x0)
@@ -342,7 +354,9 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                    + 2 * 2 * cfg.head_dim + b3 * cfg.n_kv_heads * 1025 * cfg.head_dim * 2 * 2
                    + b3 * cfg.n_kv_heads * cfg.head_dim * 2 * 2 + b3 * cfg.hidden * 2 * 2)
     out["decode_layer"] = {"workload": f"one fused Qwen3-0.6B decode layer, batch 8, context 1024 ({n3} distinct "
-                                       "layers back to back in one graph, HBM-cold)",
+                                       "layers back to back in one graph, HBM-cold"
+                                       + (", RMSNorms chained as in the model)" if chain3 else ")"),
+                           "chained_norm": bool(chain3),
                            "us": round(layer_us, 2), "algorithmic_bytes": layer_bytes,
                            "TBps": round(layer_bytes / (layer_us * 1e-6) / 1e12, 4),
                            "frac_of_8TBps": round(layer_bytes / (layer_us * 1e-6) / 8e12, 4)}
@@ -352,16 +366,31 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
     from torch2iron_amd import ops
 
     def layer_ops(lay, kc, vc):
+        # each launch in the form the layer runs it (chained norm: see above)
         c, lw = cfg, lay.w
+        if lay.chain_in:
+            qkv = lambda: ops.prenormed_linear(buf.xg, buf.ssp, c.eps, lw.qkv, out=buf.qkv)
+        else:
+            qkv = lambda: ops.rmsnorm_linear(buf.x, lw.ln1, c.eps, lw.qkv, out=buf.qkv)
+        if lay.chain:
+            o = lambda: ops.linear_residual_next_norm(buf.ctx, lw.o, buf.x, buf.x, lw.ln2, buf.xg, buf.ssp)
+            gu = lambda: ops.prenormed_gate_up(buf.xg, buf.ssp, c.eps, lw.gate_up, swiglu=True, out=buf.hmlp)
+        else:
+            o = lambda: ops.linear(buf.ctx, lw.o, residual=buf.x, out=buf.x)
+            gu = lambda: ops.rmsnorm_gate_up(buf.x, lw.ln2, c.eps, lw.gate_up, swiglu=True, out=buf.hmlp)
+        if lay.next_ln1 is not None:
+            down = lambda: ops.linear_residual_next_norm(buf.hmlp, lw.down, buf.x, buf.x, lay.next_ln1, buf.xg,
+                                                         buf.ssp)
+        else:
+            down = lambda: ops.linear(buf.hmlp, lw.down, residual=buf.x, out=buf.x)
         return [
-            ("rmsnorm_qkv", lambda: ops.rmsnorm_linear(buf.x, lw.ln1, c.eps, lw.qkv, out=buf.qkv)),
+            ("rmsnorm_qkv", qkv),
             ("attention", lambda: ops.decode_attention(buf.qkv, pos, c.n_heads, c.n_kv_heads, lw.q_norm, lw.k_norm,
                                                        c.eps, lay.rope, kc, vc, rope_style=lay.rope_style,
                                                        out=buf.ctx, workspace=buf.workspace)),
-            ("o_proj_residual", lambda: ops.linear(buf.ctx, lw.o, residual=buf.x, out=buf.x)),
-            ("rmsnorm_gate_up_swiglu", lambda: ops.rmsnorm_gate_up(buf.x, lw.ln2, c.eps, lw.gate_up, swiglu=True,
-                                                                   out=buf.hmlp)),
-            ("down_residual", lambda: ops.linear(buf.hmlp, lw.down, residual=buf.x, out=buf.x)),
+            ("o_proj_residual", o),
+            ("rmsnorm_gate_up_swiglu", gu),
+            ("down_residual", down),
         ]
 
     calls = [layer_ops(lay, kc, vc) for lay, kc, vc in layers3]
@@ -498,7 +527,9 @@ def bench_decode(dev, steps: int, warmup: int, prompt_len: int, new_tokens: int,
                          "method": "each kernel's launches of 5 steps in a graph of their own (140 launches, "
                                    "each round on its own weight copies; a per-step kernel 140 times), HBM-cold "
                                    "(a 512 MB read between replays), HIP events per replay on the launch stream, "
-                                   "no host wait between replays; wall time per launch"},
+                                   "no host wait between replays; wall time per launch; with the chained norm "
+                                   "(by_kernel.chained_norm) qkv and gate_up take the norm's input from o_proj and "
+                                   "down, which write it (keys as without)"},
         "teacher_forced_prompt": teacher_forced,
         "one_launch_step": one_launch,
         "greedy_parity": oracle,
@@ -548,21 +579,46 @@ def time_step_kernels(model, dev, reps: int, pos: int, passes: int = 5) -> dict:
 
     wq, wo = copies(lambda w: w.qkv), copies(lambda w: w.o)
     wgu, wd = copies(lambda w: w.gate_up), copies(lambda w: w.down)
+    # the layers' own forms: with the chained norm, o_proj and down also write the next
+    # norm's input and sums of squares, which qkv and gate_up take (layer 0's qkv and the
+    # last layer's down run unchained in the step, counted here in the chained form)
+    chain = model.layers[0].chain
+    ss_bytes = b * (c.hidden // 16) * 4
+
+    def qkv_op(r, i, L):
+        if chain:
+            return ops.prenormed_linear(buf.xg, buf.ssp, c.eps, wq[r][i], out=buf.qkv)
+        return ops.rmsnorm_linear(buf.x, L.w.ln1, c.eps, wq[r][i], out=buf.qkv)
+
+    def o_op(r, i, L):
+        if chain:
+            return ops.linear_residual_next_norm(buf.ctx, wo[r][i], buf.x, buf.x, L.w.ln2, buf.xg, buf.ssp)
+        return ops.linear(buf.ctx, wo[r][i], residual=buf.x, out=buf.x)
+
+    def gu_op(r, i, L):
+        if chain:
+            return ops.prenormed_gate_up(buf.xg, buf.ssp, c.eps, wgu[r][i], swiglu=True, out=buf.hmlp)
+        return ops.rmsnorm_gate_up(buf.x, L.w.ln2, c.eps, wgu[r][i], swiglu=True, out=buf.hmlp)
+
+    def down_op(r, i, L):
+        if chain:
+            return ops.linear_residual_next_norm(buf.hmlp, wd[r][i], buf.x, buf.x, L.w.ln1, buf.xg, buf.ssp)
+        return ops.linear(buf.hmlp, wd[r][i], residual=buf.x, out=buf.x)
+
+    # a producer's extra bytes: the next norm's weight read, its input and the sums written
+    nxt_bytes = (c.hidden * 2 + b * c.hidden * 2 + ss_bytes) if chain else 0
+    norm_in_bytes = ss_bytes if chain else c.hidden * 2   # the sums read, or the norm weight
     per_layer = [
-        ("rmsnorm_qkv", lambda r, i, L: ops.rmsnorm_linear(buf.x, L.w.ln1, c.eps, wq[r][i], out=buf.qkv),
-         algorithmic_bytes(b, c.hidden, qkv_n) + c.hidden * 2),
+        ("rmsnorm_qkv", qkv_op, algorithmic_bytes(b, c.hidden, qkv_n) + norm_in_bytes),
         ("attention", lambda r, i, L: ops.decode_attention(buf.qkv, positions, c.n_heads, c.n_kv_heads, L.w.q_norm,
                                                            L.w.k_norm, c.eps, model.rope, model.k_cache[i],
                                                            model.v_cache[i], rope_style=L.rope_style, out=buf.ctx,
                                                            workspace=buf.workspace),
          kv_bytes + b * qkv_n * 2 + b * c.n_kv_heads * c.head_dim * 2 * 2 + b * hq * 2),
-        ("o_proj_residual", lambda r, i, L: ops.linear(buf.ctx, wo[r][i], residual=buf.x, out=buf.x),
-         algorithmic_bytes(b, hq, c.hidden) + b * c.hidden * 2),
-        ("rmsnorm_gate_up_swiglu", lambda r, i, L: ops.rmsnorm_gate_up(buf.x, L.w.ln2, c.eps, wgu[r][i],
-                                                                       swiglu=True, out=buf.hmlp),
-         algorithmic_bytes(b, c.hidden, 2 * c.intermediate) - b * c.intermediate * 2 + c.hidden * 2),
-        ("down_residual", lambda r, i, L: ops.linear(buf.hmlp, wd[r][i], residual=buf.x, out=buf.x),
-         algorithmic_bytes(b, c.intermediate, c.hidden) + b * c.hidden * 2),
+        ("o_proj_residual", o_op, algorithmic_bytes(b, hq, c.hidden) + b * c.hidden * 2 + nxt_bytes),
+        ("rmsnorm_gate_up_swiglu", gu_op,
+         algorithmic_bytes(b, c.hidden, 2 * c.intermediate) - b * c.intermediate * 2 + norm_in_bytes),
+        ("down_residual", down_op, algorithmic_bytes(b, c.intermediate, c.hidden) + b * c.hidden * 2 + nxt_bytes),
     ]
     per_step = [
         ("embedding_gather_rmsnorm", lambda: ops.rmsnorm(model.embed, model.layers[0].w.ln1, c.eps, out=buf.xn,
@@ -611,6 +667,7 @@ def time_step_kernels(model, dev, reps: int, pos: int, passes: int = 5) -> dict:
         del g
     floor = out.pop("graph_floor_one_element_fill")
     out["graph_floor_us_per_launch"] = floor["us_per_launch"]
+    out["chained_norm"] = bool(chain)
     model.x.copy_(x0)
     model.tokens.copy_(tokens)
     del pool, sink
