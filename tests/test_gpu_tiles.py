@@ -199,7 +199,8 @@ def test_random_shapes_over_tiles_are_bit_identical(gpu, form, m, k, n):
 
 # ---- chained RMSNorm between decode linears ----
 CHAIN_SHAPES = [(1, 2048, 1024, 1024), (16, 2048, 1024, 4096), (16, 3072, 1024, 1024), (5, 2048, 2048, 4096),
-                (13, 3072, 1024, 3072)]
+                (13, 3072, 1024, 3072), (8, 3072, 1024, 6144), (32, 2048, 1024, 4096), (32, 2048, 2048, 4096),
+                (64, 3072, 1024, 1024)]
 
 
 @pytest.mark.parametrize("m,kp,h,nc", CHAIN_SHAPES, ids=[f"M{m}-K{kp}-H{h}-N{nc}" for m, kp, h, nc in CHAIN_SHAPES])
@@ -234,11 +235,12 @@ def test_chained_norm_matches_the_fused_norm(gpu, m, kp, h, nc):
     assert rel <= 2.0 ** -7, f"max relative difference {rel:.3e}"
 
 
-def test_chained_norm_paired_consumer(gpu):
-    m, h, inter = 16, 1024, 3072
+@pytest.mark.parametrize("m", [8, 16])
+def test_chained_norm_paired_consumer(gpu, m):
+    h, inter = 1024, 3072
     if not ops.chain_supported(m, h, 2 * inter, ops.CHAIN_PAIRED_CONSUMER):
         pytest.skip("no chained form of this plan")
-    seed = 4242
+    seed = 4242 + m
     gate, up = ow.synthetic_tensors(h, inter, seed=seed), ow.synthetic_tensors(h, inter, seed=seed + 1)
     w = ops.tile_weight(W4A16Weight.from_numpy(*interleave_gate_up(gate, up), device=gpu))
     y = _x(m, h, seed + 2, gpu, scale=3.0)
