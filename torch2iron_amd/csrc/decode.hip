@@ -905,6 +905,9 @@ AttnPlan plan_attention(int B, int Hq, int Hkv, int ctx_cap) {
       pl.chunk = (ctx_cap + s9 - 1) / s9;
     }
   }
+  // A balanced chunk that fits in seven passes runs seven (batch 16, 640 slots: 6 chunks
+  // of 107): the eighth pass would only reload masked slots.
+  if (!tuned && Q <= 2 && pl.rows == 8 && pl.splits > 1 && pl.chunk <= 16 * 7) pl.rows = 7;
   if (pl.splits > 1) {
     pl.off_ml = align256(units * sizeof(unsigned));
     pl.off_o = pl.off_ml + align256(units * pl.splits * Q * 2 * sizeof(float));
@@ -926,10 +929,12 @@ template <bool PREP>
 hipError_t launch_attention_plan(const AttnParams& p, int Q, int rows, dim3 grid, hipStream_t s) {
   switch (Q * 100 + rows) {
     case 104: return launch_attention<1, 4, PREP>(p, grid, s);
+    case 107: return launch_attention<1, 7, PREP>(p, grid, s);
     case 108: return launch_attention<1, 8, PREP>(p, grid, s);
     case 109: return launch_attention<1, 9, PREP>(p, grid, s);
     case 116: return launch_attention<1, 16, PREP>(p, grid, s);
     case 204: return launch_attention<2, 4, PREP>(p, grid, s);
+    case 207: return launch_attention<2, 7, PREP>(p, grid, s);
     case 208: return launch_attention<2, 8, PREP>(p, grid, s);
     case 209: return launch_attention<2, 9, PREP>(p, grid, s);
     case 216: return launch_attention<2, 16, PREP>(p, grid, s);
