@@ -101,8 +101,10 @@ def _attention_case(gpu, b, hq, hkv, ctx_cap, positions, style, seed):
     (2, 16, 8, 1100, [1099, 300]),                                  # few sequences, long context: split chunks
     (1, 16, 8, 3000, [2500]),                                       # one sequence, 24 chunks (merge groups of 8)
     # batch 16: 5 chunks of 128 slots would give 640 workgroups, so 6 chunks of 107
-    # (768 = 3 x 256); positions at and around the chunk boundaries
+    # (768 = 3 x 256), seven passes each; positions at and around the chunk boundaries
     (16, 16, 8, 640, [0, 105, 106, 107, 108, 213, 214, 320, 321, 427, 428, 533, 534, 535, 600, 639]),
+    # one q head per kv head, the same 6 chunks of 107 slots in seven passes
+    (8, 16, 16, 640, [0, 106, 107, 213, 214, 500, 600, 639]),
     # many (sequence, kv head) pairs; positions at 128-slot boundaries
     (16, 16, 8, 1088, [1024] * 8 + [0, 127, 128, 255, 256, 383, 384, 1087]),
     (128, 8, 8, 300, [(37 * i) % 300 for i in range(128)]),
